@@ -1,0 +1,28 @@
+// Per-thread error reporting of the C ABI (ferrite_hip_last_error).
+#include <string>
+
+#include "common.h"
+
+namespace ferrite {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(FERRITE_ERR_LAUNCH, std::string(what) + ": " + hipGetErrorString(e));
+  g_last_error.clear();
+  return FERRITE_OK;
+}
+
+}  // namespace ferrite
+
+extern "C" const char* ferrite_hip_last_error(void) { return ferrite::g_last_error.c_str(); }
+
+extern "C" const char* ferrite_hip_version(void) { return "ferrite_hip 0.1.0 gfx950"; }

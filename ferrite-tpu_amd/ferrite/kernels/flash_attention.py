@@ -1,0 +1,196 @@
+"""Causal flash attention, forward and backward, on MI355X HIP kernels.
+
+Reference: src/ferrite/kernels/flash_attention.py. Same public names, arguments,
+defaults and ValueError conditions; the custom VJP wiring of the reference
+(`_flash` with non-differentiable (causal, scale, block_sizes), residuals
+(q, k, v, out, lse), backward = delta + dK/dV kernel + dQ kernel,
+flash_attention.py:315-333) is a torch.autograd.Function here.
+
+Kernels (csrc/attention.hip, through include/ferrite_hip.h):
+  forward   ferrite_hip_attn_fwd        -> O [B,H,S,D], lse f32 [B,H,S]
+  delta     ferrite_hip_attn_bwd_delta  -> rowsum(f32 dO * f32 O)
+  dK, dV    ferrite_hip_attn_bwd_dkv
+  dQ        ferrite_hip_attn_bwd_dq
+lse and delta are compact [B,H,S] f32 rather than the reference's
+lane-replicated [B,H,S,128] (flash_attention.py:156-160, :329).
+
+Block sizes are validated exactly as in the reference and otherwise treated as
+hints: the HIP kernels use their own tiles (128-row query tiles in 32-row MFMA
+wave tiles), which changes only the f32 summation order.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+
+import numpy as np
+import torch
+
+from ferrite import _hip, platform
+
+NUM_LANES = platform.LANES
+# Large negative finite value the reference uses for masked scores (flash_attention.py:43-44).
+MASK_VALUE = -0.7 * float(np.finfo(np.float32).max)
+
+
+@dataclasses.dataclass(frozen=True)
+class BlockSizes:
+    """Tile sizes. ``block_q`` is a multiple of 8, ``block_k`` a multiple of 128 (flash_attention.py:49-62)."""
+
+    block_q: int = 128
+    block_k: int = 128
+    block_q_bwd: int = 128
+    block_k_bwd: int = 128
+
+    @classmethod
+    def for_device(cls) -> "BlockSizes":
+        t = platform.default_tile()
+        return cls(t, t, t, t)
+
+
+def _on_or_below_diag(qi: int, bq: int, ki: int, bk: int) -> bool:
+    """True when block (qi, ki) has at least one unmasked (col <= row) entry (flash_attention.py:65-67)."""
+    return (qi + 1) * bq - 1 >= ki * bk
+
+
+# --------------------------------------------------------------------------
+# kernel launches
+# --------------------------------------------------------------------------
+
+
+def _flash_forward(q, k, v, *, causal: bool, scale: float, bs: BlockSizes | None = None):
+    """O and the compact logsumexp. Reference: _flash_forward, flash_attention.py:130-175."""
+    _hip.require_gpu(q, k, v)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    b, h, sq, d = q.shape
+    sk = k.shape[2]
+    out = torch.empty_like(q)
+    lse = torch.empty((b, h, sq), dtype=torch.float32, device=q.device)
+    rc = _hip.lib().ferrite_hip_attn_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+        b, h, sq, sk, d, _hip.dtype_code(q.dtype), int(causal), float(scale), _hip.stream_of(q),
+    )
+    _hip.check(rc, "ferrite_flash_attention_fwd")
+    return out, lse
+
+
+def _flash_delta(out, do):
+    """delta = rowsum(f32 dO * f32 O), flash_attention.py:328."""
+    out, do = out.contiguous(), do.contiguous()
+    b, h, s, d = out.shape
+    delta = torch.empty((b, h, s), dtype=torch.float32, device=out.device)
+    rc = _hip.lib().ferrite_hip_attn_bwd_delta(
+        out.data_ptr(), do.data_ptr(), delta.data_ptr(), b, h, s, d, _hip.dtype_code(out.dtype), _hip.stream_of(out)
+    )
+    _hip.check(rc, "ferrite_flash_attention_bwd_delta")
+    return delta
+
+
+def _flash_backward(q, k, v, do, lse, delta, *, causal: bool, scale: float, bs: BlockSizes | None = None):
+    """dQ, dK, dV. Reference: _flash_backward, flash_attention.py:246-307 (two kernels, no atomics)."""
+    _hip.require_gpu(q, k, v, do, lse, delta)
+    q, k, v, do = q.contiguous(), k.contiguous(), v.contiguous(), do.contiguous()
+    lse, delta = lse.contiguous(), delta.contiguous()
+    b, h, sq, d = q.shape
+    sk = k.shape[2]
+    dt = _hip.dtype_code(q.dtype)
+    stream = _hip.stream_of(q)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    lib = _hip.lib()
+    rc = lib.ferrite_hip_attn_bwd_dkv(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(), delta.data_ptr(),
+        dk.data_ptr(), dv.data_ptr(), b, h, sq, sk, d, dt, int(causal), float(scale), stream,
+    )
+    _hip.check(rc, "ferrite_flash_attention_bwd_dkv")
+    rc = lib.ferrite_hip_attn_bwd_dq(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(), delta.data_ptr(),
+        dq.data_ptr(), b, h, sq, sk, d, dt, int(causal), float(scale), stream,
+    )
+    _hip.check(rc, "ferrite_flash_attention_bwd_dq")
+    return dq, dk, dv
+
+
+# --------------------------------------------------------------------------
+# custom VJP and public API
+# --------------------------------------------------------------------------
+
+
+class _Flash(torch.autograd.Function):
+    """`_flash` of the reference (flash_attention.py:315-333): non-differentiable (causal, scale, bs)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, causal: bool, scale: float, bs: BlockSizes):
+        out, lse = _flash_forward(q, k, v, causal=causal, scale=scale, bs=bs)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.causal, ctx.scale, ctx.bs = causal, scale, bs
+        return out
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, out, lse = ctx.saved_tensors
+        do = do.to(out.dtype)
+        delta = _flash_delta(out, do)
+        dq, dk, dv = _flash_backward(q, k, v, do, lse, delta, causal=ctx.causal, scale=ctx.scale, bs=ctx.bs)
+        return dq, dk, dv, None, None, None
+
+
+def _validate(q, k, v, causal, bs):
+    """ValueErrors of the reference (flash_attention.py:336-353), same conditions and order."""
+    if not (q.ndim == 4 and k.shape == v.shape and q.shape[:2] == k.shape[:2] and q.shape[3] == k.shape[3]):
+        raise ValueError(f"expected q,k,v as [b,h,s,d] with matching b,h,d; got {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError("q, k, v must share a dtype")
+    d = q.shape[3]
+    if d % NUM_LANES and d > NUM_LANES:
+        raise ValueError(f"head_dim must be <= {NUM_LANES} or a multiple of it; got {d}")
+    if causal and q.shape[2] != k.shape[2]:
+        raise ValueError("causal attention needs equal q and k sequence lengths")
+    for name, blk, dim, mult in [
+        ("block_q", bs.block_q, q.shape[2], platform.SUBLANES),
+        ("block_k", bs.block_k, k.shape[2], NUM_LANES),
+        ("block_q_bwd", bs.block_q_bwd, q.shape[2], platform.SUBLANES),
+        ("block_k_bwd", bs.block_k_bwd, k.shape[2], NUM_LANES),
+    ]:
+        if blk % mult or dim % blk:
+            raise ValueError(f"{name}={blk} must be a multiple of {mult} and divide the sequence length {dim}")
+
+
+def flash_attention(q, k, v, *, causal: bool = True, scale: float | None = None, block_sizes: BlockSizes | None = None):
+    """Memory-efficient attention ``softmax(q k^T * scale) v`` with exact numerics.
+
+    Differentiable through autograd (custom backward with HIP dK/dV and dQ
+    kernels). Shapes ``[batch, heads, seq, head_dim]``; sequence lengths must be
+    multiples of the block sizes, as in the reference (flash_attention.py:356-367).
+    """
+    bs = block_sizes or BlockSizes()
+    _validate(q, k, v, causal, bs)
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    return _Flash.apply(q, k, v, bool(causal), float(scale), bs)
+
+
+def flash_attention_reference(q, k, v, *, causal: bool = True, scale: float | None = None):
+    """Materialised-scores attention in f32 with torch ops (the reference's XLA route,
+    flash_attention.py:370-380). Not used by the HIP path."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    qf, kf, vf = q.float(), k.float(), v.float()
+    s = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) * scale
+    if causal:
+        sq, sk = q.shape[2], k.shape[2]
+        mask = torch.ones((sq, sk), dtype=torch.bool, device=q.device).tril(diagonal=sk - sq)
+        s = torch.where(mask, s, torch.full_like(s, MASK_VALUE))
+    p = torch.softmax(s, dim=-1)
+    return torch.matmul(p, vf).to(q.dtype)
+
+
+def attention_flops(b: int, h: int, sq: int, sk: int, d: int, *, causal: bool, backward: bool = False) -> int:
+    """FLOPs for one forward (and optionally backward) pass, skipped blocks free (flash_attention.py:383-390)."""
+    frac = 0.5 if causal else 1.0
+    fwd = 4 * b * h * sq * sk * d * frac
+    if not backward:
+        return int(fwd)
+    return int(fwd * 2.5)

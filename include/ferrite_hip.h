@@ -1,0 +1,113 @@
+/*
+ * ferrite_hip.h — C ABI of the MI355X (gfx950) kernels behind ferrite.kernels.
+ *
+ * Every entry point takes device pointers, sizes and attributes as plain C types,
+ * enqueues its kernels on `stream` (a hipStream_t passed as void*, NULL = the
+ * default stream), never synchronises, never allocates, and returns 0 on
+ * success. A non-zero return is one of the FERRITE_ERR_* codes; the message
+ * for the calling thread's last failure is ferrite_hip_last_error().
+ *
+ * All tensors are dense and row-major (last dimension contiguous). Outputs are
+ * preallocated by the caller, exactly as XLA preallocates the out_shape buffers
+ * of the reference's pallas_call custom calls. Inputs are read-only.
+ *
+ * Each function replaces one Pallas kernel of the reference (paths relative to
+ * the reference repository, src/ferrite/kernels/):
+ *
+ *   ferrite_hip_attn_fwd      flash_attention.py:91-175  (_fwd_kernel + _flash_forward,
+ *                                                          custom call "ferrite_flash_attention_fwd")
+ *   ferrite_hip_attn_bwd_delta flash_attention.py:328-329 (delta = rowsum(f32 dO * f32 O),
+ *                                                          an XLA fusion in the reference)
+ *   ferrite_hip_attn_bwd_dkv  flash_attention.py:197-221, :253-279 ("ferrite_flash_attention_bwd_dkv")
+ *   ferrite_hip_attn_bwd_dq   flash_attention.py:224-243, :281-306 ("ferrite_flash_attention_bwd_dq")
+ *   ferrite_hip_add_rmsnorm   rmsnorm.py:52-56, :77-110  ("ferrite_add_rmsnorm")
+ *   ferrite_hip_rmsnorm       rmsnorm.py:46-49, :77-110  ("ferrite_rmsnorm")
+ *   ferrite_hip_matmul        matmul.py:27-38, :52-86    ("ferrite_matmul")
+ *
+ * The one layout change against the reference: the softmax statistics
+ * (logsumexp `lse` and `delta`) are compact f32 [B, H, S] arrays instead of the
+ * reference's lane-replicated [B, H, S, 128] (flash_attention.py:156-160, :329).
+ */
+#ifndef FERRITE_HIP_H
+#define FERRITE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types. */
+#define FERRITE_F32 0
+#define FERRITE_BF16 1
+
+/* Return codes. */
+#define FERRITE_OK 0
+#define FERRITE_ERR_INVALID_ARGUMENT 1 /* shape / dtype / attribute not supported */
+#define FERRITE_ERR_LAUNCH 2           /* hipLaunchKernel or hipGetLastError failed */
+
+/* Message describing the calling thread's most recent failure ("" if none). */
+const char* ferrite_hip_last_error(void);
+
+/* Library version string, e.g. "ferrite_hip 0.1.0 gfx950". */
+const char* ferrite_hip_version(void);
+
+/*
+ * Fused residual-add + RMSNorm (rmsnorm.py:52-56):
+ *   h = f32(x) + f32(residual);  store h rounded to x's dtype
+ *   y = h * rsqrt(sum(h*h)/dim + eps) * f32(weight); store y in x's dtype
+ * y uses the unrounded f32 h. x, residual, h, y: [rows, dim] of x_dtype;
+ * weight: [dim] of w_dtype. rows >= 0, dim >= 1.
+ */
+int ferrite_hip_add_rmsnorm(const void* x, const void* residual, const void* weight, void* h, void* y,
+                            int64_t rows, int64_t dim, int x_dtype, int w_dtype, float eps, void* stream);
+
+/* Plain RMSNorm (rmsnorm.py:46-49): y = x * rsqrt(mean(x^2) + eps) * weight. */
+int ferrite_hip_rmsnorm(const void* x, const void* weight, void* y, int64_t rows, int64_t dim, int x_dtype,
+                        int w_dtype, float eps, void* stream);
+
+/*
+ * out[M, N] = x[M, K] @ y[K, N] with f32 accumulation (matmul.py:27-38, :52-86).
+ * in_dtype FERRITE_BF16 uses bf16 MFMA; FERRITE_F32 uses fp32 MFMA (true fp32
+ * products, the reference's Precision.HIGHEST, _compat.py:17-25). Ragged shapes
+ * need no padding from the caller: out-of-range elements read as zero, which is
+ * what the reference's zero padding contributes. out_dtype may differ from
+ * in_dtype. M, N, K >= 1.
+ */
+int ferrite_hip_matmul(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k, int in_dtype,
+                       int out_dtype, void* stream);
+
+/*
+ * Flash attention forward (flash_attention.py:91-175).
+ * q: [B, H, Sq, D]; k, v: [B, H, Sk, D]; o: [B, H, Sq, D], all of `dtype`.
+ * lse: f32 [B, H, Sq] = logsumexp_j(scale * q_i . k_j) over the visible keys.
+ * causal != 0 masks key j > query i and requires Sq == Sk. Supported head dims:
+ * D <= 128 and D == 256 (inputs of other D <= 128 are zero-padded inside the
+ * kernel). Sq, Sk >= 1; Sq and Sk need not be multiples of any tile size.
+ */
+int ferrite_hip_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t b, int64_t h,
+                         int64_t sq, int64_t sk, int64_t d, int dtype, int causal, float scale, void* stream);
+
+/* delta[B, H, S] = sum_d f32(dO) * f32(O) (flash_attention.py:328). */
+int ferrite_hip_attn_bwd_delta(const void* o, const void* dout, float* delta, int64_t b, int64_t h, int64_t s,
+                               int64_t d, int dtype, void* stream);
+
+/*
+ * dK, dV of flash attention (flash_attention.py:197-221). Inputs q, k, v, dout of
+ * `dtype`, lse and delta f32 [B, H, Sq] from ferrite_hip_attn_fwd and
+ * ferrite_hip_attn_bwd_delta. dk, dv: [B, H, Sk, D] of `dtype`.
+ */
+int ferrite_hip_attn_bwd_dkv(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                             const float* delta, void* dk, void* dv, int64_t b, int64_t h, int64_t sq, int64_t sk,
+                             int64_t d, int dtype, int causal, float scale, void* stream);
+
+/* dQ of flash attention (flash_attention.py:224-243). dq: [B, H, Sq, D] of `dtype`. */
+int ferrite_hip_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                            const float* delta, void* dq, int64_t b, int64_t h, int64_t sq, int64_t sk, int64_t d,
+                            int dtype, int causal, float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FERRITE_HIP_H */

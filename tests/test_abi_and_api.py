@@ -1,0 +1,124 @@
+"""CPU tests of the boundary: the C ABI library loads and exports every symbol
+of include/ferrite_hip.h, its argument checks return error codes without
+touching a GPU, and the Python API raises the reference's ValueErrors before
+dispatch and refuses (loudly) to run on CPU tensors."""
+
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from ferrite import _hip, platform
+from ferrite.kernels import (BlockSizes, attention_flops, flash_attention, flash_attention_reference, matmul,
+                             matmul_flops, matmul_reference, rmsnorm, rmsnorm_reference)
+from tests.conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "ferrite_hip.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(ferrite_hip_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    declared = _declared_symbols()
+    assert len(declared) == 9
+    out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\sT\s(\w+)", out))
+    missing = [s for s in declared if s not in exported]
+    assert not missing, missing
+    assert set(declared) == set(_hip.SIGNATURES)
+    for s in declared:
+        getattr(_hip.lib(), s)
+
+
+def test_abi_argument_checks_return_codes():
+    lib = _hip.lib()
+    assert lib.ferrite_hip_version().startswith(b"ferrite_hip")
+    assert lib.ferrite_hip_matmul(None, None, None, 0, 4, 4, _hip.BF16, _hip.BF16, None) == 1
+    assert "M, N, K" in _hip.last_error()
+    assert lib.ferrite_hip_matmul(None, None, None, 4, 4, 4, 7, _hip.BF16, None) == 1
+    assert "dtype" in _hip.last_error()
+    # causal needs sq == sk
+    assert lib.ferrite_hip_attn_fwd(1, 1, 1, 1, 1, 1, 1, 128, 256, 64, _hip.BF16, 1, 0.125, None) == 1
+    assert "sq == sk" in _hip.last_error()
+    # unsupported head dims
+    assert lib.ferrite_hip_attn_fwd(1, 1, 1, 1, 1, 1, 1, 128, 128, 384, _hip.BF16, 1, 0.1, None) == 1
+    assert lib.ferrite_hip_attn_bwd_dq(1, 1, 1, 1, 1, 1, 1, 1, 1, 128, 128, 256, _hip.BF16, 1, 0.1, None) == 1
+    assert "backward" in _hip.last_error()
+    assert lib.ferrite_hip_add_rmsnorm(None, None, None, None, None, 4, 0, 1, 1, 1e-6, None) == 1
+    # rows == 0 is a valid no-op and launches nothing
+    assert lib.ferrite_hip_rmsnorm(None, None, None, 0, 16, 1, 1, 1e-6, None) == 0
+
+
+def _qkv(s=256, d=128, dtype=torch.float32):
+    g = torch.Generator().manual_seed(0)
+    return tuple(torch.randn(1, 1, s, d, generator=g).to(dtype) for _ in range(3))
+
+
+def test_flash_attention_validation_errors():
+    """Mirrors the reference's test_validation_errors (tests/test_flash_attention.py:69-76)."""
+    q, k, v = _qkv()
+    with pytest.raises(ValueError):
+        flash_attention(q, k, v, block_sizes=BlockSizes(block_k=100))
+    with pytest.raises(ValueError):
+        flash_attention(q, k[:, :, :128], v[:, :, :128], causal=True)
+    with pytest.raises(ValueError):
+        flash_attention(q, k, v.to(torch.bfloat16))
+    with pytest.raises(ValueError):
+        flash_attention(q[..., :1], k, v)  # mismatched head dims
+    qq = torch.zeros(1, 1, 256, 200)
+    with pytest.raises(ValueError):  # d > 128 and not a multiple of 128
+        flash_attention(qq, qq, qq)
+    with pytest.raises(ValueError):
+        flash_attention(q, k, v, block_sizes=BlockSizes(block_q=12))
+
+
+def test_matmul_and_rmsnorm_validation_errors():
+    x = torch.zeros(128, 128)
+    with pytest.raises(ValueError):
+        matmul(x, x, block_n=100)
+    with pytest.raises(ValueError):
+        matmul(x, torch.zeros(64, 128))
+    with pytest.raises(ValueError):
+        rmsnorm(x, torch.ones(64))
+    with pytest.raises(ValueError):
+        rmsnorm(x, torch.ones(128), residual=torch.zeros(64, 128))
+    with pytest.raises(ValueError):
+        rmsnorm(x, torch.ones(128), block_rows=12)
+
+
+def test_product_path_refuses_cpu_tensors():
+    q, k, v = _qkv()
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        flash_attention(q, k, v)
+    x = torch.zeros(128, 128)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        matmul(x, x)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        rmsnorm(x, torch.ones(128))
+
+
+def test_reference_functions_and_flop_formulas():
+    q, k, v = _qkv(s=16, d=8)
+    out = flash_attention_reference(q, k, v, causal=True)
+    torch.testing.assert_close(out[:, :, 0], v[:, :, 0])
+    assert attention_flops(4, 16, 2048, 2048, 128, causal=True) == 68_719_476_736
+    assert attention_flops(4, 16, 2048, 2048, 128, causal=True, backward=True) == int(68_719_476_736 * 2.5)
+    assert matmul_flops(4096, 4096, 4096) == 2 * 4096**3
+    x = torch.randn(4, 8)
+    torch.testing.assert_close(matmul_reference(x, torch.eye(8)), x)
+    h, y = rmsnorm_reference(x, torch.ones(8), residual=x)
+    torch.testing.assert_close(h, 2 * x)
+
+
+def test_platform_peaks():
+    p = platform.peaks("MI355X")
+    assert p.bf16_flops == pytest.approx(2.5166e15) and p.hbm_bytes_per_s == 8e12
+    assert p.ridge_point > 300
+    assert BlockSizes.for_device() == BlockSizes(128, 128, 128, 128)
+    with platform.interpret_mode() as on:
+        assert on is False

@@ -1,0 +1,176 @@
+"""GPU parity of the flash attention kernels (forward, delta, dK/dV, dQ) against the oracle.
+
+Reference tests mirrored: tests/test_flash_attention.py:18-66 (f32 forward at
+2e-5, bf16 forward at 2e-2, f32 backward at 5e-4, bf16 backward relative
+Frobenius < 5e-2, prefix invariance). fwd/bwd at
+4x16x2048x128 bf16 and the long-context 1x8x8192x64, bars max-abs <= 2e-2 for
+bf16 outputs and <= 1e-3 for the logsumexp.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from ferrite import _hip
+from ferrite.kernels import BlockSizes, flash_attention
+from ferrite.kernels.flash_attention import _flash_backward, _flash_delta, _flash_forward
+from oracle import attention as oatt
+from tests._util import max_abs, normal, rel_fro, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _qkv(seed, shape, dtype, kv_len=None):
+    kshape = shape if kv_len is None else (*shape[:2], kv_len, shape[3])
+    return normal(seed, shape, dtype), normal(seed + 1, kshape, dtype), normal(seed + 2, kshape, dtype)
+
+
+def _grads(q, k, v, do, dev, dtype, causal, bs=None):
+    qt, kt, vt = (to_dev(a, dtype, dev).requires_grad_() for a in (q, k, v))
+    out = flash_attention(qt, kt, vt, causal=causal, block_sizes=bs)
+    out.backward(to_dev(do, dtype, dev))
+    return to_np(out), to_np(qt.grad), to_np(kt.grad), to_np(vt.grad)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("s,d,bs", [(256, 128, BlockSizes(128, 128)), (512, 64, BlockSizes(128, 256)), (256, 256, BlockSizes(64, 128))])
+def test_forward_f32(dev, causal, s, d, bs):
+    """tests/test_flash_attention.py:18-24."""
+    q, k, v = _qkv(0, (1, 2, s, d), "f32")
+    out = flash_attention(to_dev(q, "f32", dev), to_dev(k, "f32", dev), to_dev(v, "f32", dev), causal=causal, block_sizes=bs)
+    ref, _ = oatt.forward(q, k, v, causal=causal)
+    np.testing.assert_allclose(to_np(out), ref, atol=2e-5, rtol=2e-5)
+
+
+def test_forward_bf16(dev):
+    """tests/test_flash_attention.py:27-32."""
+    q, k, v = _qkv(3, (2, 2, 256, 128), "bf16")
+    out = flash_attention(to_dev(q, "bf16", dev), to_dev(k, "bf16", dev), to_dev(v, "bf16", dev), causal=True)
+    assert out.dtype == torch.bfloat16
+    ref, _ = oatt.forward(q, k, v, causal=True)
+    np.testing.assert_allclose(to_np(out), ref, atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("s,d,bs", [(256, 128, BlockSizes()), (384, 64, BlockSizes(128, 128, 64, 128))])
+def test_backward_matches_reference(dev, causal, s, d, bs):
+    """tests/test_flash_attention.py:35-47 (f32, 5e-4)."""
+    q, k, v = _qkv(6, (1, 2, s, d), "f32")
+    do = normal(9, q.shape)
+    _, dq, dk, dv = _grads(q, k, v, do, dev, "f32", causal, bs)
+    for name, a, b in zip("qkv", (dq, dk, dv), oatt.backward(q, k, v, do, causal=causal)):
+        np.testing.assert_allclose(a, b, atol=5e-4, rtol=5e-4, err_msg=f"d{name}")
+
+
+def test_backward_bf16_is_close(dev):
+    """tests/test_flash_attention.py:50-58: loss = sum(f32(out)^2), relative Frobenius < 5e-2."""
+    q, k, v = _qkv(10, (1, 2, 256, 128), "bf16")
+    qt, kt, vt = (to_dev(a, "bf16", dev).requires_grad_() for a in (q, k, v))
+    (flash_attention(qt, kt, vt, causal=True).float() ** 2).sum().backward()
+    o, _ = oatt.forward(q, k, v, causal=True)
+    for a, b in zip((qt.grad, kt.grad, vt.grad), oatt.backward(q, k, v, 2 * o, causal=True)):
+        assert rel_fro(to_np(a), b) < 5e-2
+
+
+def test_causal_output_is_prefix_invariant(dev):
+    """tests/test_flash_attention.py:61-66."""
+    q, k, v = (to_dev(a, "f32", dev) for a in _qkv(13, (1, 1, 512, 128), "f32"))
+    full = flash_attention(q, k, v, causal=True)
+    short = flash_attention(q[:, :, :256].contiguous(), k[:, :, :256].contiguous(), v[:, :, :256].contiguous(), causal=True)
+    np.testing.assert_allclose(to_np(full)[:, :, :256], to_np(short), atol=2e-5, rtol=2e-5)
+
+
+def test_causal_row0_is_exact(dev):
+    q, k, v = _qkv(16, (2, 3, 256, 128), "bf16")
+    out = flash_attention(to_dev(q, "bf16", dev), to_dev(k, "bf16", dev), to_dev(v, "bf16", dev), causal=True)
+    np.testing.assert_array_equal(to_np(out)[:, :, 0], v[:, :, 0])
+
+
+def test_noncausal_different_lengths(dev):
+    q, k, v = _qkv(19, (1, 2, 256, 64), "f32", kv_len=384)
+    do = normal(22, q.shape)
+    out, dq, dk, dv = _grads(q, k, v, do, dev, "f32", False)
+    ref, _ = oatt.forward(q, k, v, causal=False)
+    np.testing.assert_allclose(out, ref, atol=2e-5, rtol=2e-5)
+    for a, b in zip((dq, dk, dv), oatt.backward(q, k, v, do, causal=False)):
+        np.testing.assert_allclose(a, b, atol=5e-4, rtol=5e-4)
+
+
+def _check_config(dev, b, h, s, d, seed):
+    """BASELINE bars at a full config: O, dQ, dK, dV max-abs <= 2e-2, lse <= 1e-3."""
+    q, k, v = _qkv(seed, (b, h, s, d), "bf16")
+    do = normal(seed + 3, q.shape, "bf16")
+    qt, kt, vt, dot = (to_dev(a, "bf16", dev) for a in (q, k, v, do))
+    scale = 1.0 / np.sqrt(d)
+    out, lse = _flash_forward(qt, kt, vt, causal=True, scale=scale)
+    delta = _flash_delta(out, dot)
+    dq, dk, dv = _flash_backward(qt, kt, vt, dot, lse, delta, causal=True, scale=scale)
+    o_ref, lse_ref = oatt.forward(q, k, v, causal=True, dtype=np.float32)
+    assert max_abs(to_np(out), o_ref) <= 2e-2
+    assert max_abs(to_np(lse), lse_ref) <= 1e-3
+    for name, a, r in zip(("dq", "dk", "dv"), (dq, dk, dv), oatt.backward(q, k, v, do, causal=True, dtype=np.float32)):
+        err = max_abs(to_np(a), r)
+        assert err <= 2e-2, (name, err)
+
+
+def test_baseline_config_fwd_bwd(dev):
+    """BASELINE configs 3 and 4: q, k, v, dO bf16 [4,16,2048,128] ~ N(0,1), scale 1/sqrt(128), causal."""
+    _check_config(dev, 4, 16, 2048, 128, seed=7)
+
+
+def test_long_context_config(dev):
+    """BASELINE config 4, long-context variant: B=1, H=8, T=8192, d=64."""
+    _check_config(dev, 1, 8, 8192, 64, seed=27)
+
+
+def _abi_case(dev, b, h, sq, sk, d, dtype, causal, seed):
+    """Ragged lengths and odd head dims through the C ABI (the Python API requires
+    block-multiple lengths, like the reference)."""
+    q, k, v = _qkv(seed, (b, h, sq, d), dtype, kv_len=sk)
+    do = normal(seed + 3, q.shape, dtype)
+    qt, kt, vt, dot = (to_dev(a, dtype, dev) for a in (q, k, v, do))
+    scale = 0.37
+    o = torch.full_like(qt, float("nan"))
+    lse = torch.full((b, h, sq), float("nan"), device=dev)
+    lib, st, dt = _hip.lib(), _hip.stream_of(qt), _hip.dtype_code(qt.dtype)
+    _hip.check(lib.ferrite_hip_attn_fwd(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                        b, h, sq, sk, d, dt, int(causal), scale, st), "fwd")
+    delta = _flash_delta(o, dot)
+    dq = torch.full_like(qt, float("nan"))
+    dk = torch.full_like(kt, float("nan"))
+    dv = torch.full_like(vt, float("nan"))
+    _hip.check(lib.ferrite_hip_attn_bwd_dkv(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), dot.data_ptr(), lse.data_ptr(),
+                                            delta.data_ptr(), dk.data_ptr(), dv.data_ptr(), b, h, sq, sk, d, dt,
+                                            int(causal), scale, st), "dkv")
+    _hip.check(lib.ferrite_hip_attn_bwd_dq(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), dot.data_ptr(), lse.data_ptr(),
+                                           delta.data_ptr(), dq.data_ptr(), b, h, sq, sk, d, dt, int(causal), scale,
+                                           st), "dq")
+    torch.cuda.synchronize()
+    o_ref, lse_ref = oatt.forward(q, k, v, causal=causal, scale=scale)
+    grads_ref = oatt.backward(q, k, v, do, causal=causal, scale=scale)
+    tol = 2e-2 if dtype == "bf16" else 5e-4
+    assert max_abs(to_np(o), o_ref) <= (2e-2 if dtype == "bf16" else 2e-5)
+    assert max_abs(to_np(lse), lse_ref) <= 1e-3
+    for name, a, r in zip(("dq", "dk", "dv"), (dq, dk, dv), grads_ref):
+        assert max_abs(to_np(a), r) <= tol, name
+
+
+@pytest.mark.parametrize("b,h,sq,sk,d,dtype,causal", [
+    (1, 2, 200, 200, 64, "bf16", True),     # ragged length, aligned head dim
+    (2, 1, 77, 77, 80, "bf16", True),       # d padded 80 -> 128
+    (1, 2, 130, 130, 36, "bf16", True),     # d % 8 != 0: element-wise (unaligned) path
+    (1, 1, 100, 260, 128, "bf16", False),   # non-causal, sk != sq, both ragged
+    (1, 2, 150, 150, 30, "f32", True),      # f32 unaligned path
+    (1, 1, 33, 33, 128, "f32", True),
+    (1, 1, 1, 1, 64, "bf16", True),         # single token
+])
+def test_ragged_and_unaligned_via_abi(dev, b, h, sq, sk, d, dtype, causal):
+    _abi_case(dev, b, h, sq, sk, d, dtype, causal, seed=31)
+
+
+def test_deterministic(dev):
+    q, k, v = _qkv(40, (2, 4, 512, 128), "bf16")
+    do = normal(43, q.shape, "bf16")
+    runs = [_grads(q, k, v, do, dev, "bf16", True) for _ in range(2)]
+    for a, b in zip(*runs):
+        np.testing.assert_array_equal(a, b)

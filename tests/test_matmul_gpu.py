@@ -1,0 +1,111 @@
+"""GPU parity of the blocked MFMA matmul against the oracle.
+
+Reference tests mirrored: tests/test_matmul.py:13-41. bf16
+4096^3 (U(-1,1)) and ragged f32 1000^3 (relative error <= 1e-5). The bf16
+output bar of BASELINE (2e-2 max-abs against the f32 product) is below the
+bf16 rounding of outputs of magnitude ~100, so the bf16 product is held to one
+bf16 ulp of the rounded exact product and a relative error bar instead.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from ferrite import _hip
+from ferrite.kernels import matmul
+from oracle import matmul as omm
+from tests._util import bf16_ulp, normal, rel_fro, to_dev, to_np, uniform
+
+pytestmark = pytest.mark.gpu
+
+
+def test_baseline_bf16_4096(dev):
+    a, b = uniform(3, (4096, 4096), "bf16"), uniform(4, (4096, 4096), "bf16")
+    out = matmul(to_dev(a, "bf16", dev), to_dev(b, "bf16", dev))
+    assert out.dtype == torch.bfloat16 and out.shape == (4096, 4096)
+    exact = omm.reference(a, b)  # f64 accumulation, f32 result
+    g = to_np(out).astype(np.float64)
+    assert np.all(np.abs(g - exact) <= bf16_ulp(exact))  # within one bf16 ulp of the exact product
+    assert rel_fro(g, exact) < 4e-3
+
+
+def test_ragged_f32_1000(dev):
+    a, b = uniform(5, (1000, 1000)), uniform(6, (1000, 1000))
+    out = to_np(matmul(to_dev(a, "f32", dev), to_dev(b, "f32", dev)))
+    exact = omm.reference(a, b)
+    rel = np.max(np.abs(out.astype(np.float64) - exact)) / np.max(np.abs(exact))
+    assert rel <= 1e-5, rel
+
+
+@pytest.mark.parametrize("dtype,atol", [("f32", 1e-3), ("bf16", 0.5)])
+def test_matches_reference_aligned(dev, dtype, atol):
+    """tests/test_matmul.py:13-20."""
+    x, y = normal(7, (256, 384), dtype), normal(8, (384, 512), dtype)
+    out = matmul(to_dev(x, dtype, dev), to_dev(y, dtype, dev), block_m=128, block_n=256, block_k=128)
+    assert out.shape == (256, 512)
+    np.testing.assert_allclose(to_np(out), omm.reference(x, y, out_bf16=dtype == "bf16"), atol=atol, rtol=1e-2)
+
+
+def test_ragged_shapes_are_padded_exactly(dev):
+    """tests/test_matmul.py:23-27, plus exactness on integer-valued inputs (every f32 sum is exact,
+    so any accumulation order must reproduce the zero-padded product bit for bit)."""
+    x, y = normal(9, (77, 130)), normal(10, (130, 203))
+    out = matmul(to_dev(x, "f32", dev), to_dev(y, "f32", dev), block_m=64, block_n=128, block_k=128)
+    np.testing.assert_allclose(to_np(out), omm.reference(x, y), atol=1e-3, rtol=1e-3)
+    rng = np.random.default_rng(11)
+    xi = rng.integers(-8, 9, (77, 130)).astype(np.float32)
+    yi = rng.integers(-8, 9, (130, 203)).astype(np.float32)
+    exact = omm.blocked_padded(xi, yi, bm=64, bn=128, bk=128)
+    for dt in ("f32", "bf16"):
+        got = to_np(matmul(to_dev(xi, dt, dev), to_dev(yi, dt, dev), out_dtype=torch.float32))
+        np.testing.assert_array_equal(got, exact)
+
+
+def test_f32_output_from_bf16_inputs(dev):
+    """tests/test_matmul.py:30-35."""
+    x, y = normal(12, (128, 256), "bf16"), normal(13, (256, 128), "bf16")
+    out = matmul(to_dev(x, "bf16", dev), to_dev(y, "bf16", dev), out_dtype=torch.float32)
+    assert out.dtype == torch.float32
+    np.testing.assert_allclose(to_np(out), omm.reference(x, y), atol=1e-2, rtol=1e-2)
+    out2 = matmul(to_dev(x, "bf16", dev), to_dev(y, "bf16", dev), out_dtype="float32")
+    assert out2.dtype == torch.float32
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (5, 7, 3), (33, 17, 65), (300, 1000, 4100), (513, 64, 257), (64, 4096, 8)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_edge_shapes(dev, m, k, n, dtype):
+    x, y = uniform(14, (m, k), dtype), uniform(15, (k, n), dtype)
+    out = to_np(matmul(to_dev(x, dtype, dev), to_dev(y, dtype, dev), out_dtype=torch.float32))
+    exact = omm.reference(x, y)
+    assert np.max(np.abs(out - exact)) <= 1e-5 * max(1.0, np.max(np.abs(exact))) * (1 + k / 64)
+
+
+def test_bf16_output_from_f32_inputs(dev):
+    x, y = uniform(16, (200, 300)), uniform(17, (300, 100))
+    out = matmul(to_dev(x, "f32", dev), to_dev(y, "f32", dev), out_dtype=torch.bfloat16)
+    exact = omm.reference(x, y)
+    assert np.all(np.abs(to_np(out) - exact) <= bf16_ulp(exact))
+
+
+def test_gradients(dev):
+    """The VJP (matmul.py:99-104): dX = G Y^T, dY = X^T G through the same kernel."""
+    x, y, g = normal(18, (64, 96)), normal(19, (96, 80)), normal(20, (64, 80))
+    xt, yt = to_dev(x, "f32", dev).requires_grad_(), to_dev(y, "f32", dev).requires_grad_()
+    (matmul(xt, yt) * to_dev(g, "f32", dev)).sum().backward()
+    np.testing.assert_allclose(to_np(xt.grad), g.astype(np.float64) @ y.T, atol=1e-4, rtol=1e-4)
+    np.testing.assert_allclose(to_np(yt.grad), x.T.astype(np.float64) @ g, atol=1e-4, rtol=1e-4)
+
+
+def test_every_element_written_and_deterministic(dev):
+    m, k, n = 1000, 520, 777
+    x, y = uniform(21, (m, k), "bf16"), uniform(22, (k, n), "bf16")
+    xt, yt = to_dev(x, "bf16", dev), to_dev(y, "bf16", dev)
+    outs = []
+    for _ in range(2):
+        o = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+        _hip.check(_hip.lib().ferrite_hip_matmul(xt.data_ptr(), yt.data_ptr(), o.data_ptr(), m, n, k, _hip.BF16,
+                                                 _hip.F32, _hip.stream_of(xt)), "matmul")
+        torch.cuda.synchronize()
+        assert not torch.isnan(o).any()
+        outs.append(o.clone())
+    assert torch.equal(outs[0], outs[1])

@@ -1,0 +1,132 @@
+"""GPU parity of the fused add+RMSNorm kernel against the oracle.
+
+Reference tests mirrored: tests/test_rmsnorm.py:9-54 (forward shapes, fused
+residual, gradients). Bars: h bit-exact in bf16; y within 2e-2 max-abs of the
+exact (f64-statistics) result and within one bf16 ulp of the reference's own
+f32-statistics rounding; f32 outputs within 1e-5.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from ferrite import _hip
+from ferrite.kernels import rmsnorm
+from oracle import rmsnorm as orms
+from oracle.bf16 import round_bf16
+from tests._util import bf16_ulp, max_abs, normal, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_bf16(h, y, x, w, r, eps=1e-6):
+    h_ref, y32 = orms.add_rmsnorm(x, w, r, eps=eps, out_bf16=True)
+    _, y64 = orms.add_rmsnorm(x, w, r, eps=eps, acc=np.float64)
+    np.testing.assert_array_equal(to_np(h).view(np.uint32), h_ref.view(np.uint32))
+    yg = to_np(y)
+    assert max_abs(yg, y64) <= 2e-2
+    assert np.all(np.abs(yg.astype(np.float64) - y32) <= bf16_ulp(y32))
+    return yg
+
+
+def test_baseline_config_add_rmsnorm(dev):
+    """BASELINE config: x, r bf16 [4096,1024] ~ N(0,1), w bf16 = 1 + 0.1 N(0,1), eps 1e-6."""
+    x = normal(0, (4096, 1024), "bf16")
+    r = normal(1, (4096, 1024), "bf16")
+    w = normal(2, (1024,), "bf16", loc=1.0, scale=0.1)
+    h, y = rmsnorm(to_dev(x, "bf16", dev), to_dev(w, "bf16", dev), residual=to_dev(r, "bf16", dev), eps=1e-6)
+    assert h.dtype == y.dtype == torch.bfloat16
+    _check_bf16(h, y, x, w, r)
+
+
+@pytest.mark.parametrize("shape", [(4, 64, 256), (300, 384), (2, 8, 128)])
+def test_forward_matches_reference(dev, shape):
+    """tests/test_rmsnorm.py:9-14 (f32, atol = rtol = 1e-5)."""
+    x = normal(3, shape)
+    w = normal(4, shape[-1:], loc=1.0, scale=0.1)
+    y = rmsnorm(to_dev(x, "f32", dev), to_dev(w, "f32", dev))
+    np.testing.assert_allclose(to_np(y), orms.add_rmsnorm(x, w, acc=np.float64), atol=1e-5, rtol=1e-5)
+
+
+def test_fused_residual_forward(dev):
+    """tests/test_rmsnorm.py:17-25 (bf16 2x256x256, w = 1)."""
+    x, r = normal(5, (2, 256, 256), "bf16"), normal(6, (2, 256, 256), "bf16")
+    w = np.ones(256, np.float32)
+    h, y = rmsnorm(to_dev(x, "bf16", dev), to_dev(w, "bf16", dev), residual=to_dev(r, "bf16", dev))
+    _check_bf16(h.reshape(-1, 256), y.reshape(-1, 256), x.reshape(-1, 256), w, r.reshape(-1, 256))
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 1024), (3, 1024), (37, 100), (8, 8192), (5, 4096), (64, 2048), (16, 8)])
+def test_shapes_and_paths(dev, rows, dim):
+    """Vector path (dim % 8 == 0, dim <= 4096), generic path (other dims), odd row counts."""
+    x, r = normal(7, (rows, dim), "bf16"), normal(8, (rows, dim), "bf16")
+    w = normal(9, (dim,), "bf16", loc=1.0, scale=0.1)
+    h, y = rmsnorm(to_dev(x, "bf16", dev), to_dev(w, "bf16", dev), residual=to_dev(r, "bf16", dev))
+    _check_bf16(h, y, x, w, r)
+    y2 = rmsnorm(to_dev(x, "bf16", dev), to_dev(w, "bf16", dev))
+    y2_ref = round_bf16(orms.add_rmsnorm(x, w))
+    assert np.all(np.abs(to_np(y2).astype(np.float64) - y2_ref) <= bf16_ulp(y2_ref))
+
+
+def test_f32_weight_with_bf16_activations(dev):
+    """The model's case (gpt.py:75, :108-109): f32 weight, bf16 x and residual."""
+    x, r = normal(10, (256, 768), "bf16"), normal(11, (256, 768), "bf16")
+    w = normal(12, (768,), "f32", loc=1.0, scale=0.1)
+    h, y = rmsnorm(to_dev(x, "bf16", dev), to_dev(w, "f32", dev), residual=to_dev(r, "bf16", dev))
+    _check_bf16(h, y, x, w, r)
+
+
+def test_mixed_residual_dtype(dev):
+    x = normal(13, (64, 256), "bf16")
+    r = normal(14, (64, 256), "f32")
+    w = np.ones(256, np.float32)
+    h, y = rmsnorm(to_dev(x, "bf16", dev), to_dev(w, "f32", dev), residual=to_dev(r, "f32", dev))
+    _check_bf16(h, y, x, w, r)
+
+
+def test_gradients_match_reference(dev):
+    """tests/test_rmsnorm.py:28-44: loss = sum(y * cot) + sum(h * cot[::-1]), f32, 1e-4."""
+    x, r = normal(15, (64, 256)), normal(16, (64, 256))
+    w = normal(17, (256,), loc=1.0, scale=0.1)
+    cot = normal(18, (64, 256))
+    xt, rt, wt = (to_dev(a, "f32", dev).requires_grad_() for a in (x, r, w))
+    h, y = rmsnorm(xt, wt, residual=rt)
+    c = to_dev(cot, "f32", dev)
+    (torch.sum(y * c) + torch.sum(h * c.flip(0))).backward()
+    hh = x + r
+    dh, dw = orms.rmsnorm_bwd(hh, w, cot)
+    dh = dh + cot[::-1]
+    np.testing.assert_allclose(to_np(xt.grad), dh, atol=1e-4, rtol=1e-4)
+    np.testing.assert_allclose(to_np(rt.grad), dh, atol=1e-4, rtol=1e-4)
+    np.testing.assert_allclose(to_np(wt.grad), dw, atol=1e-4, rtol=1e-4)
+
+
+def test_plain_gradient(dev):
+    """tests/test_rmsnorm.py:47-54: loss = sum(tanh(rmsnorm(x, w))), 1e-5."""
+    x = normal(19, (32, 128))
+    w = np.ones(128, np.float32)
+    xt, wt = to_dev(x, "f32", dev).requires_grad_(), to_dev(w, "f32", dev).requires_grad_()
+    torch.sum(torch.tanh(rmsnorm(xt, wt))).backward()
+    y = orms.add_rmsnorm(x, w, acc=np.float64)
+    dx, dw = orms.rmsnorm_bwd(x, w, 1.0 - np.tanh(y) ** 2)
+    np.testing.assert_allclose(to_np(xt.grad), dx, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(to_np(wt.grad), dw, atol=1e-5, rtol=1e-5)
+
+
+def test_every_element_written_and_deterministic(dev):
+    """NaN-prefilled outputs through the C ABI: every element is written; reruns are bitwise equal."""
+    rows, dim = 1000, 1024
+    x, r = normal(20, (rows, dim), "bf16"), normal(21, (rows, dim), "bf16")
+    w = normal(22, (dim,), "bf16", loc=1.0, scale=0.1)
+    xt, rt, wt = to_dev(x, "bf16", dev), to_dev(r, "bf16", dev), to_dev(w, "bf16", dev)
+    outs = []
+    for _ in range(2):
+        h = torch.full_like(xt, float("nan"))
+        y = torch.full_like(xt, float("nan"))
+        rc = _hip.lib().ferrite_hip_add_rmsnorm(xt.data_ptr(), rt.data_ptr(), wt.data_ptr(), h.data_ptr(), y.data_ptr(),
+                                                rows, dim, _hip.BF16, _hip.BF16, 1e-6, _hip.stream_of(xt))
+        _hip.check(rc, "add_rmsnorm")
+        torch.cuda.synchronize()
+        assert not torch.isnan(h).any() and not torch.isnan(y).any()
+        outs.append((h.clone(), y.clone()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
