@@ -1,0 +1,284 @@
+#!/usr/bin/env python
+"""Benchmark of ferrite's MI355X kernels on BASELINE.json's metric.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Prints ONE JSON line. `value` is the headline: causal flash-attention forward
+throughput (algorithmic TFLOP/s, causal-skipped work counted free as in the
+reference's attention_flops) at B=4, H=16, T=2048, d=128 bf16. A "step" is
+one forward pass over that batch; K steps are timed back to back with HIP
+events on the stream the kernels run on, with inputs resident in HBM. The same
+line carries every other kernel of the path under "kernels": attention
+backward (delta, dK/dV, dQ), the long-context variant (B=1, H=8, T=8192, d=64),
+fused add+RMSNorm ([4096,1024] bf16, timed over 24 rotating buffer sets so the
+working set exceeds the 256 MB Infinity Cache) and the blocked matmul (bf16
+4096^3, f32 1000^3). Each carries its roofline fraction against MI355X peaks.
+
+cpu_baseline: the CPU oracle (numpy f32, the reference's materialised
+impl='xla' math) timed on this host's cores on a bounded sample of the same
+forward workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "ferrite-tpu_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "flash-attn fwd/bwd TFLOP/s + add-RMSNorm GB/s, % of MI355X roofline"
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+
+
+def _events_time(fn, iters: int, warmup: int) -> float:
+    """Average seconds per call of `fn` over `iters` back-to-back calls (HIP events on the current stream)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e-3 / iters
+
+
+def _traffic(kernel: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), read from the committed summary."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 4 and cells[0] == kernel:
+            try:
+                return float(cells[3])
+            except ValueError:
+                return None
+    return None
+
+
+def _roofline(bound: str, achieved: float, peak: float, unit: str, traffic):
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+def bench_attention(b, h, t, d, steps, warmup, seed=7):
+    import torch
+
+    from ferrite import _hip
+    from ferrite.kernels import attention_flops
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q, k, v, do = (torch.randn(b, h, t, d, device=dev, generator=g).to(torch.bfloat16) for _ in range(4))
+    o = torch.empty_like(q)
+    lse = torch.empty(b, h, t, device=dev)
+    delta = torch.empty(b, h, t, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    scale = d**-0.5
+    lib, st, bf = _hip.lib(), _hip.stream_of(q), _hip.BF16
+    P = [x.data_ptr() for x in (q, k, v, o, lse, delta, do, dq, dk, dv)]
+    qp, kp, vp, op, lp, dp, dop, dqp, dkp, dvp = P
+
+    def fwd():
+        _hip.check(lib.ferrite_hip_attn_fwd(qp, kp, vp, op, lp, b, h, t, t, d, bf, 1, scale, st), "fwd")
+
+    def dlt():
+        _hip.check(lib.ferrite_hip_attn_bwd_delta(op, dop, dp, b, h, t, d, bf, st), "delta")
+
+    def dkv():
+        _hip.check(lib.ferrite_hip_attn_bwd_dkv(qp, kp, vp, dop, lp, dp, dkp, dvp, b, h, t, t, d, bf, 1, scale, st), "dkv")
+
+    def dqk():
+        _hip.check(lib.ferrite_hip_attn_bwd_dq(qp, kp, vp, dop, lp, dp, dqp, b, h, t, t, d, bf, 1, scale, st), "dq")
+
+    def bwd():
+        dlt()
+        dkv()
+        dqk()
+
+    t_fwd = _events_time(fwd, steps, warmup)
+    t_delta = _events_time(dlt, steps, warmup)
+    t_dkv = _events_time(dkv, steps, warmup)
+    t_dq = _events_time(dqk, steps, warmup)
+    t_bwd = _events_time(bwd, steps, warmup)
+    f_fwd = attention_flops(b, h, t, t, d, causal=True)
+    f_bwd = attention_flops(b, h, t, t, d, causal=True, backward=True)
+    return {
+        "shape": [b, h, t, d],
+        "fwd_us": t_fwd * 1e6, "fwd_tflops": f_fwd / t_fwd / 1e12,
+        "delta_us": t_delta * 1e6, "dkv_us": t_dkv * 1e6, "dq_us": t_dq * 1e6,
+        "bwd_us": t_bwd * 1e6, "bwd_tflops": f_bwd / t_bwd / 1e12,
+        "fwd_bwd_tflops": (f_fwd + f_bwd) / (t_fwd + t_bwd) / 1e12,
+        "fwd_frac_bf16_peak": f_fwd / t_fwd / 1e12 / PEAK_BF16_TFLOPS,
+        "bwd_frac_bf16_peak": f_bwd / t_bwd / 1e12 / PEAK_BF16_TFLOPS,
+        "flops_fwd": f_fwd, "flops_bwd": f_bwd,
+    }
+
+
+def bench_rmsnorm(rows, dim, steps, warmup, sets=24):
+    """add+RMSNorm over `sets` rotating buffer sets (24 x 33.5 MB = 805 MB > the 256 MB MALL),
+    launched through a captured HIP graph so host launch cost does not pace the 4 us kernels."""
+    import torch
+
+    from ferrite import _hip
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    w = (1 + 0.1 * torch.randn(dim, device=dev, generator=g)).to(torch.bfloat16)
+    bufs = []
+    for _ in range(sets):
+        x = torch.randn(rows, dim, device=dev, generator=g).to(torch.bfloat16)
+        r = torch.randn(rows, dim, device=dev, generator=g).to(torch.bfloat16)
+        bufs.append((x, r, torch.empty_like(x), torch.empty_like(x)))
+    lib = _hip.lib()
+
+    def launch_all():
+        st = torch.cuda.current_stream().cuda_stream
+        for x, r, hh, y in bufs:
+            _hip.check(lib.ferrite_hip_add_rmsnorm(x.data_ptr(), r.data_ptr(), w.data_ptr(), hh.data_ptr(), y.data_ptr(),
+                                                   rows, dim, _hip.BF16, _hip.BF16, 1e-6, st), "add_rmsnorm")
+
+    launch_all()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch_all()
+    per_replay = _events_time(graph.replay, max(steps, 10), warmup)
+    t = per_replay / sets
+    nbytes = 4 * rows * dim * 2 + dim * 2  # read x, r, w; write h, y
+    # Same kernels launched eagerly from Python, for reference.
+    t_eager = _events_time(launch_all, max(steps // 2, 5), 2) / sets
+    return {"shape": [rows, dim], "us": t * 1e6, "gbs": nbytes / t / 1e9, "bytes": nbytes,
+            "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS, "buffer_sets": sets, "eager_us": t_eager * 1e6}
+
+
+def bench_matmul(steps, warmup):
+    import torch
+
+    from ferrite import _hip
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(3)
+    out = {}
+    for name, n, dt, code in (("bf16_4096", 4096, torch.bfloat16, _hip.BF16), ("f32_1000", 1000, torch.float32, _hip.F32)):
+        a = (torch.rand(n, n, device=dev, generator=g) * 2 - 1).to(dt)
+        bm = (torch.rand(n, n, device=dev, generator=g) * 2 - 1).to(dt)
+        c = torch.empty(n, n, device=dev, dtype=dt)
+        lib, st = _hip.lib(), _hip.stream_of(a)
+
+        def mm():
+            _hip.check(lib.ferrite_hip_matmul(a.data_ptr(), bm.data_ptr(), c.data_ptr(), n, n, n, code, code, st), "mm")
+
+        t = _events_time(mm, steps, warmup)
+        t_torch = _events_time(lambda: torch.matmul(a, bm), steps, warmup)
+        peak = PEAK_BF16_TFLOPS if dt == torch.bfloat16 else PEAK_FP32_TFLOPS
+        out[name] = {"us": t * 1e6, "tflops": 2 * n**3 / t / 1e12, "frac_peak": 2 * n**3 / t / 1e12 / peak,
+                     "torch_matmul_us": t_torch * 1e6}
+    return out
+
+
+def cpu_baseline(budget_s: float = 12.0):
+    """The oracle's materialised f32 attention forward (numpy; BLAS threads on this host's cores) on a
+    bounded sample of the headline workload's (b, h) heads, reported in the same unit."""
+    import numpy as np
+
+    from oracle import attention as oatt
+
+    b, h, t, d = 4, 16, 2048, 128
+    rng = np.random.default_rng(7)
+    q, k, v = (rng.standard_normal((1, 1, t, d)).astype(np.float32) for _ in range(3))
+    oatt.forward(q, k, v, causal=True, dtype=np.float32)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:  # whole passes over the 64 heads until the time budget is spent
+        oatt.forward(q, k, v, causal=True, dtype=np.float32)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and n % (b * h) == 0:
+            break
+    per_head = el / n
+    flops_head = 4 * t * t * d * 0.5
+    cores = len(os.sched_getaffinity(0))
+    return {"value": round(flops_head / per_head / 1e12, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"{n // (b * h)} full passes over the {b * h} (b,h) heads of the 4x16x2048x128 causal forward "
+                      f"({n} heads), oracle.attention.forward in numpy float32, {el:.1f} s",
+            "threads_env": os.environ.get("OMP_NUM_THREADS")}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["attn", "rmsnorm", "matmul", "all"], default="all")
+    a = ap.parse_args(argv)
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (single-GPU tier); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from ferrite import _hip, platform
+
+    _hip.lib()
+    torch.cuda.synchronize()
+    kernels = {}
+    if a.only in ("attn", "all"):
+        kernels["attention"] = bench_attention(4, 16, 2048, 128, a.steps, a.warmup)
+        kernels["attention_long_context"] = bench_attention(1, 8, 8192, 64, max(a.steps // 2, 3), 2, seed=27)
+    if a.only in ("rmsnorm", "all"):
+        kernels["add_rmsnorm"] = bench_rmsnorm(4096, 1024, a.steps, a.warmup)
+    if a.only in ("matmul", "all"):
+        kernels["matmul"] = bench_matmul(max(a.steps // 2, 3), 2)
+
+    att = kernels.get("attention")
+    if att is not None:
+        value = att["fwd_tflops"]
+        ms = att["fwd_us"] / 1e3
+        roof = _roofline("mfma", value, PEAK_BF16_TFLOPS, "TFLOP/s", _traffic("attn_fwd"))
+    else:  # partial runs report the first kernel measured
+        first = next(iter(kernels.values()))
+        value, ms, roof = first.get("gbs", first.get("tflops", 0.0)), first.get("us", 0.0) / 1e3, None
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "causal flash attention forward, q,k,v bf16 [B=4,H=16,T=2048,d=128] ~ N(0,1), "
+                               "scale 1/sqrt(128); step = one forward over the batch",
+                   "global_batch": 4, "seq_len": 2048, "heads": 16, "head_dim": 128, "parallelism": "none (1 GPU)"},
+        "roofline": roof,
+        "cpu_baseline": None if a.no_cpu_baseline else cpu_baseline(),
+        "kernels": kernels,
+        "platform": platform.describe(),
+    }
+    if "add_rmsnorm" in kernels:
+        r = kernels["add_rmsnorm"]
+        line["add_rmsnorm_roofline"] = _roofline("hbm", r["gbs"], PEAK_HBM_GBS, "GB/s", _traffic("add_rmsnorm"))
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -25,7 +25,11 @@ def test_baseline_bf16_4096(dev):
     assert out.dtype == torch.bfloat16 and out.shape == (4096, 4096)
     exact = omm.reference(a, b)  # f64 accumulation, f32 result
     g = to_np(out).astype(np.float64)
-    assert np.all(np.abs(g - exact) <= bf16_ulp(exact))  # within one bf16 ulp of the exact product
+    # One bf16 ulp of the exact product plus the f32 accumulation error bound (2^-20 sum|a||b|,
+    # which matters only where the product cancels to near zero).
+    absab = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    assert np.all(np.abs(g - exact) <= bf16_ulp(exact) + 2.0**-20 * absab)
+    assert np.mean(g != omm.reference(a, b, out_bf16=True)) < 0.01  # almost all equal bf16(exact)
     assert rel_fro(g, exact) < 4e-3
 
 
