@@ -191,6 +191,17 @@ def bench_matmul(steps, warmup):
     return out
 
 
+def bench_copy(nbytes: int = 256 << 20, iters: int = 5):
+    """A plain device-to-device copy of `nbytes`: reads and writes exactly nbytes, so FETCH_SIZE and
+    WRITE_SIZE of its dispatch calibrate the byte counters; also a ceiling for streaming kernels."""
+    import torch
+
+    src = torch.ones(nbytes // 4, device="cuda:0")
+    dst = torch.empty_like(src)
+    t = _events_time(lambda: dst.copy_(src), iters, 2)
+    return {"bytes_each_way": nbytes, "us": t * 1e6, "gbs_read_plus_write": 2 * nbytes / t / 1e9}
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """The oracle's materialised f32 attention forward (numpy; BLAS threads on this host's cores) on a
     bounded sample of the headline workload's (b, h) heads, reported in the same unit."""
@@ -225,6 +236,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["attn", "rmsnorm", "matmul", "all"], default="all")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 256 MiB device copy (the HBM byte-counter calibration for rocprofv3 --pmc)")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (single-GPU tier); run with --gpus 1", file=sys.stderr)
@@ -237,6 +250,8 @@ def main(argv=None):
     _hip.lib()
     torch.cuda.synchronize()
     kernels = {}
+    if a.calibrate_copy:
+        kernels["copy_256MiB"] = bench_copy()
     if a.only in ("attn", "all"):
         kernels["attention"] = bench_attention(4, 16, 2048, 128, a.steps, a.warmup)
         kernels["attention_long_context"] = bench_attention(1, 8, 8192, 64, max(a.steps // 2, 3), 2, seed=27)

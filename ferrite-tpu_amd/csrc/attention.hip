@@ -106,12 +106,44 @@ struct Stager {
   static constexpr int kColGroups = D / kVec;
   static constexpr int kJobs = (ROWS / 4) * kColGroups;
   static constexpr int kJobsPerThread = (kJobs + kThreads - 1) / kThreads;
+  static constexpr uint32_t kOutOfRange = 0x80000000u;  // >= any num_records (heads are < 2 GiB)
   typedef typename Elem<T>::vec vec;
   vec v[kJobsPerThread][4];
+  uint32_t voff[kJobsPerThread][4];  // byte offset of each job row inside a tile (aligned path)
+
+  // Aligned rows use raw buffer loads: the tile's first row is folded into the
+  // buffer base, each lane's offset inside the tile is fixed, and the hardware
+  // range check returns zeros for rows past the end and for padded columns
+  // (whose offset is kOutOfRange), so the staging has no branches.
+  __device__ __forceinline__ explicit Stager(int d) {
+    if constexpr (ALIGNED) {
+      const int t = threadIdx.x;
+#pragma unroll
+      for (int j = 0; j < kJobsPerThread; ++j) {
+        const int job = t + kThreads * j;
+        const int cg = job % kColGroups, rg = job / kColGroups;
+        const int c0 = cg * kVec;
+        const bool ok = job < kJobs && c0 < d;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) voff[j][i] = ok ? (uint32_t)(((rg * 4 + i) * d + c0) * (int)sizeof(T)) : kOutOfRange;
+      }
+    }
+  }
 
   // Rows [r0, r0 + ROWS) of a [nrows, d] matrix (row stride d) at `base`.
-  __device__ __forceinline__ void load(const T* __restrict__ base, int64_t r0, int64_t nrows, int d) {
+  __device__ __forceinline__ void load(const T* __restrict__ base, int r0, int nrows, int d) {
     const int t = threadIdx.x;
+    if constexpr (ALIGNED) {
+      const int rows_left = nrows - r0 > 0 ? nrows - r0 : 0;
+      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<T*>(base) + (int64_t)r0 * d, (short)0, rows_left * d * (int)sizeof(T), 0x00020000);
+#pragma unroll
+      for (int j = 0; j < kJobsPerThread; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          v[j][i] = __builtin_bit_cast(vec, __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)voff[j][i], 0, 0));
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < kJobsPerThread; ++j) {
       const int job = t + kThreads * j;
@@ -119,18 +151,10 @@ struct Stager {
       const int c0 = cg * kVec;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t row = r0 + rg * 4 + i;
+        const int row = r0 + rg * 4 + i;
         const bool rok = job < kJobs && row < nrows;
-        if constexpr (ALIGNED) {
-          if (rok && c0 < d)
-            v[j][i] = *reinterpret_cast<const vec*>(base + row * d + c0);
-          else
 #pragma unroll
-            for (int e = 0; e < kVec; ++e) v[j][i][e] = (T)0.f;
-        } else {
-#pragma unroll
-          for (int e = 0; e < kVec; ++e) v[j][i][e] = (rok && c0 + e < d) ? base[row * d + c0 + e] : (T)0.f;
-        }
+        for (int e = 0; e < kVec; ++e) v[j][i][e] = (rok && c0 + e < d) ? base[row * d + c0 + e] : (T)0.f;
       }
     }
   }
@@ -172,38 +196,49 @@ struct Stager {
 };
 
 // Q / dO fragments of one wave's 32 rows held in registers as the B operand:
-// lane (l32, g) holds row r0 + l32, elements kk*16 + g*8 .. +8.
-template <typename T, int D, bool ALIGNED>
+// lane (l32, g) holds row r0 + l32, elements kk*16 + g*8 .. +8. With NEG the
+// fragments are negated (used for a negative softmax scale).
+template <typename T, int D, bool ALIGNED, bool NEG = false>
 __device__ __forceinline__ void load_row_frags(typename Elem<T>::frag (&f)[D / 16], const T* __restrict__ base,
-                                               int64_t r0, int64_t nrows, int d) {
+                                               int r0, int nrows, int d) {
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
-  const int64_t row = r0 + l32;
-  const bool rok = row < nrows;
+  const int row = r0 + l32;
+  if constexpr (ALIGNED) {
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), (short)0, nrows * d * (int)sizeof(T), 0x00020000);
 #pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) {
-    const int c0 = kk * 16 + g * 8;
-    if constexpr (ALIGNED) {
-      if (rok && c0 < d) {
-        if constexpr (sizeof(T) == 2) {
-          f[kk] = *reinterpret_cast<const bf16x8*>(base + row * d + c0);
-        } else {
-          f32x4 a = *reinterpret_cast<const f32x4*>(base + row * d + c0);
-          f32x4 b = (c0 + 4 < d) ? *reinterpret_cast<const f32x4*>(base + row * d + c0 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            f[kk][e] = a[e];
-            f[kk][4 + e] = b[e];
-          }
-        }
+    for (int kk = 0; kk < D / 16; ++kk) {
+      const int c0 = kk * 16 + g * 8;
+      if constexpr (sizeof(T) == 2) {
+        const int off = c0 < d ? (row * d + c0) * 2 : 0x7ffffff0;
+        f[kk] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
       } else {
+        const int off0 = c0 < d ? (row * d + c0) * 4 : 0x7ffffff0;
+        const int off1 = c0 + 4 < d ? (row * d + c0 + 4) * 4 : 0x7ffffff0;
+        const f32x4 a = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off0, 0, 0));
+        const f32x4 b = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off1, 0, 0));
 #pragma unroll
-        for (int e = 0; e < 8; ++e) f[kk][e] = (T)0.f;
+        for (int e = 0; e < 4; ++e) {
+          f[kk][e] = a[e];
+          f[kk][4 + e] = b[e];
+        }
       }
-    } else {
+    }
+  } else {
+    const bool rok = row < nrows;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+      const int c0 = kk * 16 + g * 8;
 #pragma unroll
       for (int e = 0; e < 8; ++e) f[kk][e] = (rok && c0 + e < d) ? base[row * d + c0 + e] : (T)0.f;
     }
+  }
+  if constexpr (NEG) {
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[kk][e] = -f[kk][e];
   }
 }
 
@@ -240,6 +275,34 @@ __device__ __forceinline__ void store_acc_rows(const f32x16 (&acc)[D / 32], T* _
   }
 }
 
+// N products acc(i) += A(i) * B(i) whose A operands come from LDS: the reads
+// run kAhead products ahead of the MFMAs and the scheduler is asked to
+// alternate one MFMA with one LDS read, so the read latency hides behind the
+// matrix pipe instead of stalling each product.
+constexpr int kAhead = 4;
+
+template <int N, typename Read, typename Mma>
+__device__ __forceinline__ void lds_mfma_pipeline(Read read, Mma mma) {
+  typedef decltype(read(0)) FragT;
+  FragT buf[N];
+#pragma unroll
+  for (int i = 0; i < kAhead && i < N; ++i) buf[i] = read(i);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if (i + kAhead < N) buf[i + kAhead] = read(i + kAhead);
+    mma(i, buf[i]);
+  }
+  if constexpr (sizeof(FragT) == 16) {  // bf16: one LDS read and one MFMA per product
+#pragma unroll
+    for (int i = 0; i < kAhead && i < N; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i + kAhead < N) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  }
+}
+
 template <typename T>
 struct AttnTiles {
   // kv rows per forward / dQ step, q rows per dK/dV step: one 128-byte
@@ -264,10 +327,12 @@ struct Fwd {
   static constexpr int kMinBlocks = (D <= 128 && sizeof(T) == 2) ? 2 : 1;
 };
 
+// `scale_log2` = |scale| * log2(e) (> 0); a negative scale arrives as neg_q = 1
+// and is applied by negating the query fragments.
 template <typename T, int D, bool ALIGNED>
 __global__ __launch_bounds__(kThreads, (Fwd<T, D, ALIGNED>::kMinBlocks)) void attn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
-    float* __restrict__ lse, int bh_count, int64_t Sq, int64_t Sk, int d, int causal, float scale_log2,
+    float* __restrict__ lse, int bh_count, int Sq, int Sk, int d, int causal, float scale_log2, int neg_q,
     int n_qtiles) {
   typedef Fwd<T, D, ALIGNED> F;
   typedef typename Elem<T>::frag frag;
@@ -279,31 +344,34 @@ __global__ __launch_bounds__(kThreads, (Fwd<T, D, ALIGNED>::kMinBlocks)) void at
   const int qt = n_qtiles - 1 - (int)(blockIdx.x / bh_count);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
-  const int64_t q0 = (int64_t)qt * F::BQ;
-  const int64_t q0w = q0 + wave * 32;
-  const int64_t qrow = q0w + l32;
+  const int q0 = qt * F::BQ;
+  const int q0w = q0 + wave * 32;
+  const int qrow = q0w + l32;
 
   const T* qb = q + (int64_t)bh * Sq * d;
   const T* kb = k + (int64_t)bh * Sk * d;
   const T* vb = v + (int64_t)bh * Sk * d;
 
-  const int64_t q_last = (q0 + F::BQ < Sq ? q0 + F::BQ : Sq) - 1;
-  const int n_tiles = causal ? (int)((q_last < Sk - 1 ? q_last : Sk - 1) / F::BK + 1) : (int)cdiv(Sk, F::BK);
+  const int q_last = min(q0 + F::BQ, Sq) - 1;
+  const int n_tiles = causal ? min(q_last, Sk - 1) / F::BK + 1 : (Sk + F::BK - 1) / F::BK;
   const bool wave_active = q0w < Sq;
-  const int64_t wq_last = (q0w + 31 < Sq ? q0w + 31 : Sq - 1);
-  const int wave_tiles = !wave_active ? 0 : causal ? (int)(wq_last / F::BK + 1) : n_tiles;
+  const int wave_tiles = !wave_active ? 0 : causal ? min(q0w + 31, Sq - 1) / F::BK + 1 : n_tiles;
 
   frag qf[F::KS];
-  load_row_frags<T, D, ALIGNED>(qf, qb, q0w, Sq, d);
+  if (neg_q)
+    load_row_frags<T, D, ALIGNED, true>(qf, qb, q0w, Sq, d);
+  else
+    load_row_frags<T, D, ALIGNED, false>(qf, qb, q0w, Sq, d);
 
   f32x16 acc[F::DT];
 #pragma unroll
   for (int u = 0; u < F::DT; ++u)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[u][r] = 0.f;
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY;
+  float lsum[4] = {0.f, 0.f, 0.f, 0.f};
 
-  Stager<T, D, F::BK, ALIGNED> ks, vs;
+  Stager<T, D, F::BK, ALIGNED> ks(d), vs(d);
   ks.load(kb, 0, Sk, d);
   vs.load(vb, 0, Sk, d);
 
@@ -315,72 +383,78 @@ __global__ __launch_bounds__(kThreads, (Fwd<T, D, ALIGNED>::kMinBlocks)) void at
     vs.store_transposed(vl);
     __syncthreads();
     if (j + 1 < n_tiles) {
-      ks.load(kb, (int64_t)(j + 1) * F::BK, Sk, d);
-      vs.load(vb, (int64_t)(j + 1) * F::BK, Sk, d);
+      ks.load(kb, (j + 1) * F::BK, Sk, d);
+      vs.load(vb, (j + 1) * F::BK, Sk, d);
     }
     if (j >= wave_tiles) continue;
 
-    const int64_t kv0 = (int64_t)j * F::BK;
-    // S^T = K Q^T: s[t][r] is key kv0 + t*32 + g*16 + r, query qrow.
+    const int kv0 = j * F::BK;
+    // S^T = K Q^T: s[t][r] is key kv0 + t*32 + g*16 + r, query qrow. All K
+    // fragments of the tile are read before the products so the LDS latency
+    // overlaps the MFMA chain; the two subtiles alternate accumulators.
     f32x16 s[F::NT];
 #pragma unroll
     for (int t = 0; t < F::NT; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < F::KS; ++kk)
-#pragma unroll
-      for (int t = 0; t < F::NT; ++t) mma32(RowTile<T, D>::frag(kl, t * 32 + l32, kk * 16 + g * 8), qf[kk], s[t]);
+    lds_mfma_pipeline<F::KS * F::NT>(
+        [&](int i) { return RowTile<T, D>::frag(kl, (i % F::NT) * 32 + l32, (i / F::NT) * 16 + g * 8); },
+        [&](int i, const frag& a) { mma32(a, qf[i / F::NT], s[i % F::NT]); });
 
-    const bool need_mask = (causal && kv0 + F::BK - 1 > q0w) || (kv0 + F::BK > Sk);
+    // Mask on the raw scores (diagonal and ragged tiles only), then the row max.
+    if ((causal && kv0 + F::BK - 1 > q0w) || kv0 + F::BK > Sk) {
+      const int lim = causal ? min(qrow, Sk - 1) : Sk - 1;
+#pragma unroll
+      for (int t = 0; t < F::NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[t][r] = (kv0 + t * 32 + g * 16 + r > lim) ? -INFINITY : s[t][r];
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < F::NT; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[t][r] * scale_log2;
-        if (need_mask) {
-          const int64_t kv = kv0 + t * 32 + g * 16 + r;
-          if (kv >= Sk || (causal && kv > qrow)) x = -INFINITY;
-        }
-        s[t][r] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = lane32_max(mx);
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+    mx = lane32_max(mx) * scale_log2;
     if (__any(mx > m + kRescaleThreshold)) {
       const float m_new = fmaxf(m, mx);
       const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lsum[i] *= alpha;
 #pragma unroll
       for (int u = 0; u < F::DT; ++u)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[u][r] *= alpha;
       m = m_new;
     }
+    const float neg_m = -m;
     frag pf[F::NT][2];
 #pragma unroll
     for (int t = 0; t < F::NT; ++t) {
       float p[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        p[r] = __builtin_amdgcn_exp2f(s[t][r] - m);
-        l += p[r];
+        p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][r], scale_log2, neg_m));
+        lsum[r & 3] += p[r];
       }
       to_frag(p, pf[t][0]);
       to_frag(p + 8, pf[t][1]);
     }
-    // O^T += V^T P^T
-#pragma unroll
-    for (int u = 0; u < F::DT; ++u)
-#pragma unroll
-      for (int t = 0; t < F::NT; ++t)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          mma32(TrTile<T>::frag(vl, u * 32 + l32, t * 32 + g * 16 + h * 8), pf[t][h], acc[u]);
+    // O^T += V^T P^T: all V^T fragments first, then the products with the
+    // output tiles innermost (independent accumulators back to back).
+    // Product i uses chunk c = i / DT of the 16-key chunks (t, h) and output tile u = i % DT.
+    lds_mfma_pipeline<F::DT * F::NT * 2>(
+        [&](int i) {
+          const int c = i / F::DT;
+          return TrTile<T>::frag(vl, (i % F::DT) * 32 + l32, (c >> 1) * 32 + g * 16 + (c & 1) * 8);
+        },
+        [&](int i, const frag& a) {
+          const int c = i / F::DT;
+          mma32(a, pf[c >> 1][c & 1], acc[i % F::DT]);
+        });
   }
 
   if (!wave_active) return;
-  l = lane32_sum(l);
+  const float l = lane32_sum((lsum[0] + lsum[1]) + (lsum[2] + lsum[3]));
   const float inv = 1.0f / l;
   store_acc_rows<T, D, ALIGNED>(acc, o + (int64_t)bh * Sq * d, qrow, Sq, d, inv);
   if (g == 0 && qrow < Sq) lse[(int64_t)bh * Sq + qrow] = (m + __builtin_amdgcn_logf(l)) * kLn2;
@@ -479,7 +553,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_dq_kernel(const T* __restric
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[u][r] = 0.f;
 
-  Stager<T, D, F::BK, ALIGNED> ks, vs;
+  Stager<T, D, F::BK, ALIGNED> ks(d), vs(d);
   ks.load(kb, 0, Sk, d);
   vs.load(vb, 0, Sk, d);
 
@@ -607,7 +681,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_dkv_kernel(const T* __restri
       dva[u][r] = 0.f;
     }
 
-  Stager<T, D, F::BQ, ALIGNED> qs, dos;
+  Stager<T, D, F::BQ, ALIGNED> qs(d), dos(d);
   float st_lse = 0.f, st_d = 0.f;
   auto load_q = [&](int it) {
     const int64_t r0 = (int64_t)it * F::BQ;
@@ -732,6 +806,10 @@ int check_shape(const char* name, const Shape& s, int dtype, int causal, bool bw
                     (bwd ? " not supported (backward supports head_dim <= 128)"
                          : " not supported (head_dim <= 128 or == 256)"));
   if (s.b * s.h > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": b*h too large");
+  // In-kernel offsets within one (b, h) head are 32-bit byte offsets.
+  const int64_t head_bytes = (s.sq > s.sk ? s.sq : s.sk) * s.d * (dtype == FERRITE_BF16 ? 2 : 4);
+  if (head_bytes > 0x7fff0000)
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": one (b, h) head must be under 2 GiB");
   return FERRITE_OK;
 }
 
@@ -746,9 +824,15 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: grid too large");
   auto kern = attn_fwd_kernel<T, D, AL>;
   set_lds(kern, F::kLds);
+  // The kernel takes the row max on raw scores, which needs a positive
+  // multiplier: a negative scale negates q instead, and a zero scale becomes a
+  // tiny positive one (uniform weights either way).
+  float c = scale * kLog2e;
+  const int neg_q = c < 0.f;
+  c = fmaxf(fabsf(c), 1e-30f);
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(kThreads), F::kLds, stream, static_cast<const T*>(q),
-                     static_cast<const T*>(k), static_cast<const T*>(v), static_cast<T*>(o), lse, (int)bh, s.sq, s.sk,
-                     (int)s.d, causal, scale * kLog2e, (int)nq);
+                     static_cast<const T*>(k), static_cast<const T*>(v), static_cast<T*>(o), lse, (int)bh, (int)s.sq,
+                     (int)s.sk, (int)s.d, causal, c, neg_q, (int)nq);
   return check_launch("ferrite_flash_attention_fwd");
 }
 

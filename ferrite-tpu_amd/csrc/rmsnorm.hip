@@ -13,6 +13,8 @@
 //   h   = f32(x) + f32(residual)            (stored rounded to x's dtype)
 //   inv = rsqrt(sum(h*h) * (1/dim) + eps)
 //   y   = (h * inv) * f32(w)                (from the unrounded f32 h)
+#include <algorithm>
+
 #include "common.h"
 
 namespace ferrite {
@@ -52,59 +54,150 @@ __device__ __forceinline__ void store8(float* p, const float* in) {
   *reinterpret_cast<f32x4*>(p + 4) = b;
 }
 
-// Fast path: dim % 8 == 0, 16-byte aligned rows, dim <= 64 * 8 * VPL. Lane l
-// owns chunks c = l + 64 * i (i < VPL) of its row.
-template <typename TX, typename TW, bool RES, int VPL>
+// Streaming 16-byte loads/stores with the non-temporal hint: every byte of x,
+// residual, h and y is touched exactly once, so keeping them out of the caches
+// leaves the memory system to the stream (measured: ~15% faster than plain
+// loads at [4096, 1024], and the only way past a plain copy's bandwidth there).
+__device__ __forceinline__ u32x4 ld16_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ void st16_nt(void* p, u32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p)); }
+
+// 8 elements of T as raw 16-byte words (one word for bf16, two for f32).
+template <typename T>
+struct Raw8 {
+  u32x4 w[sizeof(T) / 2];
+};
+template <typename T>
+__device__ __forceinline__ void ld8_nt(const T* p, Raw8<T>& r) {
+#pragma unroll
+  for (int i = 0; i < (int)sizeof(T) / 2; ++i) r.w[i] = ld16_nt(reinterpret_cast<const char*>(p) + 16 * i);
+}
+template <typename T>
+__device__ __forceinline__ void unpack8(const Raw8<T>& r, float* out) {
+  if constexpr (sizeof(T) == 2) {
+    const bf16x8 v = __builtin_bit_cast(bf16x8, r.w[0]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = (float)v[e];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const f32x4 v = __builtin_bit_cast(f32x4, r.w[i]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[4 * i + e] = v[e];
+    }
+  }
+}
+template <typename T>
+__device__ __forceinline__ void st8_nt(T* p, const float* in) {
+  if constexpr (sizeof(T) == 2) {
+    bf16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (bf16)in[e];
+    st16_nt(p, __builtin_bit_cast(u32x4, v));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const f32x4 v = {in[4 * i], in[4 * i + 1], in[4 * i + 2], in[4 * i + 3]};
+      st16_nt(reinterpret_cast<char*>(p) + 16 * i, __builtin_bit_cast(u32x4, v));
+    }
+  }
+}
+
+// One batch of up to DEPTH consecutive rows starting at `base` for one wave.
+// With CHECK = false every row and chunk is in range (the common case: full
+// batches of rows whose width is exactly 512 * VPL), so all loads of the batch
+// are issued back to back with no branches.
+template <typename TX, typename TW, bool RES, int VPL, int DEPTH, bool CHECK>
+__device__ __forceinline__ void rms_batch(const TX* __restrict__ x, const TX* __restrict__ r, TX* __restrict__ h,
+                                          TX* __restrict__ y, const float (&wv)[VPL][kChunk], int64_t base,
+                                          int64_t rows, int dim, int nchunks, float inv_dim, float eps) {
+  const int lane = threadIdx.x & 63;
+  Raw8<TX> xr[DEPTH][VPL], rr[DEPTH][VPL];
+#pragma unroll
+  for (int k = 0; k < DEPTH; ++k) {
+    if (CHECK && base + k >= rows) break;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int c = lane + 64 * i;
+      if (!CHECK || c < nchunks) {
+        ld8_nt(x + (base + k) * dim + c * kChunk, xr[k][i]);
+        if constexpr (RES) ld8_nt(r + (base + k) * dim + c * kChunk, rr[k][i]);
+      }
+    }
+  }
+  // Keep every load of the batch ahead of the arithmetic (the scheduler would
+  // otherwise sink them next to their uses and leave few bytes in flight).
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < DEPTH; ++k) {
+    if (CHECK && base + k >= rows) break;
+    const int64_t off = (base + k) * dim;
+    float hv[VPL][kChunk];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      if (!CHECK || lane + 64 * i < nchunks) {
+        unpack8(xr[k][i], hv[i]);
+        if constexpr (RES) {
+          float rv[kChunk];
+          unpack8(rr[k][i], rv);
+#pragma unroll
+          for (int e = 0; e < kChunk; ++e) hv[i][e] += rv[e];
+        }
+#pragma unroll
+        for (int e = 0; e < kChunk; ++e) ss += hv[i][e] * hv[i][e];
+      }
+    }
+    if constexpr (RES) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int c = lane + 64 * i;
+        if (!CHECK || c < nchunks) st8_nt(h + off + c * kChunk, hv[i]);
+      }
+    }
+    ss = wave_sum(ss);
+    const float inv = __builtin_amdgcn_rsqf(ss * inv_dim + eps);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int c = lane + 64 * i;
+      if (!CHECK || c < nchunks) {
+        float yv[kChunk];
+#pragma unroll
+        for (int e = 0; e < kChunk; ++e) yv[e] = (hv[i][e] * inv) * wv[i][e];
+        st8_nt(y + off + c * kChunk, yv);
+      }
+    }
+  }
+}
+
+// Fast path: dim % 8 == 0, 16-byte aligned rows, dim <= 64 * 8 * VPL (FULL:
+// dim == 64 * 8 * VPL). Lane l owns chunks c = l + 64 * i (i < VPL) of its row.
+// The grid is persistent: each wave takes DEPTH consecutive rows at a time and
+// issues all of their loads before any arithmetic, so it keeps DEPTH rows of x
+// and residual in flight; waves then stride over the remaining rows.
+template <typename TX, typename TW, bool RES, int VPL, int DEPTH, bool FULL>
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const TX* __restrict__ x, const TX* __restrict__ r,
                                                           const TW* __restrict__ w, TX* __restrict__ h,
                                                           TX* __restrict__ y, int64_t rows, int dim, float inv_dim,
                                                           float eps) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int64_t base = row * dim;
+  const int64_t nwaves = (int64_t)gridDim.x * kRowsPerBlock;
   const int nchunks = dim / kChunk;
 
-  float hv[VPL][kChunk];
-  float ss = 0.f;
+  float wv[VPL][kChunk];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int c = lane + 64 * i;
-    if (c < nchunks) {
-      float xv[kChunk];
-      load8(x + base + c * kChunk, xv);
-      if constexpr (RES) {
-        float rv[kChunk];
-        load8(r + base + c * kChunk, rv);
-#pragma unroll
-        for (int e = 0; e < kChunk; ++e) hv[i][e] = xv[e] + rv[e];
-      } else {
-#pragma unroll
-        for (int e = 0; e < kChunk; ++e) hv[i][e] = xv[e];
-      }
-#pragma unroll
-      for (int e = 0; e < kChunk; ++e) ss += hv[i][e] * hv[i][e];
-    }
+    if (FULL || c < nchunks) load8(w + c * kChunk, wv[i]);
   }
-  if constexpr (RES) {
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int c = lane + 64 * i;
-      if (c < nchunks) store8(h + base + c * kChunk, hv[i]);
-    }
-  }
-  ss = wave_sum(ss);
-  const float inv = __builtin_amdgcn_rsqf(ss * inv_dim + eps);
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nchunks) {
-      float wv[kChunk], yv[kChunk];
-      load8(w + c * kChunk, wv);
-#pragma unroll
-      for (int e = 0; e < kChunk; ++e) yv[e] = (hv[i][e] * inv) * wv[e];
-      store8(y + base + c * kChunk, yv);
-    }
+
+  for (int64_t base = ((int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) * DEPTH; base < rows;
+       base += nwaves * DEPTH) {
+    if (FULL && base + DEPTH <= rows)
+      rms_batch<TX, TW, RES, VPL, DEPTH, false>(x, r, h, y, wv, base, rows, dim, nchunks, inv_dim, eps);
+    else
+      rms_batch<TX, TW, RES, VPL, DEPTH, true>(x, r, h, y, wv, base, rows, dim, nchunks, inv_dim, eps);
   }
 }
 
@@ -156,17 +249,28 @@ int launch(const void* x, const void* r, const void* w, void* h, void* y, int64_
   if (fast) {
     const int nchunks = (int)(dim / kChunk);
     const int vpl = (int)cdiv(nchunks, 64);
-#define FERRITE_RMS_CASE(V)                                                                                     \
-  hipLaunchKernelGGL((rmsnorm_rows_kernel<TX, TW, RES, V>), grid, block, 0, stream, xp, rp, wp, hp, yp, rows, \
-                     (int)dim, inv_dim, eps)
+    // DEPTH rows in flight per wave (fewer for wide rows, to bound registers);
+    // at most one workgroup per (CU x 4) so small problems run in one pass.
+    auto pgrid = [&](int depth) {
+      return dim3((unsigned)std::min<int64_t>(cdiv(rows, (int64_t)kRowsPerBlock * depth), 1024));
+    };
+#define FERRITE_RMS_CASE(V, DEPTH)                                                                                 \
+  do {                                                                                                             \
+    if (nchunks == 64 * (V))                                                                                       \
+      hipLaunchKernelGGL((rmsnorm_rows_kernel<TX, TW, RES, V, DEPTH, true>), pgrid(DEPTH), block, 0, stream, xp, rp, \
+                         wp, hp, yp, rows, (int)dim, inv_dim, eps);                                                \
+    else                                                                                                           \
+      hipLaunchKernelGGL((rmsnorm_rows_kernel<TX, TW, RES, V, DEPTH, false>), pgrid(DEPTH), block, 0, stream, xp,    \
+                         rp, wp, hp, yp, rows, (int)dim, inv_dim, eps);                                            \
+  } while (0)
     if (vpl <= 1)
-      FERRITE_RMS_CASE(1);
+      FERRITE_RMS_CASE(1, 4);
     else if (vpl <= 2)
-      FERRITE_RMS_CASE(2);
+      FERRITE_RMS_CASE(2, 4);
     else if (vpl <= 4)
-      FERRITE_RMS_CASE(4);
+      FERRITE_RMS_CASE(4, 2);
     else
-      FERRITE_RMS_CASE(8);
+      FERRITE_RMS_CASE(8, 1);
 #undef FERRITE_RMS_CASE
   } else {
     hipLaunchKernelGGL((rmsnorm_rows_generic_kernel<TX, TW, RES>), grid, block, 0, stream, xp, rp, wp, hp, yp, rows,
