@@ -162,8 +162,23 @@ def bench_rmsnorm(rows, dim, steps, warmup, sets=24):
     nbytes = 4 * rows * dim * 2 + dim * 2  # read x, r, w; write h, y
     # Same kernels launched eagerly from Python, for reference.
     t_eager = _events_time(launch_all, max(steps // 2, 5), 2) / sets
+
+    # A plain device copy moving the same bytes (x -> h, r -> y), replayed the same way: the
+    # bandwidth a streaming kernel of this size gets on this part.
+    def copy_all():
+        for x, r, hh, y in bufs:
+            hh.copy_(x)
+            y.copy_(r)
+
+    copy_all()
+    torch.cuda.synchronize()
+    cgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(cgraph):
+        copy_all()
+    t_copy = _events_time(cgraph.replay, max(steps, 10), warmup) / sets
     return {"shape": [rows, dim], "us": t * 1e6, "gbs": nbytes / t / 1e9, "bytes": nbytes,
-            "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS, "buffer_sets": sets, "eager_us": t_eager * 1e6}
+            "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS, "buffer_sets": sets, "eager_us": t_eager * 1e6,
+            "copy_same_bytes_us": t_copy * 1e6, "copy_same_bytes_gbs": (4 * rows * dim * 2) / t_copy / 1e9}
 
 
 def bench_matmul(steps, warmup):
