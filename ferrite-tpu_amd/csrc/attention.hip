@@ -47,6 +47,12 @@ __device__ __forceinline__ int perm_row(int r) {
   return (r & ~31) | ((rr >> 2) << 3) | (g << 2) | (rr & 3);
 }
 
+// Inverse of perm_row: the logical row held by physical row `p` (bits 4,3,2 of
+// the row inside its 32-row block rotate the other way).
+__device__ __forceinline__ int perm_src(int p) {
+  return (p & ~31) | (((p >> 2) & 1) << 4) | (((p >> 4) & 1) << 3) | (((p >> 3) & 1) << 2) | (p & 3);
+}
+
 __device__ __forceinline__ int swz(int n) { return (n ^ (n >> 3)) & 7; }
 
 // ---- tile geometry -------------------------------------------------------
@@ -461,6 +467,230 @@ __global__ __launch_bounds__(kThreads, (Fwd<T, D, ALIGNED>::kMinBlocks)) void at
 }
 
 // ===========================================================================
+// Forward, bf16 with D in {64, 128}: K and V staged by LDS DMA
+// ===========================================================================
+// Same decomposition as attn_fwd_kernel (4 waves x 32 query rows, 64-key
+// tiles, double-buffered LDS), but the K and V tiles reach LDS through
+// buffer_load ... lds (gfx950 direct-to-LDS loads): no staging registers, no
+// LDS writes, and rows past the end or padded columns arrive as zeros from the
+// buffer range check. Both tiles are plain row-major with 16-byte chunks
+// XOR-swizzled per row; V^T fragments come from ds_read_b64_tr_b16, which
+// transposes 4x4 blocks of 16-bit elements across each 16-lane group.
+template <int D>
+struct SwzTile {
+  static constexpr int kRowBytes = D * 2;
+  static constexpr int kChunks = kRowBytes / 16;       // 16-byte chunks per row
+  static constexpr int kRowsPer256 = 256 / kRowBytes;  // rows sharing one pass of the 64 banks
+  // Chunk swizzle: an odd multiplier makes it a bijection over any kChunks
+  // consecutive rows (conflict-free 16-byte fragment reads down 16 rows), and
+  // 5 also separates the 4-row x 4-chunk footprint of a transposed read.
+  static __device__ __forceinline__ int swz(int r) { return (5 * (r / kRowsPer256)) & (kChunks - 1); }
+  static __device__ __forceinline__ int off(int r, int col) {
+    return r * kRowBytes + (((col >> 3) ^ swz(r)) << 4) + (col & 7) * 2;
+  }
+  static __device__ __forceinline__ bf16x8 frag(const char* base, int r, int col) {
+    return *reinterpret_cast<const bf16x8*>(base + off(r, col));
+  }
+};
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// A-operand fragment of V^T (32 d x 16 keys) from a row-major V tile: lane
+// (l32, g) gets V[kv0 + g*16 + e][dcol0 + l32] for e = 0..7, as two transposed
+// 8-byte reads (e = 0..3 and 4..7). Within each 16-lane group, slot s = lane %
+// 16 supplies the address of keys kv0 + g*16 + half*4 + s/4, columns
+// dcol0 + 16*((lane/16) % 2) + 4*(s % 4); the instruction hands lane 4a + b of
+// the group element b of the pieces supplied by slots a, a+4, a+8, a+12.
+template <int D>
+__device__ __forceinline__ bf16x8 vt_frag(const char* vl, int kv0, int dcol0) {
+  const int lane = threadIdx.x & 63;
+  const int s = lane & 15;
+  const int row = kv0 + (lane >> 5) * 16 + (s >> 2);
+  const int col = dcol0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const lds_i16x4* p0 = reinterpret_cast<const lds_i16x4*>(
+      reinterpret_cast<uintptr_t>(vl + SwzTile<D>::off(row, col)));
+  const lds_i16x4* p1 = reinterpret_cast<const lds_i16x4*>(
+      reinterpret_cast<uintptr_t>(vl + SwzTile<D>::off(row + 4, col)));
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p0));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p1));
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// DMA of one 64-row tile of a [nrows, d] bf16 matrix into a swizzled LDS tile.
+// Each wave instruction fills 1 KB of LDS (64 lanes x 16 bytes, lane order);
+// lane (row R, physical chunk c) loads logical chunk c ^ swz(R) of source row
+// src_row(R). PERM applies the 32-row permutation of the MFMA output order.
+template <int D, bool PERM>
+struct TileDma {
+  static constexpr int kRows = 64;
+  static constexpr int kRowsPerInst = 64 / SwzTile<D>::kChunks;
+  static constexpr int kInsts = kRows / kRowsPerInst;  // per tile, all waves
+  static constexpr int kPerWave = kInsts / 4;
+  uint32_t voff[kPerWave];
+
+  __device__ __forceinline__ explicit TileDma(int d) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) {
+      const int inst = wave + 4 * i;
+      const int R = inst * kRowsPerInst + lane / SwzTile<D>::kChunks;
+      const int c = lane % SwzTile<D>::kChunks;
+      const int col = (c ^ SwzTile<D>::swz(R)) * 8;
+      const int src = PERM ? perm_src(R) : R;
+      voff[i] = col < d ? (uint32_t)((src * d + col) * 2) : 0x80000000u;
+    }
+  }
+
+  // Rows [r0, r0 + 64) of `base`; rows past nrows read as zeros.
+  __device__ __forceinline__ void issue(const bf16* base, int r0, int nrows, int d, char* lds) const {
+    const int wave = threadIdx.x >> 6;
+    const int rows_left = nrows - r0 > 0 ? nrows - r0 : 0;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(base) + (int64_t)r0 * d, (short)0, rows_left * d * 2, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) {
+      char* dst = lds + (wave + 4 * i) * 1024;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc, reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(dst)), 16,
+          (int)voff[i], 0, 0, 0);
+    }
+  }
+};
+
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int D>
+struct FwdDma {
+  static constexpr int BQ = 128, BK = 64, NT = 2, KS = D / 16, DT = D / 32;
+  static constexpr int kTileBytes = BK * D * 2;
+  static constexpr int kStageBytes = 2 * kTileBytes;  // K then V
+  static constexpr int kLds = 2 * kStageBytes;
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_dma_kernel(const bf16* __restrict__ q,
+                                                                  const bf16* __restrict__ k,
+                                                                  const bf16* __restrict__ v, bf16* __restrict__ o,
+                                                                  float* __restrict__ lse, int bh_count, int Sq,
+                                                                  int Sk, int d, int causal, float scale_log2,
+                                                                  int neg_q, int n_qtiles) {
+  typedef FwdDma<D> F;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int bh = blockIdx.x % bh_count;
+  const int qt = n_qtiles - 1 - (int)(blockIdx.x / bh_count);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int q0 = qt * F::BQ;
+  const int q0w = q0 + wave * 32;
+  const int qrow = q0w + l32;
+
+  const bf16* qb = q + (int64_t)bh * Sq * d;
+  const bf16* kb = k + (int64_t)bh * Sk * d;
+  const bf16* vb = v + (int64_t)bh * Sk * d;
+
+  const int q_last = min(q0 + F::BQ, Sq) - 1;
+  const int n_tiles = causal ? min(q_last, Sk - 1) / F::BK + 1 : (Sk + F::BK - 1) / F::BK;
+  const bool wave_active = q0w < Sq;
+  const int wave_tiles = !wave_active ? 0 : causal ? min(q0w + 31, Sq - 1) / F::BK + 1 : n_tiles;
+
+  TileDma<D, true> kdma(d);
+  TileDma<D, false> vdma(d);
+  kdma.issue(kb, 0, Sk, d, smem);
+  vdma.issue(vb, 0, Sk, d, smem + F::kTileBytes);
+
+  bf16x8 qf[F::KS];
+  if (neg_q)
+    load_row_frags<bf16, D, true, true>(qf, qb, q0w, Sq, d);
+  else
+    load_row_frags<bf16, D, true, false>(qf, qb, q0w, Sq, d);
+
+  f32x16 acc[F::DT];
+#pragma unroll
+  for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[u][r] = 0.f;
+  float m = -INFINITY;
+  float lsum[4] = {0.f, 0.f, 0.f, 0.f};
+
+  for (int j = 0; j < n_tiles; ++j) {
+    wait_dma();
+    __syncthreads();
+    const char* kl = smem + (j & 1) * F::kStageBytes;
+    const char* vl = kl + F::kTileBytes;
+    if (j + 1 < n_tiles) {
+      char* nxt = smem + ((j + 1) & 1) * F::kStageBytes;
+      kdma.issue(kb, (j + 1) * F::BK, Sk, d, nxt);
+      vdma.issue(vb, (j + 1) * F::BK, Sk, d, nxt + F::kTileBytes);
+    }
+    if (j >= wave_tiles) continue;
+
+    const int kv0 = j * F::BK;
+    f32x16 s[F::NT];
+#pragma unroll
+    for (int t = 0; t < F::NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+    lds_mfma_pipeline<F::KS * F::NT>(
+        [&](int i) { return SwzTile<D>::frag(kl, (i % F::NT) * 32 + l32, (i / F::NT) * 16 + g * 8); },
+        [&](int i, const bf16x8& a) { mma32(a, qf[i / F::NT], s[i % F::NT]); });
+
+    if ((causal && kv0 + F::BK - 1 > q0w) || kv0 + F::BK > Sk) {
+      const int lim = causal ? min(qrow, Sk - 1) : Sk - 1;
+#pragma unroll
+      for (int t = 0; t < F::NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[t][r] = (kv0 + t * 32 + g * 16 + r > lim) ? -INFINITY : s[t][r];
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < F::NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+    mx = lane32_max(mx) * scale_log2;
+    if (__any(mx > m + kRescaleThreshold)) {
+      const float m_new = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lsum[i] *= alpha;
+#pragma unroll
+      for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[u][r] *= alpha;
+      m = m_new;
+    }
+    const float neg_m = -m;
+    bf16x8 pf[F::NT][2];
+#pragma unroll
+    for (int t = 0; t < F::NT; ++t) {
+      float p[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][r], scale_log2, neg_m));
+        lsum[r & 3] += p[r];
+      }
+      to_frag(p, pf[t][0]);
+      to_frag(p + 8, pf[t][1]);
+    }
+    // O^T += V^T P^T. Product i uses key chunk c = i / DT (subtile c/2, half
+    // c%2) and output tile u = i % DT.
+#pragma unroll
+    for (int i = 0; i < F::DT * F::NT * 2; ++i) {
+      const int c = i / F::DT, u = i % F::DT;
+      mma32(vt_frag<D>(vl, (c >> 1) * 32 + (c & 1) * 8, u * 32), pf[c >> 1][c & 1], acc[u]);
+    }
+  }
+
+  if (!wave_active) return;
+  const float l = lane32_sum((lsum[0] + lsum[1]) + (lsum[2] + lsum[3]));
+  store_acc_rows<bf16, D, true>(acc, o + (int64_t)bh * Sq * d, qrow, Sq, d, 1.0f / l);
+  if (g == 0 && qrow < Sq) lse[(int64_t)bh * Sq + qrow] = (m + __builtin_amdgcn_logf(l)) * kLn2;
+}
+
+// ===========================================================================
 // delta = rowsum(f32 dO * f32 O)
 // ===========================================================================
 template <typename T>
@@ -815,6 +1045,21 @@ int check_shape(const char* name, const Shape& s, int dtype, int causal, bool bw
 
 int pad_dim(int64_t d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
 
+template <int D>
+int fwd_dma_launch(const void* q, const void* k, const void* v, void* o, float* lse, const Shape& s, int causal,
+                   float c, int neg_q, hipStream_t stream) {
+  typedef FwdDma<D> F;
+  const int64_t nq = cdiv(s.sq, F::BQ);
+  const int64_t bh = s.b * s.h;
+  if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: grid too large");
+  auto kern = attn_fwd_dma_kernel<D>;
+  set_lds(kern, F::kLds);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(kThreads), F::kLds, stream, static_cast<const bf16*>(q),
+                     static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<bf16*>(o), lse, (int)bh,
+                     (int)s.sq, (int)s.sk, (int)s.d, causal, c, neg_q, (int)nq);
+  return check_launch("ferrite_flash_attention_fwd");
+}
+
 template <typename T, int D, bool AL>
 int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse, const Shape& s, int causal,
                float scale, hipStream_t stream) {
@@ -830,6 +1075,7 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
   float c = scale * kLog2e;
   const int neg_q = c < 0.f;
   c = fmaxf(fabsf(c), 1e-30f);
+  if constexpr (sizeof(T) == 2 && AL && D <= 128) return fwd_dma_launch<D>(q, k, v, o, lse, s, causal, c, neg_q, stream);
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(kThreads), F::kLds, stream, static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v), static_cast<T*>(o), lse, (int)bh, (int)s.sq,
                      (int)s.sk, (int)s.d, causal, c, neg_q, (int)nq);
