@@ -467,125 +467,229 @@ __global__ __launch_bounds__(kThreads, (Fwd<T, D, ALIGNED>::kMinBlocks)) void at
 }
 
 // ===========================================================================
-// Forward, bf16 with D in {64, 128}: K and V staged by LDS DMA
+// Forward, bf16 with D in {64, 128}: ping-pong schedule over LDS DMA
 // ===========================================================================
-// Same decomposition as attn_fwd_kernel (4 waves x 32 query rows, 64-key
-// tiles, double-buffered LDS), but the K and V tiles reach LDS through
-// buffer_load ... lds (gfx950 direct-to-LDS loads): no staging registers, no
-// LDS writes, and rows past the end or padded columns arrive as zeros from the
-// buffer range check. Both tiles are plain row-major with 16-byte chunks
-// XOR-swizzled per row; V^T fragments come from ds_read_b64_tr_b16, which
-// transposes 4x4 blocks of 16-bit elements across each 16-lane group.
+// 8 waves and 256 query rows per workgroup, 32 rows per wave. Waves w and
+// w + 4 run on the same SIMD and belong to opposite groups. Each tile step
+// has two phases separated by a workgroup barrier; in every phase one group
+// issues its matrix products (S^T = K Q^T for tile t and O^T += V^T P^T for
+// tile t - 1) while the other runs the softmax of its scores, so each SIMD's
+// MFMA pipe is fed by one wave while the other one works on the VALU.
+//
+// K and V tiles of 64 keys reach LDS through buffer_load ... lds (one 1 KB
+// block per instruction, no staging registers) in three-slot rings, K two
+// steps and V one step ahead of use. Rows past the end of the keys read as
+// zeros from the buffer range check.
+
+// K tile for the A operand of S^T = K Q^T: 16-byte reads in which lane
+// (l32, g) takes physical row 32t + l32, 16-byte chunk 2kc + g. Row r sits in
+// 1 KB block r % kBlocks at position r / kBlocks. The 16-byte gap between
+// blocks puts the 16 rows of each 16-lane quarter in 16 different bank
+// groups, and the address of (32t + l32, chunk) is a per-lane base plus a
+// constant, so the reads need no address arithmetic.
 template <int D>
-struct SwzTile {
-  static constexpr int kRowBytes = D * 2;
-  static constexpr int kChunks = kRowBytes / 16;       // 16-byte chunks per row
-  static constexpr int kRowsPer256 = 256 / kRowBytes;  // rows sharing one pass of the 64 banks
-  // Chunk swizzle: an odd multiplier makes it a bijection over any kChunks
-  // consecutive rows (conflict-free 16-byte fragment reads down 16 rows), and
-  // 5 also separates the 4-row x 4-chunk footprint of a transposed read.
-  static __device__ __forceinline__ int swz(int r) { return (5 * (r / kRowsPer256)) & (kChunks - 1); }
-  static __device__ __forceinline__ int off(int r, int col) {
-    return r * kRowBytes + (((col >> 3) ^ swz(r)) << 4) + (col & 7) * 2;
+struct PpKTile {
+  static constexpr int kRowBytes = 2 * D;
+  static constexpr int kChunks = kRowBytes / 16;
+  static constexpr int kBlocks = 64 * kRowBytes / 1024;  // 16 (D = 128) or 8 (D = 64)
+  static constexpr int kStride = 1024 + 16;
+  static constexpr int kBytes = kBlocks * kStride;
+  static __host__ __device__ constexpr int off(int r, int byte) {
+    return (r % kBlocks) * kStride + (r / kBlocks) * kRowBytes + byte;
   }
-  static __device__ __forceinline__ bf16x8 frag(const char* base, int r, int col) {
-    return *reinterpret_cast<const bf16x8*>(base + off(r, col));
+  // Row that lane L of the instruction filling block b loads.
+  static __device__ __forceinline__ int dma_row(int b, int L) { return b + (L / kChunks) * kBlocks; }
+};
+
+// V tile for V^T fragments read with ds_read_b64_tr_b16, in which lanes 0-31
+// take 64 bytes from each of rows r..r+3 (r % 4 == 0). Row r sits in block
+// (r % 4) + 4 * (r / (4 * kRowsPerBlock)) at position (r / 4) % kRowsPerBlock:
+// the 64-byte gap between blocks puts those four rows in the four 64-byte
+// bank groups, and addresses again split into a lane base plus a constant.
+template <int D>
+struct PpVTile {
+  static constexpr int kRowBytes = 2 * D;
+  static constexpr int kChunks = kRowBytes / 16;
+  static constexpr int kRowsPerBlock = 1024 / kRowBytes;  // 4 or 8
+  static constexpr int kBlocks = 64 / kRowsPerBlock;
+  static constexpr int kStride = 1024 + 64;
+  static constexpr int kBytes = kBlocks * kStride;
+  static __host__ __device__ constexpr int off(int r, int byte) {
+    return ((r & 3) + 4 * (r / (4 * kRowsPerBlock))) * kStride + ((r >> 2) % kRowsPerBlock) * kRowBytes + byte;
+  }
+  static __device__ __forceinline__ int dma_row(int b, int L) {
+    return (b & 3) + 4 * (L / kChunks) + 4 * kRowsPerBlock * (b >> 2);
+  }
+};
+
+// One wave's share of the DMA of a 64-row bf16 tile with d == D: the four
+// waves of a group split the blocks, wave gw of the group taking blocks
+// gw + 4i. PERM loads physical row r from logical row perm_src(r).
+template <class Layout, bool PERM>
+struct PpDma {
+  static constexpr int kPerWave = Layout::kBlocks / 4;
+  uint32_t voff[kPerWave];
+  int gw;
+
+  __device__ __forceinline__ PpDma(int gw_, int d) : gw(gw_) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) {
+      const int r = Layout::dma_row(gw + 4 * i, lane);
+      const int src = PERM ? perm_src(r) : r;
+      voff[i] = (uint32_t)((src * d + (lane % Layout::kChunks) * 8) * 2);
+    }
+  }
+
+  // Rows [r0, r0 + 64) of `base` into the tile at `lds`; rows at or past
+  // nrows arrive as zeros. Issued as inline assembly so that the compiler's
+  // wait insertion does not tie every later LDS read to these loads; the
+  // kernel orders them itself with explicit vmcnt waits and barriers.
+  __device__ __forceinline__ void issue(const bf16* base, int r0, int nrows, int d, char* lds) const {
+    const int rows_left = nrows - r0 > 0 ? nrows - r0 : 0;
+    // Every operand is wave-uniform; readfirstlane keeps them in SGPRs.
+    const uint64_t addr = reinterpret_cast<uint64_t>(base + (int64_t)r0 * d);
+    const u32x4 rsrc = {(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
+                        (uint32_t)__builtin_amdgcn_readfirstlane((int)((addr >> 32) & 0xffffu)),
+                        (uint32_t)__builtin_amdgcn_readfirstlane(rows_left * d * 2), 0x00020000u};
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) {
+      const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane(
+          (int)(uint32_t)reinterpret_cast<uintptr_t>(lds + (gw + 4 * i) * Layout::kStride));
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff[i]),
+                   "s"(rsrc)
+                   : "memory", "m0");
+    }
   }
 };
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
-// A-operand fragment of V^T (32 d x 16 keys) from a row-major V tile: lane
-// (l32, g) gets V[kv0 + g*16 + e][dcol0 + l32] for e = 0..7, as two transposed
-// 8-byte reads (e = 0..3 and 4..7). Within each 16-lane group, slot s = lane %
-// 16 supplies the address of keys kv0 + g*16 + half*4 + s/4, columns
-// dcol0 + 16*((lane/16) % 2) + 4*(s % 4); the instruction hands lane 4a + b of
-// the group element b of the pieces supplied by slots a, a+4, a+8, a+12.
-template <int D>
-__device__ __forceinline__ bf16x8 vt_frag(const char* vl, int kv0, int dcol0) {
-  const int lane = threadIdx.x & 63;
-  const int s = lane & 15;
-  const int row = kv0 + (lane >> 5) * 16 + (s >> 2);
-  const int col = dcol0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+// Two transposed 8-byte reads at `p` and `p + hi_off`, joined into one
+// 8-element A fragment. Within each 16-lane group the instruction hands lane
+// 4a + b element b of the 4-element pieces addressed by lanes a, a+4, a+8, a+12.
+__device__ __forceinline__ bf16x8 tr_frag(const char* p, int hi_off) {
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-  const lds_i16x4* p0 = reinterpret_cast<const lds_i16x4*>(
-      reinterpret_cast<uintptr_t>(vl + SwzTile<D>::off(row, col)));
-  const lds_i16x4* p1 = reinterpret_cast<const lds_i16x4*>(
-      reinterpret_cast<uintptr_t>(vl + SwzTile<D>::off(row + 4, col)));
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p0));
-  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_i16x4*>(p1));
+  lds_i16x4* p0 = reinterpret_cast<lds_i16x4*>(reinterpret_cast<uintptr_t>(p));
+  lds_i16x4* p1 = reinterpret_cast<lds_i16x4*>(reinterpret_cast<uintptr_t>(p + hi_off));
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p0);
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p1);
   typedef short i16x8 __attribute__((ext_vector_type(8)));
   const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return __builtin_bit_cast(bf16x8, v);
 }
 
-// DMA of one 64-row tile of a [nrows, d] bf16 matrix into a swizzled LDS tile.
-// Each wave instruction fills 1 KB of LDS (64 lanes x 16 bytes, lane order);
-// lane (row R, physical chunk c) loads logical chunk c ^ swz(R) of source row
-// src_row(R). PERM applies the 32-row permutation of the MFMA output order.
-template <int D, bool PERM>
-struct TileDma {
-  static constexpr int kRows = 64;
-  static constexpr int kRowsPerInst = 64 / SwzTile<D>::kChunks;
-  static constexpr int kInsts = kRows / kRowsPerInst;  // per tile, all waves
-  static constexpr int kPerWave = kInsts / 4;
-  uint32_t voff[kPerWave];
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
-  __device__ __forceinline__ explicit TileDma(int d) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int i = 0; i < kPerWave; ++i) {
-      const int inst = wave + 4 * i;
-      const int R = inst * kRowsPerInst + lane / SwzTile<D>::kChunks;
-      const int c = lane % SwzTile<D>::kChunks;
-      const int col = (c ^ SwzTile<D>::swz(R)) * 8;
-      const int src = PERM ? perm_src(R) : R;
-      voff[i] = col < d ? (uint32_t)((src * d + col) * 2) : 0x80000000u;
-    }
-  }
-
-  // Rows [r0, r0 + 64) of `base`; rows past nrows read as zeros.
-  __device__ __forceinline__ void issue(const bf16* base, int r0, int nrows, int d, char* lds) const {
-    const int wave = threadIdx.x >> 6;
-    const int rows_left = nrows - r0 > 0 ? nrows - r0 : 0;
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<bf16*>(base) + (int64_t)r0 * d, (short)0, rows_left * d * 2, 0x00020000);
-#pragma unroll
-    for (int i = 0; i < kPerWave; ++i) {
-      char* dst = lds + (wave + 4 * i) * 1024;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rsrc, reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(dst)), 16,
-          (int)voff[i], 0, 0, 0);
-    }
-  }
-};
-
-__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Workgroup barrier that leaves outstanding global loads (the DMA ring) alone
+// and that the scheduler may not move any instruction across.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
 
 template <int D>
-struct FwdDma {
-  static constexpr int BQ = 128, BK = 64, NT = 2, KS = D / 16, DT = D / 32;
-  static constexpr int kTileBytes = BK * D * 2;
-  static constexpr int kStageBytes = 2 * kTileBytes;  // K then V
-  static constexpr int kLds = 2 * kStageBytes;
+struct FwdPp {
+  static constexpr int kWaves = 8, kThreads = 64 * kWaves;
+  static constexpr int BQ = 32 * kWaves, BK = 64, NT = 2, KS = D / 16, DT = D / 32;
+  typedef PpKTile<D> KT;
+  typedef PpVTile<D> VT;
+  static constexpr int kSlots = 3;
+  static constexpr int kLds = kSlots * (KT::kBytes + VT::kBytes);
+  static constexpr int kDma = KT::kBlocks / 4;  // DMA instructions per tile for each wave of the loading group
+  static_assert(KT::kBlocks == VT::kBlocks, "K and V tiles take the same number of DMA blocks");
 };
 
+// The matrix phase: S^T = K_t Q^T into s (QK) and O^T += V_{t-1}^T P^T (PV).
+// kp / vp are the lane's base addresses inside the K and V slots. Reads run
+// kPpAhead products ahead of the MFMAs: four matrix waves share the LDS, so
+// its latency is longer than in a lone wave.
+constexpr int kPpAhead = 8;
+
+template <int D, bool QK, bool PV>
+__device__ __forceinline__ void pp_gemm(const char* kp, const char* vp, const bf16x8 (&qf)[D / 16],
+                                        const bf16x8 (&pf)[2][2], f32x16 (&s)[2], f32x16 (&acc)[D / 32]) {
+  typedef FwdPp<D> F;
+  typedef typename F::KT KT;
+  typedef typename F::VT VT;
+  constexpr int NQ = QK ? F::KS * F::NT : 0;
+  constexpr int NP = PV ? F::DT * 4 : 0;
+  constexpr int N = NQ + NP;
+  if constexpr (QK) {
+#pragma unroll
+    for (int t = 0; t < F::NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+  }
+  // Product i < NQ: subtile i % NT, k-chunk i / NT. Product NQ + j: key chunk
+  // c = j / DT (subtile c / 2, half c % 2), output tile u = j % DT.
+  auto read = [&](int i) -> bf16x8 {
+    if (i < NQ) {
+      return *reinterpret_cast<const bf16x8*>(kp + KT::off(32 * (i % F::NT), (i / F::NT) * 32));
+    } else {
+      const int j = i - NQ, c = j / F::DT, u = j % F::DT;
+      return tr_frag(vp + VT::off((c >> 1) * 32 + (c & 1) * 8, u * 64), VT::off(4, 0));
+    }
+  };
+  bf16x8 buf[N];
+#pragma unroll
+  for (int i = 0; i < kPpAhead && i < N; ++i) buf[i] = read(i);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if (i + kPpAhead < N) buf[i + kPpAhead] = read(i + kPpAhead);
+    if (i < NQ) {
+      mma32(buf[i], qf[i / F::NT], s[i % F::NT]);
+    } else {
+      const int j = i - NQ, c = j / F::DT;
+      mma32(buf[i], pf[c >> 1][c & 1], acc[j % F::DT]);
+    }
+  }
+  // One MFMA, then the LDS reads of the product kPpAhead further on (one for
+  // a K fragment, two for a V^T fragment).
+  auto reads = [](int i) {
+    if (i < NQ)
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    else
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+  };
+#pragma unroll
+  for (int i = 0; i < kPpAhead && i < N; ++i) reads(i);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (i + kPpAhead < N) reads(i + kPpAhead);
+  }
+}
+
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_dma_kernel(const bf16* __restrict__ q,
-                                                                  const bf16* __restrict__ k,
-                                                                  const bf16* __restrict__ v, bf16* __restrict__ o,
-                                                                  float* __restrict__ lse, int bh_count, int Sq,
-                                                                  int Sk, int d, int causal, float scale_log2,
-                                                                  int neg_q, int n_qtiles) {
-  typedef FwdDma<D> F;
+__global__ __launch_bounds__(512, 2) void attn_fwd_pp_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                             const bf16* __restrict__ v, bf16* __restrict__ o,
+                                                             float* __restrict__ lse, int bh_count, int Sq, int Sk,
+                                                             int d, int causal, float scale_log2, int neg_q,
+                                                             int n_qtiles) {
+  typedef FwdPp<D> F;
+  typedef typename F::KT KT;
+  typedef typename F::VT VT;
   extern __shared__ __attribute__((aligned(16))) char smem[];
+  char* const kring = smem;
+  char* const vring = smem + F::kSlots * KT::kBytes;
 
+  // Heaviest (last) query tiles first; all tiles of one head share an XCD
+  // when bh_count is a multiple of 8.
   const int bh = blockIdx.x % bh_count;
   const int qt = n_qtiles - 1 - (int)(blockIdx.x / bh_count);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
+  const int group = wave >> 2;
+  // SIMD w % 4 holds row blocks 2 (w % 4) and 2 (w % 4) + 1, one per group,
+  // so both groups see the same share of the causal diagonal.
   const int q0 = qt * F::BQ;
-  const int q0w = q0 + wave * 32;
+  const int q0w = q0 + 32 * (2 * (wave & 3) + group);
   const int qrow = q0w + l32;
 
   const bf16* qb = q + (int64_t)bh * Sq * d;
@@ -593,14 +697,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_dma_kernel(const bf16* _
   const bf16* vb = v + (int64_t)bh * Sk * d;
 
   const int q_last = min(q0 + F::BQ, Sq) - 1;
-  const int n_tiles = causal ? min(q_last, Sk - 1) / F::BK + 1 : (Sk + F::BK - 1) / F::BK;
+  const int n = causal ? min(q_last, Sk - 1) / F::BK + 1 : (Sk + F::BK - 1) / F::BK;
   const bool wave_active = q0w < Sq;
-  const int wave_tiles = !wave_active ? 0 : causal ? min(q0w + 31, Sq - 1) / F::BK + 1 : n_tiles;
+  const int n_w = !wave_active ? 0 : causal ? min(min(q0w + 31, Sq - 1), Sk - 1) / F::BK + 1 : n;
 
-  TileDma<D, true> kdma(d);
-  TileDma<D, false> vdma(d);
-  kdma.issue(kb, 0, Sk, d, smem);
-  vdma.issue(vb, 0, Sk, d, smem + F::kTileBytes);
+  // Group 1 loads the K tiles and group 0 the V tiles, each at the start of
+  // its softmax phase, so that a wave about to run its matrix products never
+  // waits behind the DMA issue.
+  const PpDma<KT, true> kdma(wave & 3, d);
+  const PpDma<VT, false> vdma(wave & 3, d);
 
   bf16x8 qf[F::KS];
   if (neg_q)
@@ -608,48 +713,46 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_dma_kernel(const bf16* _
   else
     load_row_frags<bf16, D, true, false>(qf, qb, q0w, Sq, d);
 
+  // Ring prologue: K_0 and K_1 into K slots 0 and 1, V_0 into V slot 0.
+  if (group == 1) {
+    kdma.issue(kb, 0, Sk, d, kring);
+    if (1 < n) kdma.issue(kb, F::BK, Sk, d, kring + KT::kBytes);
+  } else {
+    vdma.issue(vb, 0, Sk, d, vring);
+  }
+
+  // Lane bases inside a K / V slot.
+  const int kbase = KT::off(l32, g * 16);
+  const int vbase = VT::off((lane >> 5) * 16 + ((lane & 15) >> 2), 2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
+
   f32x16 acc[F::DT];
 #pragma unroll
   for (int u = 0; u < F::DT; ++u)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[u][r] = 0.f;
+  f32x16 s[F::NT];
+  bf16x8 pf[F::NT][2];
   float m = -INFINITY;
   float lsum[4] = {0.f, 0.f, 0.f, 0.f};
 
-  for (int j = 0; j < n_tiles; ++j) {
-    wait_dma();
-    __syncthreads();
-    const char* kl = smem + (j & 1) * F::kStageBytes;
-    const char* vl = kl + F::kTileBytes;
-    if (j + 1 < n_tiles) {
-      char* nxt = smem + ((j + 1) & 1) * F::kStageBytes;
-      kdma.issue(kb, (j + 1) * F::BK, Sk, d, nxt);
-      vdma.issue(vb, (j + 1) * F::BK, Sk, d, nxt + F::kTileBytes);
-    }
-    if (j >= wave_tiles) continue;
+  auto kslot = [&](int t) { return kring + (t % F::kSlots) * KT::kBytes + kbase; };
+  auto vslot = [&](int t) { return vring + (t % F::kSlots) * VT::kBytes + vbase; };
 
-    const int kv0 = j * F::BK;
-    f32x16 s[F::NT];
-#pragma unroll
-    for (int t = 0; t < F::NT; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
-    lds_mfma_pipeline<F::KS * F::NT>(
-        [&](int i) { return SwzTile<D>::frag(kl, (i % F::NT) * 32 + l32, (i / F::NT) * 16 + g * 8); },
-        [&](int i, const bf16x8& a) { mma32(a, qf[i / F::NT], s[i % F::NT]); });
-
+  auto softmax = [&](int t) {
+    const int kv0 = t * F::BK;
+    // Mask on the raw scores (diagonal and ragged tiles only), then the row max.
     if ((causal && kv0 + F::BK - 1 > q0w) || kv0 + F::BK > Sk) {
       const int lim = causal ? min(qrow, Sk - 1) : Sk - 1;
 #pragma unroll
-      for (int t = 0; t < F::NT; ++t)
+      for (int u = 0; u < F::NT; ++u)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[t][r] = (kv0 + t * 32 + g * 16 + r > lim) ? -INFINITY : s[t][r];
+        for (int r = 0; r < 16; ++r) s[u][r] = (kv0 + u * 32 + g * 16 + r > lim) ? -INFINITY : s[u][r];
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < F::NT; ++t)
+    for (int u = 0; u < F::NT; ++u)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[u][r]);
     mx = lane32_max(mx) * scale_log2;
     if (__any(mx > m + kRescaleThreshold)) {
       const float m_new = fmaxf(m, mx);
@@ -663,25 +766,85 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_dma_kernel(const bf16* _
       m = m_new;
     }
     const float neg_m = -m;
-    bf16x8 pf[F::NT][2];
 #pragma unroll
-    for (int t = 0; t < F::NT; ++t) {
+    for (int u = 0; u < F::NT; ++u) {
       float p[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][r], scale_log2, neg_m));
+        p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][r], scale_log2, neg_m));
         lsum[r & 3] += p[r];
       }
-      to_frag(p, pf[t][0]);
-      to_frag(p + 8, pf[t][1]);
+      to_frag(p, pf[u][0]);
+      to_frag(p + 8, pf[u][1]);
     }
-    // O^T += V^T P^T. Product i uses key chunk c = i / DT (subtile c/2, half
-    // c%2) and output tile u = i % DT.
-#pragma unroll
-    for (int i = 0; i < F::DT * F::NT * 2; ++i) {
-      const int c = i / F::DT, u = i % F::DT;
-      mma32(vt_frag<D>(vl, (c >> 1) * 32 + (c & 1) * 8, u * 32), pf[c >> 1][c & 1], acc[u]);
+  };
+
+  // Step st has two phases, each opened by a workgroup barrier. Group 0 runs
+  // the products of tile st (and PV of st - 1) in the first phase and the
+  // softmax of tile st in the second; group 1 runs the softmax of st - 1 in
+  // the first and the products of st in the second. K_{st+2} goes out from
+  // group 1 after the first barrier of step st and V_{st+1} from group 0
+  // after the second, once every wave has left the slots they overwrite.
+  // Both groups pass 2 (n + 1) barriers.
+  auto open_step = [&](int st) {
+    // The loads of K_st (group 1, issued in step st - 2) and V_{st-1}
+    // (group 0, step st - 2) are complete; the group's loads from step
+    // st - 1 may still be in flight.
+    if (group == 1 ? st + 1 < n : st < n)
+      wait_vmem<F::kDma>();
+    else
+      wait_vmem<0>();
+    lds_barrier();
+    if (group == 1 && st + 2 < n) kdma.issue(kb, (st + 2) * F::BK, Sk, d, kring + ((st + 2) % F::kSlots) * KT::kBytes);
+  };
+  auto mid_step = [&](int st) {
+    lds_barrier();
+    if (group == 0 && st + 1 < n) vdma.issue(vb, (st + 1) * F::BK, Sk, d, vring + ((st + 1) % F::kSlots) * VT::kBytes);
+  };
+  // The wave in its matrix phase takes issue priority over the one in its
+  // softmax, which fills the remaining VALU cycles; without it the older wave
+  // of the pair wins every tie and starves the other's MFMAs.
+  auto gemm_phase = [&](auto&& body) {
+    __builtin_amdgcn_s_setprio(1);
+    body();
+    __builtin_amdgcn_s_setprio(0);
+  };
+  int st = 0;
+  if (n_w > 0) {
+    if (group == 0) {
+      open_step(0);
+      gemm_phase([&] { pp_gemm<D, true, false>(kslot(0), vslot(0), qf, pf, s, acc); });
+      mid_step(0);
+      softmax(0);
+      for (st = 1; st < n_w; ++st) {
+        open_step(st);
+        gemm_phase([&] { pp_gemm<D, true, true>(kslot(st), vslot(st - 1), qf, pf, s, acc); });
+        mid_step(st);
+        softmax(st);
+      }
+      open_step(n_w);
+      gemm_phase([&] { pp_gemm<D, false, true>(kslot(n_w), vslot(n_w - 1), qf, pf, s, acc); });
+      mid_step(n_w);
+    } else {
+      open_step(0);
+      mid_step(0);
+      gemm_phase([&] { pp_gemm<D, true, false>(kslot(0), vslot(0), qf, pf, s, acc); });
+      for (st = 1; st < n_w; ++st) {
+        open_step(st);
+        softmax(st - 1);
+        mid_step(st);
+        gemm_phase([&] { pp_gemm<D, true, true>(kslot(st), vslot(st - 1), qf, pf, s, acc); });
+      }
+      open_step(n_w);
+      softmax(n_w - 1);
+      mid_step(n_w);
+      gemm_phase([&] { pp_gemm<D, false, true>(kslot(n_w), vslot(n_w - 1), qf, pf, s, acc); });
     }
+    st = n_w + 1;
+  }
+  for (; st <= n; ++st) {
+    open_step(st);
+    mid_step(st);
   }
 
   if (!wave_active) return;
@@ -1046,15 +1209,15 @@ int check_shape(const char* name, const Shape& s, int dtype, int causal, bool bw
 int pad_dim(int64_t d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
 
 template <int D>
-int fwd_dma_launch(const void* q, const void* k, const void* v, void* o, float* lse, const Shape& s, int causal,
-                   float c, int neg_q, hipStream_t stream) {
-  typedef FwdDma<D> F;
+int fwd_pp_launch(const void* q, const void* k, const void* v, void* o, float* lse, const Shape& s, int causal,
+                  float c, int neg_q, hipStream_t stream) {
+  typedef FwdPp<D> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: grid too large");
-  auto kern = attn_fwd_dma_kernel<D>;
+  auto kern = attn_fwd_pp_kernel<D>;
   set_lds(kern, F::kLds);
-  hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(kThreads), F::kLds, stream, static_cast<const bf16*>(q),
+  hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<bf16*>(o), lse, (int)bh,
                      (int)s.sq, (int)s.sk, (int)s.d, causal, c, neg_q, (int)nq);
   return check_launch("ferrite_flash_attention_fwd");
@@ -1075,7 +1238,7 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
   float c = scale * kLog2e;
   const int neg_q = c < 0.f;
   c = fmaxf(fabsf(c), 1e-30f);
-  if constexpr (sizeof(T) == 2 && AL && D <= 128) return fwd_dma_launch<D>(q, k, v, o, lse, s, causal, c, neg_q, stream);
+  if constexpr (sizeof(T) == 2 && AL && D <= 128) return fwd_pp_launch<D>(q, k, v, o, lse, s, causal, c, neg_q, stream);
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(kThreads), F::kLds, stream, static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v), static_cast<T*>(o), lse, (int)bh, (int)s.sq,
                      (int)s.sk, (int)s.d, causal, c, neg_q, (int)nq);
