@@ -32,6 +32,7 @@
 //    tile.
 //  * lse and delta are compact f32 [B, H, S].
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 
@@ -497,6 +498,7 @@ struct PpKTile {
   static __host__ __device__ constexpr int off(int r, int byte) {
     return (r % kBlocks) * kStride + (r / kBlocks) * kRowBytes + byte;
   }
+  static __host__ __device__ constexpr int block_off(int b) { return b * kStride; }
   // Row that lane L of the instruction filling block b loads.
   static __device__ __forceinline__ int dma_row(int b, int L) { return b + (L / kChunks) * kBlocks; }
 };
@@ -517,14 +519,15 @@ struct PpVTile {
   static __host__ __device__ constexpr int off(int r, int byte) {
     return ((r & 3) + 4 * (r / (4 * kRowsPerBlock))) * kStride + ((r >> 2) % kRowsPerBlock) * kRowBytes + byte;
   }
+  static __host__ __device__ constexpr int block_off(int b) { return b * kStride; }
   static __device__ __forceinline__ int dma_row(int b, int L) {
     return (b & 3) + 4 * (L / kChunks) + 4 * kRowsPerBlock * (b >> 2);
   }
 };
 
-// One wave's share of the DMA of a 64-row bf16 tile with d == D: the four
-// waves of a group split the blocks, wave gw of the group taking blocks
-// gw + 4i. PERM loads physical row r from logical row perm_src(r).
+// One wave's share of the DMA of a 64-row bf16 tile with d == D: four waves
+// split the blocks, wave gw taking blocks gw + 4i. PERM loads physical row r
+// from logical row perm_src(r).
 template <class Layout, bool PERM>
 struct PpDma {
   static constexpr int kPerWave = Layout::kBlocks / 4;
@@ -541,6 +544,22 @@ struct PpDma {
     }
   }
 
+  // Buffer descriptor of rows [r0, nrows) of `base` (rows past nrows read as zeros).
+  static __device__ __forceinline__ u32x4 rsrc_of(const bf16* base, int r0, int nrows, int d) {
+    const int rows_left = nrows - r0 > 0 ? nrows - r0 : 0;
+    const uint64_t addr = reinterpret_cast<uint64_t>(base + (int64_t)r0 * d);
+    return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
+                 (uint32_t)__builtin_amdgcn_readfirstlane((int)((addr >> 32) & 0xffffu)),
+                 (uint32_t)__builtin_amdgcn_readfirstlane(rows_left * d * 2), 0x00020000u};
+  }
+  // The i-th of this wave's instructions for the tile at `lds`.
+  __device__ __forceinline__ void issue_one(const u32x4& rsrc, char* lds, int i) const {
+    const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(uint32_t)reinterpret_cast<uintptr_t>(lds + Layout::block_off(gw + 4 * i)));
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff[i]), "s"(rsrc)
+                 : "memory", "m0");
+  }
+
   // Rows [r0, r0 + 64) of `base` into the tile at `lds`; rows at or past
   // nrows arrive as zeros. Issued as inline assembly so that the compiler's
   // wait insertion does not tie every later LDS read to these loads; the
@@ -555,7 +574,7 @@ struct PpDma {
 #pragma unroll
     for (int i = 0; i < kPerWave; ++i) {
       const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane(
-          (int)(uint32_t)reinterpret_cast<uintptr_t>(lds + (gw + 4 * i) * Layout::kStride));
+          (int)(uint32_t)reinterpret_cast<uintptr_t>(lds + Layout::block_off(gw + 4 * i)));
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff[i]),
                    "s"(rsrc)
                    : "memory", "m0");
@@ -1171,6 +1190,243 @@ __global__ __launch_bounds__(kThreads, 1) void attn_dkv_kernel(const T* __restri
 }
 
 // ===========================================================================
+// Backward, bf16 with D = 128: streamed tiles read as rows and transposed
+// ===========================================================================
+// The backward kernels read each streamed 64-row tile twice: as row
+// fragments (16-byte reads, A operand of S = Q K^T or S^T = K Q^T) and
+// transposed (ds_read_b64_tr_b16, A operand of dK^T += Q^T dS or
+// dQ^T += K^T dS^T). Row p sits in the 1 KB block of the rows congruent to p
+// mod 16, at position p / 16, and block b is placed at index 4 (b % 4) + b / 4
+// with a 1040-byte stride. Sixteen consecutive rows then lie in sixteen
+// different 16-byte bank slots (row reads), four consecutive rows in four
+// different 64-byte bank groups (transposed reads), and every fragment
+// address is a per-lane base plus a constant. Rows are stored in the MFMA
+// output order of perm_row, as in the forward K tile.
+template <int D>
+struct BwdTile {
+  static_assert(D == 128, "256-byte rows");
+  static constexpr int kRowBytes = 2 * D;
+  static constexpr int kChunks = kRowBytes / 16;
+  static constexpr int kBlocks = 16;
+  static constexpr int kStride = 1024 + 16;
+  static constexpr int kBytes = kBlocks * kStride;
+  static __host__ __device__ constexpr int place(int b) { return 4 * (b & 3) + (b >> 2); }
+  static __host__ __device__ constexpr int block_off(int b) { return place(b) * kStride; }
+  static __host__ __device__ constexpr int off(int p, int byte) {
+    return block_off(p & 15) + (p >> 4) * kRowBytes + byte;
+  }
+  static __device__ __forceinline__ int dma_row(int b, int L) { return b + 16 * (L / kChunks); }
+  // Row fragment (physical rows 32 half + l32, bytes 32 kk + 16 g): lane base
+  // plus row_at(half, kk).
+  static __device__ __forceinline__ int row_base(int lane) { return off(lane & 31, (lane >> 5) * 16); }
+  static __host__ __device__ constexpr int row_at(int half, int kk) { return off(32 * half, 32 * kk); }
+  // Transposed fragment of logical rows 32 half + 16 g + 8 h + e (e = 0..7),
+  // column 32 u + l32: physical rows 32 half + 16 h + 4 g + (0..3), then + 8.
+  static __device__ __forceinline__ int tr_base(int lane) {
+    return off(4 * (lane >> 5) + ((lane & 15) >> 2), 2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
+  }
+  static __host__ __device__ constexpr int tr_at(int half, int h, int u) { return off(32 * half + 16 * h, 64 * u); }
+  static constexpr int kTrHi = off(8, 0);
+};
+
+template <int D>
+struct DkvPp {
+  static constexpr int kWaves = 4, kThreads = 64 * kWaves;
+  static constexpr int BKV = 32 * kWaves, BQ = 64, KS = D / 16, DT = D / 32;
+  typedef BwdTile<D> Tile;
+  static constexpr int kSlots = 4;
+  static constexpr int kStatBytes = 2048;  // lse at +0, delta at +1024: one DMA instruction each
+  static constexpr int kSlotBytes = 2 * Tile::kBytes + kStatBytes;
+  static constexpr int kLds = kSlots * kSlotBytes;
+  static constexpr int kDma = Tile::kBlocks / kWaves;  // per wave per tile, for Q and for dO
+};
+
+// DMA of 64 f32 row statistics (lse or delta) starting at row r0 into `lds`
+// (lanes 0-15, 16 bytes each; the other lanes write zeros past them).
+__device__ __forceinline__ void stat_dma(const float* base, int r0, int nrows, char* lds) {
+  const int lane = threadIdx.x & 63;
+  const int rows_left = nrows - r0 > 0 ? nrows - r0 : 0;
+  const uint64_t addr = reinterpret_cast<uint64_t>(base + r0);
+  const u32x4 rsrc = {(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
+                      (uint32_t)__builtin_amdgcn_readfirstlane((int)((addr >> 32) & 0xffffu)),
+                      (uint32_t)__builtin_amdgcn_readfirstlane(rows_left * 4), 0x00020000u};
+  const uint32_t voff = lane < 16 ? (uint32_t)(lane * 16) : 0x80000000u;
+  const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)reinterpret_cast<uintptr_t>(lds));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// dK, dV for 128 keys (32 per wave, K and V fragments in registers), sweeping
+// 64-query tiles from the diagonal on. Each tile is processed in two halves of
+// 32 queries; the S / dP products of the next half are issued while the VALU
+// turns the current half into P and dS, then dV^T += dO^T P and
+// dK^T += Q^T dS run from transposed reads of the same tiles.
+template <int D>
+__global__ __launch_bounds__(256, 1) void attn_dkv_pp_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                            const bf16* __restrict__ v, const bf16* __restrict__ dout,
+                                                            const float* __restrict__ lse,
+                                                            const float* __restrict__ delta, bf16* __restrict__ dk,
+                                                            bf16* __restrict__ dv, int bh_count, int Sq, int Sk, int d,
+                                                            int causal, float scale, float scale_log2) {
+  typedef DkvPp<D> F;
+  typedef typename F::Tile Tile;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  // Heaviest (first) key blocks first.
+  const int bh = blockIdx.x % bh_count;
+  const int kt = (int)(blockIdx.x / bh_count);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int k0 = kt * F::BKV;
+  const int k0w = k0 + 32 * wave;
+  const int kvrow = k0w + l32;
+
+  const bf16* qb = q + (int64_t)bh * Sq * d;
+  const bf16* dob = dout + (int64_t)bh * Sq * d;
+  const bf16* kb = k + (int64_t)bh * Sk * d;
+  const bf16* vb = v + (int64_t)bh * Sk * d;
+  const float* lseb = lse + (int64_t)bh * Sq;
+  const float* db = delta + (int64_t)bh * Sq;
+
+  // Query tiles first .. first + nt - 1; tile t lives in ring slot t % kSlots.
+  const int first = causal ? k0 / F::BQ : 0;
+  const int nt = (Sq + F::BQ - 1) / F::BQ - first;
+
+  bf16x8 kf[F::KS], vf[F::KS];
+  load_row_frags<bf16, D, true, false>(kf, kb, k0w, Sk, d);
+  load_row_frags<bf16, D, true, false>(vf, vb, k0w, Sk, d);
+
+  const PpDma<Tile, true> dma(wave, d);
+  auto slot = [&](int t) { return smem + (t % F::kSlots) * F::kSlotBytes; };
+  auto issue_tile = [&](int t) {
+    char* sl = slot(t);
+    const int r0 = (first + t) * F::BQ;
+    dma.issue(qb, r0, Sq, d, sl);
+    dma.issue(dob, r0, Sq, d, sl + Tile::kBytes);
+    if (wave == 0) {
+      stat_dma(lseb, r0, Sq, sl + 2 * Tile::kBytes);
+      stat_dma(db, r0, Sq, sl + 2 * Tile::kBytes + 1024);
+    }
+  };
+  // The wave's loads for `tiles` more tiles may stay in flight.
+  auto wait_tiles = [&](int tiles) {
+    if (wave == 0) {
+      if (tiles >= 2) wait_vmem<2 * (2 * F::kDma + 2)>();
+      else if (tiles == 1) wait_vmem<2 * F::kDma + 2>();
+      else wait_vmem<0>();
+    } else {
+      if (tiles >= 2) wait_vmem<2 * (2 * F::kDma)>();
+      else if (tiles == 1) wait_vmem<2 * F::kDma>();
+      else wait_vmem<0>();
+    }
+  };
+
+  if (nt > 0) issue_tile(0);
+  if (nt > 1) issue_tile(1);
+  if (nt > 2) issue_tile(2);
+
+  f32x16 dka[F::DT], dva[F::DT];
+#pragma unroll
+  for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dka[u][r] = 0.f;
+      dva[u][r] = 0.f;
+    }
+
+  const int rb = Tile::row_base(lane);
+  const int tb = Tile::tr_base(lane);
+
+  // S = Q K^T and dP = dO V^T for half `half` of the tile at `sl`:
+  // s[r] / dp[r] is query 32 half + 16 g + r of the tile, key kvrow.
+  auto sdp = [&](const char* sl, int half, f32x16& s, f32x16& dp) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[r] = 0.f;
+      dp[r] = 0.f;
+    }
+    const char* qp = sl + rb;
+    const char* dp_ = sl + Tile::kBytes + rb;
+#pragma unroll
+    for (int kk = 0; kk < F::KS; ++kk) {
+      mma32(*reinterpret_cast<const bf16x8*>(qp + Tile::row_at(half, kk)), kf[kk], s);
+      mma32(*reinterpret_cast<const bf16x8*>(dp_ + Tile::row_at(half, kk)), vf[kk], dp);
+    }
+  };
+
+  // P and dS of a half from its S and dP.
+  auto softmax_grad = [&](const char* sl, int qt0, int half, const f32x16& s, const f32x16& dp, bf16x8 (&pf)[2],
+                          bf16x8 (&dsf)[2]) {
+    const float* st = reinterpret_cast<const float*>(sl + 2 * Tile::kBytes) + 32 * half + 16 * g;
+    const int qh = qt0 + 32 * half + 16 * g;
+    const bool mask = causal && qt0 + 32 * half < k0w + 31;
+    float p[16], ds[16];
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const f32x4 ls = *reinterpret_cast<const f32x4*>(st + 4 * r4);
+      const f32x4 dl = *reinterpret_cast<const f32x4*>(st + 256 + 4 * r4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * r4 + e;
+        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], scale_log2, -ls[e] * kLog2e));
+        if (mask && kvrow > qh + r) pv = 0.f;
+        p[r] = pv;
+        ds[r] = pv * (dp[r] - dl[e]);
+      }
+    }
+    to_frag(p, pf[0]);
+    to_frag(p + 8, pf[1]);
+    to_frag(ds, dsf[0]);
+    to_frag(ds + 8, dsf[1]);
+  };
+
+  // dV^T += dO^T P, dK^T += Q^T dS for half `half` of the tile at `sl`.
+  auto grad_kv = [&](const char* sl, int half, const bf16x8 (&pf)[2], const bf16x8 (&dsf)[2]) {
+    const char* qp = sl + tb;
+    const char* dp_ = sl + Tile::kBytes + tb;
+#pragma unroll
+    for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        mma32(tr_frag(dp_ + Tile::tr_at(half, h, u), Tile::kTrHi), pf[h], dva[u]);
+        mma32(tr_frag(qp + Tile::tr_at(half, h, u), Tile::kTrHi), dsf[h], dka[u]);
+      }
+  };
+
+  f32x16 s0, dp0, s1, dp1;
+  bf16x8 pf[2], dsf[2];
+  if (nt > 0) {
+    wait_tiles(nt - 1 < 2 ? nt - 1 : 2);
+    lds_barrier();
+    sdp(slot(0), 0, s0, dp0);
+  }
+  for (int t = 0; t < nt; ++t) {
+    const char* sl = slot(t);
+    const int qt0 = (first + t) * F::BQ;
+    // Half 0: its P / dS while the products of half 1 go out.
+    softmax_grad(sl, qt0, 0, s0, dp0, pf, dsf);
+    sdp(sl, 1, s1, dp1);
+    grad_kv(sl, 0, pf, dsf);
+    // Half 1, with the first half of the next tile.
+    if (t + 1 < nt) {
+      wait_tiles(t + 2 < nt ? 1 : 0);
+      lds_barrier();
+      if (t + 3 < nt) issue_tile(t + 3);
+      softmax_grad(sl, qt0, 1, s1, dp1, pf, dsf);
+      sdp(slot(t + 1), 0, s0, dp0);
+    } else {
+      softmax_grad(sl, qt0, 1, s1, dp1, pf, dsf);
+    }
+    grad_kv(sl, 1, pf, dsf);
+  }
+
+  if (k0w >= Sk) return;
+  store_acc_rows<bf16, D, true>(dka, dk + (int64_t)bh * Sk * d, kvrow, Sk, d, scale);
+  store_acc_rows<bf16, D, true>(dva, dv + (int64_t)bh * Sk * d, kvrow, Sk, d, 1.0f);
+}
+
+// ===========================================================================
 // Host side
 // ===========================================================================
 template <typename K>
@@ -1260,9 +1516,27 @@ int dq_launch(const void* q, const void* k, const void* v, const void* dout, con
   return check_launch("ferrite_flash_attention_bwd_dq");
 }
 
+template <int D>
+int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
+                  void* dk, void* dv, const Shape& s, int causal, float scale, hipStream_t stream) {
+  typedef DkvPp<D> F;
+  const int64_t nk = cdiv(s.sk, F::BKV);
+  const int64_t bh = s.b * s.h;
+  if (nk * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dkv: grid too large");
+  auto kern = attn_dkv_pp_kernel<D>;
+  set_lds(kern, F::kLds);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
+                     static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
+                     delta, static_cast<bf16*>(dk), static_cast<bf16*>(dv), (int)bh, (int)s.sq, (int)s.sk, (int)s.d,
+                     causal, scale, scale * kLog2e);
+  return check_launch("ferrite_flash_attention_bwd_dkv");
+}
+
 template <typename T, int D, bool AL>
 int dkv_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
                void* dk, void* dv, const Shape& s, int causal, float scale, hipStream_t stream) {
+  if constexpr (sizeof(T) == 2 && AL && D == 128)
+    return dkv_pp_launch<D>(q, k, v, dout, lse, delta, dk, dv, s, causal, scale, stream);
   typedef Dkv<T, D, AL> F;
   const int64_t nk = cdiv(s.sk, F::BKV);
   const int64_t bh = s.b * s.h;

@@ -68,6 +68,13 @@ __device__ __forceinline__ void mma32(const f32x8& a, const f32x8& b, f32x16& ac
 }
 
 // Convert 8 f32 values to a fragment of T.
+// Two floats rounded to bf16 (round to nearest even) and packed, a in the
+// low half: one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
 __device__ __forceinline__ void to_frag(const float* v, bf16x8& out) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) out[e] = (bf16)v[e];
