@@ -525,12 +525,12 @@ struct PpVTile {
   }
 };
 
-// One wave's share of the DMA of a 64-row bf16 tile with d == D: four waves
-// split the blocks, wave gw taking blocks gw + 4i. PERM loads physical row r
-// from logical row perm_src(r).
-template <class Layout, bool PERM>
+// One wave's share of the DMA of a 64-row bf16 tile with d == D: GROUP waves
+// split the blocks, wave gw taking blocks gw + GROUP i. PERM loads physical
+// row r from logical row perm_src(r).
+template <class Layout, bool PERM, int GROUP = 4>
 struct PpDma {
-  static constexpr int kPerWave = Layout::kBlocks / 4;
+  static constexpr int kPerWave = Layout::kBlocks / GROUP;
   uint32_t voff[kPerWave];
   int gw;
 
@@ -538,7 +538,7 @@ struct PpDma {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int i = 0; i < kPerWave; ++i) {
-      const int r = Layout::dma_row(gw + 4 * i, lane);
+      const int r = Layout::dma_row(gw + GROUP * i, lane);
       const int src = PERM ? perm_src(r) : r;
       voff[i] = (uint32_t)((src * d + (lane % Layout::kChunks) * 8) * 2);
     }
@@ -555,7 +555,7 @@ struct PpDma {
   // The i-th of this wave's instructions for the tile at `lds`.
   __device__ __forceinline__ void issue_one(const u32x4& rsrc, char* lds, int i) const {
     const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane(
-        (int)(uint32_t)reinterpret_cast<uintptr_t>(lds + Layout::block_off(gw + 4 * i)));
+        (int)(uint32_t)reinterpret_cast<uintptr_t>(lds + Layout::block_off(gw + GROUP * i)));
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff[i]), "s"(rsrc)
                  : "memory", "m0");
   }
@@ -574,7 +574,7 @@ struct PpDma {
 #pragma unroll
     for (int i = 0; i < kPerWave; ++i) {
       const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane(
-          (int)(uint32_t)reinterpret_cast<uintptr_t>(lds + Layout::block_off(gw + 4 * i)));
+          (int)(uint32_t)reinterpret_cast<uintptr_t>(lds + Layout::block_off(gw + GROUP * i)));
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff[i]),
                    "s"(rsrc)
                    : "memory", "m0");
@@ -1309,6 +1309,23 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_pp_kernel(const bf16* __restr
       stat_dma(db, r0, Sq, sl + 2 * Tile::kBytes + 1024);
     }
   };
+  // The same loads in five parts (Q blocks 0-1, 2-3, dO blocks 0-1, 2-3,
+  // lse and delta), issued at different points of a tile so that the four
+  // waves do not queue 34 loads on the address unit at once.
+  auto issue_part = [&](int t, int part) {
+    char* sl = slot(t);
+    const int r0 = (first + t) * F::BQ;
+    if (part < 4) {
+      const bf16* base = part < 2 ? qb : dob;
+      char* lds = sl + (part < 2 ? 0 : Tile::kBytes);
+      const u32x4 rs = dma.rsrc_of(base, r0, Sq, d);
+      dma.issue_one(rs, lds, 2 * (part & 1));
+      dma.issue_one(rs, lds, 2 * (part & 1) + 1);
+    } else if (wave == 0) {
+      stat_dma(lseb, r0, Sq, sl + 2 * Tile::kBytes);
+      stat_dma(db, r0, Sq, sl + 2 * Tile::kBytes + 1024);
+    }
+  };
   // The wave's loads for `tiles` more tiles may stay in flight.
   auto wait_tiles = [&](int tiles) {
     if (wave == 0) {
@@ -1338,29 +1355,12 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_pp_kernel(const bf16* __restr
   const int rb = Tile::row_base(lane);
   const int tb = Tile::tr_base(lane);
 
-  // S = Q K^T and dP = dO V^T for half `half` of the tile at `sl`:
-  // s[r] / dp[r] is query 32 half + 16 g + r of the tile, key kvrow.
-  auto sdp = [&](const char* sl, int half, f32x16& s, f32x16& dp) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[r] = 0.f;
-      dp[r] = 0.f;
-    }
-    const char* qp = sl + rb;
-    const char* dp_ = sl + Tile::kBytes + rb;
-#pragma unroll
-    for (int kk = 0; kk < F::KS; ++kk) {
-      mma32(*reinterpret_cast<const bf16x8*>(qp + Tile::row_at(half, kk)), kf[kk], s);
-      mma32(*reinterpret_cast<const bf16x8*>(dp_ + Tile::row_at(half, kk)), vf[kk], dp);
-    }
-  };
-
-  // P and dS of a half from its S and dP.
+  // P and dS of a half from its S and dP (MASK: zero above the diagonal).
   auto softmax_grad = [&](const char* sl, int qt0, int half, const f32x16& s, const f32x16& dp, bf16x8 (&pf)[2],
-                          bf16x8 (&dsf)[2]) {
+                          bf16x8 (&dsf)[2], auto mask_c) {
+    constexpr bool MASK = decltype(mask_c)::value;
     const float* st = reinterpret_cast<const float*>(sl + 2 * Tile::kBytes) + 32 * half + 16 * g;
     const int qh = qt0 + 32 * half + 16 * g;
-    const bool mask = causal && qt0 + 32 * half < k0w + 31;
     float p[16], ds[16];
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
@@ -1370,7 +1370,7 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_pp_kernel(const bf16* __restr
       for (int e = 0; e < 4; ++e) {
         const int r = 4 * r4 + e;
         float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], scale_log2, -ls[e] * kLog2e));
-        if (mask && kvrow > qh + r) pv = 0.f;
+        if constexpr (MASK) pv = kvrow > qh + r ? 0.f : pv;
         p[r] = pv;
         ds[r] = pv * (dp[r] - dl[e]);
       }
@@ -1381,49 +1381,305 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_pp_kernel(const bf16* __restr
     to_frag(ds + 8, dsf[1]);
   };
 
-  // dV^T += dO^T P, dK^T += Q^T dS for half `half` of the tile at `sl`.
+  // S = Q K^T and dP = dO V^T for half `half` of the tile at `sl` (s[r] /
+  // dp[r] is query 32 half + 16 g + r of the tile, key kvrow), with the
+  // VALU work `valu` spread between the products. Row fragments are read
+  // kBwdAhead products ahead.
+  constexpr int kBwdAhead = 6;
+  auto sdp = [&](const char* sl, int half, f32x16& s, f32x16& dp, auto&& valu) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[r] = 0.f;
+      dp[r] = 0.f;
+    }
+    const char* qp = sl + rb;
+    const char* dp_ = sl + Tile::kBytes + rb;
+    auto read = [&](int i) {
+      return *reinterpret_cast<const bf16x8*>(((i & 1) ? dp_ : qp) + Tile::row_at(half, i >> 1));
+    };
+    bf16x8 buf[16];
+#pragma unroll
+    for (int i = 0; i < kBwdAhead; ++i) buf[i] = read(i);
+    valu();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i + kBwdAhead < 16) buf[i + kBwdAhead] = read(i + kBwdAhead);
+      if (i & 1)
+        mma32(buf[i], vf[i >> 1], dp);
+      else
+        mma32(buf[i], kf[i >> 1], s);
+    }
+#pragma unroll
+    for (int i = 0; i < kBwdAhead; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i + kBwdAhead < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+    }
+  };
+
+  // dV^T += dO^T P, dK^T += Q^T dS for half `half` of the tile at `sl`;
+  // transposed fragments (two reads each) kBwdAheadTr products ahead.
+  constexpr int kBwdAheadTr = 4;
   auto grad_kv = [&](const char* sl, int half, const bf16x8 (&pf)[2], const bf16x8 (&dsf)[2]) {
     const char* qp = sl + tb;
     const char* dp_ = sl + Tile::kBytes + tb;
+    // Product i: output tile u = i / 4, key chunk h = (i / 2) % 2; even: dV, odd: dK.
+    auto read = [&](int i) {
+      return tr_frag(((i & 1) ? qp : dp_) + Tile::tr_at(half, (i >> 1) & 1, i >> 2), Tile::kTrHi);
+    };
+    bf16x8 buf[16];
 #pragma unroll
-    for (int u = 0; u < F::DT; ++u)
+    for (int i = 0; i < kBwdAheadTr; ++i) buf[i] = read(i);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        mma32(tr_frag(dp_ + Tile::tr_at(half, h, u), Tile::kTrHi), pf[h], dva[u]);
-        mma32(tr_frag(qp + Tile::tr_at(half, h, u), Tile::kTrHi), dsf[h], dka[u]);
-      }
+    for (int i = 0; i < 16; ++i) {
+      if (i + kBwdAheadTr < 16) buf[i + kBwdAheadTr] = read(i + kBwdAheadTr);
+      const int u = i >> 2, h = (i >> 1) & 1;
+      if (i & 1)
+        mma32(buf[i], dsf[h], dka[u]);
+      else
+        mma32(buf[i], pf[h], dva[u]);
+    }
+#pragma unroll
+    for (int i = 0; i < kBwdAheadTr; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i + kBwdAheadTr < 16) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
   };
 
   f32x16 s0, dp0, s1, dp1;
   bf16x8 pf[2], dsf[2];
+  auto nop = [] {};
   if (nt > 0) {
     wait_tiles(nt - 1 < 2 ? nt - 1 : 2);
     lds_barrier();
-    sdp(slot(0), 0, s0, dp0);
+    sdp(slot(0), 0, s0, dp0, nop);
   }
   for (int t = 0; t < nt; ++t) {
     const char* sl = slot(t);
     const int qt0 = (first + t) * F::BQ;
-    // Half 0: its P / dS while the products of half 1 go out.
-    softmax_grad(sl, qt0, 0, s0, dp0, pf, dsf);
-    sdp(sl, 1, s1, dp1);
+    // The causal mask touches only the halves that reach the diagonal.
+    const bool mask0 = causal && qt0 < k0w + 31;
+    const bool mask1 = causal && qt0 + 32 < k0w + 31;
+    // Half 0: P / dS between the S / dP products of half 1.
+    if (t > 0 && t + 2 < nt) {
+      issue_part(t + 2, 3);
+      issue_part(t + 2, 4);
+    }
+    if (mask0)
+      sdp(sl, 1, s1, dp1, [&] { softmax_grad(sl, qt0, 0, s0, dp0, pf, dsf, std::true_type{}); });
+    else
+      sdp(sl, 1, s1, dp1, [&] { softmax_grad(sl, qt0, 0, s0, dp0, pf, dsf, std::false_type{}); });
     grad_kv(sl, 0, pf, dsf);
-    // Half 1, with the first half of the next tile.
+    // Half 1, with the products of the next tile's first half.
     if (t + 1 < nt) {
       wait_tiles(t + 2 < nt ? 1 : 0);
       lds_barrier();
-      if (t + 3 < nt) issue_tile(t + 3);
-      softmax_grad(sl, qt0, 1, s1, dp1, pf, dsf);
-      sdp(slot(t + 1), 0, s0, dp0);
+      if (t + 3 < nt) issue_part(t + 3, 0);
+      if (mask1)
+        sdp(slot(t + 1), 0, s0, dp0, [&] { softmax_grad(sl, qt0, 1, s1, dp1, pf, dsf, std::true_type{}); });
+      else
+        sdp(slot(t + 1), 0, s0, dp0, [&] { softmax_grad(sl, qt0, 1, s1, dp1, pf, dsf, std::false_type{}); });
+      if (t + 3 < nt) issue_part(t + 3, 1);
     } else {
-      softmax_grad(sl, qt0, 1, s1, dp1, pf, dsf);
+      if (mask1)
+        softmax_grad(sl, qt0, 1, s1, dp1, pf, dsf, std::true_type{});
+      else
+        softmax_grad(sl, qt0, 1, s1, dp1, pf, dsf, std::false_type{});
     }
     grad_kv(sl, 1, pf, dsf);
+    if (t + 3 < nt) issue_part(t + 3, 2);
   }
 
   if (k0w >= Sk) return;
   store_acc_rows<bf16, D, true>(dka, dk + (int64_t)bh * Sk * d, kvrow, Sk, d, scale);
   store_acc_rows<bf16, D, true>(dva, dv + (int64_t)bh * Sk * d, kvrow, Sk, d, 1.0f);
+}
+
+template <int D>
+struct DqPp {
+  static constexpr int kWaves = 8, kThreads = 64 * kWaves;
+  static constexpr int BQ = 32 * kWaves, BK = 64, KS = D / 16, DT = D / 32;
+  typedef BwdTile<D> Tile;
+  static constexpr int kSlots = 3;
+  static constexpr int kSlotBytes = 2 * Tile::kBytes;  // K then V
+  static constexpr int kLds = kSlots * kSlotBytes;
+  static constexpr int kDma = Tile::kBlocks / kWaves;  // per wave per tile, for K and for V
+};
+
+// dQ for 256 queries (32 per wave, Q and dO fragments in registers),
+// sweeping 64-key tiles up to the diagonal. Waves w and w + 4 share a SIMD.
+// Per 32-key half: S^T = K Q^T and dP^T = V dO^T from row reads of the K and
+// V tiles, dS^T = P^T (dP^T - delta) on the VALU (one query per lane, so lse
+// and delta are per-lane scalars), then dQ^T += K^T dS^T from transposed
+// reads of the K tile.
+template <int D>
+__global__ __launch_bounds__(512, 2) void attn_dq_pp_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                           const bf16* __restrict__ v, const bf16* __restrict__ dout,
+                                                           const float* __restrict__ lse,
+                                                           const float* __restrict__ delta, bf16* __restrict__ dq,
+                                                           int bh_count, int Sq, int Sk, int d, int causal,
+                                                           float scale, float scale_log2, int n_qtiles) {
+  typedef DqPp<D> F;
+  typedef typename F::Tile Tile;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  // Heaviest (last) query tiles first.
+  const int bh = blockIdx.x % bh_count;
+  const int qt = n_qtiles - 1 - (int)(blockIdx.x / bh_count);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+  // SIMD w % 4 holds row blocks 2 (w % 4) and 2 (w % 4) + 1.
+  const int q0 = qt * F::BQ;
+  const int q0w = q0 + 32 * (2 * (wave & 3) + (wave >> 2));
+  const int qrow = q0w + l32;
+
+  const bf16* qb = q + (int64_t)bh * Sq * d;
+  const bf16* dob = dout + (int64_t)bh * Sq * d;
+  const bf16* kb = k + (int64_t)bh * Sk * d;
+  const bf16* vb = v + (int64_t)bh * Sk * d;
+
+  const int q_last = min(q0 + F::BQ, Sq) - 1;
+  const int n = causal ? min(q_last, Sk - 1) / F::BK + 1 : (Sk + F::BK - 1) / F::BK;
+  const bool wave_active = q0w < Sq;
+  const int n_w = !wave_active ? 0 : causal ? min(min(q0w + 31, Sq - 1), Sk - 1) / F::BK + 1 : n;
+
+  const PpDma<Tile, true, 8> dma(wave, d);
+  auto slot = [&](int t) { return smem + (t % F::kSlots) * F::kSlotBytes; };
+  auto issue_tile = [&](int t) {
+    char* sl = slot(t);
+    dma.issue(kb, t * F::BK, Sk, d, sl);
+    dma.issue(vb, t * F::BK, Sk, d, sl + Tile::kBytes);
+  };
+
+  bf16x8 qf[F::KS], dof[F::KS];
+  load_row_frags<bf16, D, true, false>(qf, qb, q0w, Sq, d);
+  load_row_frags<bf16, D, true, false>(dof, dob, q0w, Sq, d);
+  const bool qok = qrow < Sq;
+  const float nlse2 = qok ? -lse[(int64_t)bh * Sq + qrow] * kLog2e : 0.f;
+  const float dl = qok ? delta[(int64_t)bh * Sq + qrow] : 0.f;
+
+  issue_tile(0);
+  if (n > 1) issue_tile(1);
+
+  f32x16 acc[F::DT];
+#pragma unroll
+  for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[u][r] = 0.f;
+
+  const int rb = Tile::row_base(lane);
+  const int tb = Tile::tr_base(lane);
+
+  // S^T and dP^T of half `half` of the tile at sl: s[r] / dp[r] is key
+  // 32 half + 16 g + r of the tile, query qrow. `valu` runs between products.
+  constexpr int kAheadQ = 4;
+  auto sdp = [&](const char* sl, int half, f32x16& s, f32x16& dp, auto&& valu) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[r] = 0.f;
+      dp[r] = 0.f;
+    }
+    const char* kp = sl + rb;
+    const char* vp = sl + Tile::kBytes + rb;
+    auto read = [&](int i) {
+      return *reinterpret_cast<const bf16x8*>(((i & 1) ? vp : kp) + Tile::row_at(half, i >> 1));
+    };
+    bf16x8 buf[16];
+#pragma unroll
+    for (int i = 0; i < kAheadQ; ++i) buf[i] = read(i);
+    valu();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i + kAheadQ < 16) buf[i + kAheadQ] = read(i + kAheadQ);
+      if (i & 1)
+        mma32(buf[i], dof[i >> 1], dp);
+      else
+        mma32(buf[i], qf[i >> 1], s);
+    }
+#pragma unroll
+    for (int i = 0; i < kAheadQ; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i + kAheadQ < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+    }
+  };
+
+  // dS^T of a half (MASK: keys past the query are zero).
+  auto grad_s = [&](int kv0, const f32x16& s, const f32x16& dp, bf16x8 (&dsf)[2], auto mask_c) {
+    constexpr bool MASK = decltype(mask_c)::value;
+    float ds[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], scale_log2, nlse2));
+      if constexpr (MASK) p = kv0 + 16 * g + r > qrow ? 0.f : p;
+      ds[r] = p * (dp[r] - dl);
+    }
+    to_frag(ds, dsf[0]);
+    to_frag(ds + 8, dsf[1]);
+  };
+
+  // dQ^T += K^T dS^T for half `half` of the tile at sl.
+  constexpr int kAheadTr = 4;
+  auto grad_q = [&](const char* sl, int half, const bf16x8 (&dsf)[2]) {
+    const char* kp = sl + tb;
+    // Product i: output tile u = i / 2, key chunk h = i % 2.
+    auto read = [&](int i) { return tr_frag(kp + Tile::tr_at(half, i & 1, i >> 1), Tile::kTrHi); };
+    bf16x8 buf[8];
+#pragma unroll
+    for (int i = 0; i < kAheadTr; ++i) buf[i] = read(i);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i + kAheadTr < 8) buf[i + kAheadTr] = read(i + kAheadTr);
+      mma32(buf[i], dsf[i & 1], acc[i >> 1]);
+    }
+#pragma unroll
+    for (int i = 0; i < kAheadTr; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i + kAheadTr < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+  };
+
+  f32x16 s0, dp0, s1, dp1;
+  bf16x8 dsf[2];
+  auto nop = [] {};
+  for (int t = 0; t < n; ++t) {
+    // Tile t complete for this wave (tile t + 1 may be in flight); after the
+    // barrier every wave has left tile t - 1's slot, which tile t + 2 takes.
+    if (t + 1 < n)
+      wait_vmem<2 * F::kDma>();
+    else
+      wait_vmem<0>();
+    lds_barrier();
+    if (t + 2 < n) issue_tile(t + 2);
+    if (t >= n_w) continue;
+    const char* sl = slot(t);
+    const int kv0 = t * F::BK;
+    const bool mask0 = causal && kv0 + 31 > q0w;
+    const bool mask1 = causal && kv0 + 63 > q0w;
+    sdp(sl, 0, s0, dp0, nop);
+    if (mask0)
+      sdp(sl, 1, s1, dp1, [&] { grad_s(kv0, s0, dp0, dsf, std::true_type{}); });
+    else
+      sdp(sl, 1, s1, dp1, [&] { grad_s(kv0, s0, dp0, dsf, std::false_type{}); });
+    grad_q(sl, 0, dsf);
+    if (mask1)
+      grad_s(kv0 + 32, s1, dp1, dsf, std::true_type{});
+    else
+      grad_s(kv0 + 32, s1, dp1, dsf, std::false_type{});
+    grad_q(sl, 1, dsf);
+  }
+
+  if (!wave_active) return;
+  store_acc_rows<bf16, D, true>(acc, dq + (int64_t)bh * Sq * d, qrow, Sq, d, scale);
 }
 
 // ===========================================================================
@@ -1501,9 +1757,27 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
   return check_launch("ferrite_flash_attention_fwd");
 }
 
+template <int D>
+int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
+                 void* dq, const Shape& s, int causal, float scale, hipStream_t stream) {
+  typedef DqPp<D> F;
+  const int64_t nq = cdiv(s.sq, F::BQ);
+  const int64_t bh = s.b * s.h;
+  if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq: grid too large");
+  auto kern = attn_dq_pp_kernel<D>;
+  set_lds(kern, F::kLds);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
+                     static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
+                     delta, static_cast<bf16*>(dq), (int)bh, (int)s.sq, (int)s.sk, (int)s.d, causal, scale,
+                     scale * kLog2e, (int)nq);
+  return check_launch("ferrite_flash_attention_bwd_dq");
+}
+
 template <typename T, int D, bool AL>
 int dq_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
               void* dq, const Shape& s, int causal, float scale, hipStream_t stream) {
+  if constexpr (sizeof(T) == 2 && AL && D == 128)
+    return dq_pp_launch<D>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream);
   typedef Dq<T, D, AL> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
