@@ -501,6 +501,7 @@ struct PpKTile {
   static __host__ __device__ constexpr int block_off(int b) { return b * kStride; }
   // Row that lane L of the instruction filling block b loads.
   static __device__ __forceinline__ int dma_row(int b, int L) { return b + (L / kChunks) * kBlocks; }
+  static __device__ __forceinline__ bool dma_lane(int) { return true; }
 };
 
 // V tile for V^T fragments read with ds_read_b64_tr_b16, in which lanes 0-31
@@ -523,6 +524,7 @@ struct PpVTile {
   static __device__ __forceinline__ int dma_row(int b, int L) {
     return (b & 3) + 4 * (L / kChunks) + 4 * kRowsPerBlock * (b >> 2);
   }
+  static __device__ __forceinline__ bool dma_lane(int) { return true; }
 };
 
 // One wave's share of the DMA of a 64-row bf16 tile with d == D: GROUP waves
@@ -540,7 +542,7 @@ struct PpDma {
     for (int i = 0; i < kPerWave; ++i) {
       const int r = Layout::dma_row(gw + GROUP * i, lane);
       const int src = PERM ? perm_src(r) : r;
-      voff[i] = (uint32_t)((src * d + (lane % Layout::kChunks) * 8) * 2);
+      voff[i] = Layout::dma_lane(lane) ? (uint32_t)((src * d + (lane % Layout::kChunks) * 8) * 2) : 0x80000000u;
     }
   }
 
@@ -1190,7 +1192,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_dkv_kernel(const T* __restri
 }
 
 // ===========================================================================
-// Backward, bf16 with D = 128: streamed tiles read as rows and transposed
+// Backward, bf16 with D in {64, 128}: streamed tiles read as rows and transposed
 // ===========================================================================
 // The backward kernels read each streamed 64-row tile twice: as row
 // fragments (16-byte reads, A operand of S = Q K^T or S^T = K Q^T) and
@@ -1204,7 +1206,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_dkv_kernel(const T* __restri
 // output order of perm_row, as in the forward K tile.
 template <int D>
 struct BwdTile {
-  static_assert(D == 128, "256-byte rows");
+  static_assert(D == 64 || D == 128, "128- or 256-byte rows");
   static constexpr int kRowBytes = 2 * D;
   static constexpr int kChunks = kRowBytes / 16;
   static constexpr int kBlocks = 16;
@@ -1215,7 +1217,11 @@ struct BwdTile {
   static __host__ __device__ constexpr int off(int p, int byte) {
     return block_off(p & 15) + (p >> 4) * kRowBytes + byte;
   }
+  // With 128-byte rows a block holds its four rows in its first 512 bytes;
+  // lanes 32-63 of its DMA instruction are switched off (they write zeros
+  // into the unused half).
   static __device__ __forceinline__ int dma_row(int b, int L) { return b + 16 * (L / kChunks); }
+  static __device__ __forceinline__ bool dma_lane(int L) { return L / kChunks < 4; }
   // Row fragment (physical rows 32 half + l32, bytes 32 kk + 16 g): lane base
   // plus row_at(half, kk).
   static __device__ __forceinline__ int row_base(int lane) { return off(lane & 31, (lane >> 5) * 16); }
@@ -1397,13 +1403,14 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_pp_kernel(const bf16* __restr
     auto read = [&](int i) {
       return *reinterpret_cast<const bf16x8*>(((i & 1) ? dp_ : qp) + Tile::row_at(half, i >> 1));
     };
-    bf16x8 buf[16];
+    constexpr int N = 2 * F::KS;  // S and dP products alternate over the k-chunks
+    bf16x8 buf[N];
 #pragma unroll
     for (int i = 0; i < kBwdAhead; ++i) buf[i] = read(i);
     valu();
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (i + kBwdAhead < 16) buf[i + kBwdAhead] = read(i + kBwdAhead);
+    for (int i = 0; i < N; ++i) {
+      if (i + kBwdAhead < N) buf[i + kBwdAhead] = read(i + kBwdAhead);
       if (i & 1)
         mma32(buf[i], vf[i >> 1], dp);
       else
@@ -1412,9 +1419,9 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_pp_kernel(const bf16* __restr
 #pragma unroll
     for (int i = 0; i < kBwdAhead; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < N; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (i + kBwdAhead < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i + kBwdAhead < N) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
     }
   };
@@ -1429,12 +1436,13 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_pp_kernel(const bf16* __restr
     auto read = [&](int i) {
       return tr_frag(((i & 1) ? qp : dp_) + Tile::tr_at(half, (i >> 1) & 1, i >> 2), Tile::kTrHi);
     };
-    bf16x8 buf[16];
+    constexpr int N = 4 * F::DT;  // per output tile: two key chunks, dV and dK
+    bf16x8 buf[N];
 #pragma unroll
     for (int i = 0; i < kBwdAheadTr; ++i) buf[i] = read(i);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (i + kBwdAheadTr < 16) buf[i + kBwdAheadTr] = read(i + kBwdAheadTr);
+    for (int i = 0; i < N; ++i) {
+      if (i + kBwdAheadTr < N) buf[i + kBwdAheadTr] = read(i + kBwdAheadTr);
       const int u = i >> 2, h = (i >> 1) & 1;
       if (i & 1)
         mma32(buf[i], dsf[h], dka[u]);
@@ -1444,9 +1452,9 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_pp_kernel(const bf16* __restr
 #pragma unroll
     for (int i = 0; i < kBwdAheadTr; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < N; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (i + kBwdAheadTr < 16) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      if (i + kBwdAheadTr < N) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
   };
 
@@ -1589,13 +1597,14 @@ __global__ __launch_bounds__(512, 2) void attn_dq_pp_kernel(const bf16* __restri
     auto read = [&](int i) {
       return *reinterpret_cast<const bf16x8*>(((i & 1) ? vp : kp) + Tile::row_at(half, i >> 1));
     };
-    bf16x8 buf[16];
+    constexpr int N = 2 * F::KS;  // S^T and dP^T products alternate over the k-chunks
+    bf16x8 buf[N];
 #pragma unroll
     for (int i = 0; i < kAheadQ; ++i) buf[i] = read(i);
     valu();
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (i + kAheadQ < 16) buf[i + kAheadQ] = read(i + kAheadQ);
+    for (int i = 0; i < N; ++i) {
+      if (i + kAheadQ < N) buf[i + kAheadQ] = read(i + kAheadQ);
       if (i & 1)
         mma32(buf[i], dof[i >> 1], dp);
       else
@@ -1604,9 +1613,9 @@ __global__ __launch_bounds__(512, 2) void attn_dq_pp_kernel(const bf16* __restri
 #pragma unroll
     for (int i = 0; i < kAheadQ; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < N; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (i + kAheadQ < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i + kAheadQ < N) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
     }
   };
@@ -1631,20 +1640,21 @@ __global__ __launch_bounds__(512, 2) void attn_dq_pp_kernel(const bf16* __restri
     const char* kp = sl + tb;
     // Product i: output tile u = i / 2, key chunk h = i % 2.
     auto read = [&](int i) { return tr_frag(kp + Tile::tr_at(half, i & 1, i >> 1), Tile::kTrHi); };
-    bf16x8 buf[8];
+    constexpr int N = 2 * F::DT;  // per output tile: two key chunks
+    bf16x8 buf[N];
 #pragma unroll
     for (int i = 0; i < kAheadTr; ++i) buf[i] = read(i);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (i + kAheadTr < 8) buf[i + kAheadTr] = read(i + kAheadTr);
+    for (int i = 0; i < N; ++i) {
+      if (i + kAheadTr < N) buf[i + kAheadTr] = read(i + kAheadTr);
       mma32(buf[i], dsf[i & 1], acc[i >> 1]);
     }
 #pragma unroll
     for (int i = 0; i < kAheadTr; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < N; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (i + kAheadTr < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      if (i + kAheadTr < N) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
   };
 
@@ -1776,7 +1786,7 @@ int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, 
 template <typename T, int D, bool AL>
 int dq_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
               void* dq, const Shape& s, int causal, float scale, hipStream_t stream) {
-  if constexpr (sizeof(T) == 2 && AL && D == 128)
+  if constexpr (sizeof(T) == 2 && AL && D <= 128)
     return dq_pp_launch<D>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream);
   typedef Dq<T, D, AL> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
@@ -1809,7 +1819,7 @@ int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout,
 template <typename T, int D, bool AL>
 int dkv_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
                void* dk, void* dv, const Shape& s, int causal, float scale, hipStream_t stream) {
-  if constexpr (sizeof(T) == 2 && AL && D == 128)
+  if constexpr (sizeof(T) == 2 && AL && D <= 128)
     return dkv_pp_launch<D>(q, k, v, dout, lse, delta, dk, dv, s, causal, scale, stream);
   typedef Dkv<T, D, AL> F;
   const int64_t nk = cdiv(s.sk, F::BKV);
