@@ -584,34 +584,6 @@ struct PpDma {
   }
 };
 
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-
-// Two transposed 8-byte reads at `p` and `p + hi_off`, joined into one
-// 8-element A fragment. Within each 16-lane group the instruction hands lane
-// 4a + b element b of the 4-element pieces addressed by lanes a, a+4, a+8, a+12.
-__device__ __forceinline__ bf16x8 tr_frag(const char* p, int hi_off) {
-  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-  lds_i16x4* p0 = reinterpret_cast<lds_i16x4*>(reinterpret_cast<uintptr_t>(p));
-  lds_i16x4* p1 = reinterpret_cast<lds_i16x4*>(reinterpret_cast<uintptr_t>(p + hi_off));
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p0);
-  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p1);
-  typedef short i16x8 __attribute__((ext_vector_type(8)));
-  const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(bf16x8, v);
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmem() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Workgroup barrier that leaves outstanding global loads (the DMA ring) alone
-// and that the scheduler may not move any instruction across.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
 
 template <int D>
 struct FwdPp {

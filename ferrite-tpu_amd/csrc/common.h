@@ -84,6 +84,56 @@ __device__ __forceinline__ void to_frag(const float* v, f32x8& out) {
   for (int e = 0; e < 8; ++e) out[e] = v[e];
 }
 
+// ---- LDS DMA and transposed LDS reads (gfx950) ------------------------------
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// Two transposed 8-byte reads at `p` and `p + hi_off`, joined into one
+// 8-element A fragment. Within each 16-lane group the instruction hands lane
+// 4a + b element b of the 4-element pieces addressed by lanes a, a+4, a+8, a+12.
+__device__ __forceinline__ bf16x8 tr_frag(const char* p, int hi_off) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  lds_i16x4* p0 = reinterpret_cast<lds_i16x4*>(reinterpret_cast<uintptr_t>(p));
+  lds_i16x4* p1 = reinterpret_cast<lds_i16x4*>(reinterpret_cast<uintptr_t>(p + hi_off));
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p0);
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p1);
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier that leaves outstanding global loads (DMA rings) alone
+// and that the scheduler may not move any instruction across.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Buffer descriptor (raw, unswizzled, bounds-checked) of `bytes` bytes at p.
+// The operands must be wave-uniform; readfirstlane keeps them in SGPRs.
+__device__ __forceinline__ u32x4 buffer_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t addr = reinterpret_cast<uint64_t>(p);
+  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
+               (uint32_t)__builtin_amdgcn_readfirstlane((int)((addr >> 32) & 0xffffu)),
+               (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes), 0x00020000u};
+}
+
+// One buffer_load_dwordx4 ... lds: lane L copies the 16 bytes at voff into
+// LDS at `lds` + 16 L; lanes whose voff is past the range write zeros. Inline
+// assembly, so that the compiler's wait insertion does not tie later LDS
+// reads to it: callers order it with wait_vmem and barriers.
+__device__ __forceinline__ void dma16(const u32x4& rsrc, char* lds, uint32_t voff) {
+  const uint32_t m0 =
+      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)reinterpret_cast<uintptr_t>(lds));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
 // Swap with the lane 32 away (gfx950 v_permlane32_swap) and combine: returns
 // op(x[lane % 32], x[lane % 32 + 32]) in every lane.
 __device__ __forceinline__ float lane32_max(float x) {

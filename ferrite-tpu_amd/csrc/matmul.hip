@@ -242,6 +242,204 @@ int launch_gemm(const void* x, const void* y, void* out, int64_t M, int64_t N, i
   return check_launch("ferrite_matmul");
 }
 
+// ===========================================================================
+// bf16 GEMM on DMA-fed LDS tiles (K % 64 == 0, N % 8 == 0, 16-byte aligned)
+// ===========================================================================
+// 256 x 256 output tile per workgroup of 8 waves, 64 k per step through two
+// LDS stages filled by buffer_load ... lds. Wave w owns output rows
+// 128 (w / 4) .. +127 and columns 64 (w % 4) .. +63, computed as C^T tiles:
+// A = y^T fragments (transposed reads of the y tile), B = x row fragments.
+//
+// x tile (256 rows of 64 k, 128 bytes each): four 64-row subtiles; row r of a
+// subtile sits in 1 KB block r % 8 at position r / 8, blocks 1040 bytes apart,
+// so a 16-lane row read (16 consecutive rows, one 16-byte chunk) covers 16
+// different bank slots.
+struct GemmXTile {
+  static constexpr int kRowBytes = 128, kStride = 1040;
+  static constexpr int kSubBytes = 8 * kStride;
+  static constexpr int kBytes = 4 * kSubBytes;
+  static __host__ __device__ constexpr int off(int row, int byte) {
+    return (row >> 6) * kSubBytes + (row & 7) * kStride + ((row >> 3) & 7) * kRowBytes + byte;
+  }
+  // Instruction i = 8 s + b fills block b of subtile s: lane L takes row
+  // 64 s + b + 8 (L / 8), 16-byte chunk L % 8.
+  static __device__ __forceinline__ int dma_row(int i, int L) { return 64 * (i >> 3) + (i & 7) + 8 * (L >> 3); }
+  static __host__ __device__ constexpr int block_off(int i) { return (i >> 3) * kSubBytes + (i & 7) * kStride; }
+};
+
+// y tile (64 k-rows of 256 columns, 512 bytes each): block 4p + m holds rows
+// m + 8p and m + 8p + 4, blocks 1088 bytes apart, so the four consecutive rows
+// of a transposed read lie in the four 64-byte bank groups.
+struct GemmYTile {
+  static constexpr int kRowBytes = 512, kStride = 1088;
+  static constexpr int kBytes = 32 * kStride;
+  static __host__ __device__ constexpr int off(int row, int byte) {
+    return ((row & 3) + 4 * (row >> 3)) * kStride + ((row >> 2) & 1) * kRowBytes + byte;
+  }
+  static __device__ __forceinline__ int dma_row(int b, int L) { return (b & 3) + 8 * (b >> 2) + 4 * (L >> 5); }
+  static __host__ __device__ constexpr int block_off(int b) { return b * kStride; }
+};
+
+struct Gemm2 {
+  static constexpr int kWaves = 8, kThreads = 64 * kWaves;
+  static constexpr int BM = 256, BN = 256, BK = 64;
+  static constexpr int kStageBytes = GemmXTile::kBytes + GemmYTile::kBytes;
+  static constexpr int kLds = 2 * kStageBytes;
+  static constexpr int kDma = 32 / kWaves;  // instructions per wave per stage, for x and for y
+};
+
+template <typename TO>
+__global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict__ x, const bf16* __restrict__ y,
+                                                          TO* __restrict__ out, int M, int N, int K, int tiles_m,
+                                                          int tiles_n) {
+  typedef Gemm2 G;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  // Tiles of one XCD (blocks are dealt to the 8 XCDs round robin) are made
+  // consecutive and ordered in groups of 4 tile rows, so an XCD's L2 holds
+  // few x and y panels.
+  const int nblocks = tiles_m * tiles_n;
+  int v = blockIdx.x;
+  if (nblocks % 8 == 0) v = (blockIdx.x % 8) * (nblocks / 8) + blockIdx.x / 8;
+  constexpr int kGroup = 4;
+  const int group = v / (kGroup * tiles_n);
+  const int first_m = group * kGroup;
+  const int gsize = min(tiles_m - first_m, kGroup);
+  const int tm = first_m + (v % (kGroup * tiles_n)) % gsize;
+  const int tn = (v % (kGroup * tiles_n)) / gsize;
+  const int m0 = tm * G::BM, n0 = tn * G::BN;
+  const int wm0 = (wave >> 2) * 128, wn0 = (wave & 3) * 64;
+
+  // Per-lane DMA offsets; rows past M and columns past N read as zeros.
+  uint32_t xoff[G::kDma], yoff[G::kDma];
+#pragma unroll
+  for (int i = 0; i < G::kDma; ++i) {
+    const int xi = wave + 8 * i;
+    const int xr = GemmXTile::dma_row(xi, lane);
+    xoff[i] = m0 + xr < M ? (uint32_t)(((int64_t)xr * K + (lane & 7) * 8) * 2) : 0x80000000u;
+    const int yb = wave + 8 * i;
+    const int yr = GemmYTile::dma_row(yb, lane);
+    const int yc = (lane & 31) * 8;
+    yoff[i] = n0 + yc < N ? (uint32_t)(((int64_t)yr * N + yc) * 2) : 0x80000000u;
+  }
+  auto issue = [&](int kt) {
+    char* st = smem + (kt & 1) * G::kStageBytes;
+    const int k0 = kt * G::BK;
+    const u32x4 rx = buffer_rsrc(x + (int64_t)m0 * K + k0, 0x7ffffff0u);
+    const u32x4 ry = buffer_rsrc(y + (int64_t)k0 * N + n0, 0x7ffffff0u);
+#pragma unroll
+    for (int i = 0; i < G::kDma; ++i) {
+      dma16(rx, st + GemmXTile::block_off(wave + 8 * i), xoff[i]);
+      dma16(ry, st + GemmXTile::kBytes + GemmYTile::block_off(wave + 8 * i), yoff[i]);
+    }
+  };
+
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
+
+  // Lane bases: x row fragment (row l32, bytes 16 g) and y^T fragment (rows
+  // 8 g + (0..3), columns 16 ((lane / 16) % 2) + 4 (lane % 4)).
+  const int xb = GemmXTile::off(l32, 16 * g);
+  const int yb = GemmYTile::off(8 * g + ((lane & 15) >> 2), 2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
+  constexpr int kYHi = GemmYTile::off(4, 0);
+
+  const int nk = K / G::BK;
+  issue(0);
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_vmem<0>();
+    lds_barrier();
+    if (kt + 1 < nk) issue(kt + 1);
+    const char* xs = smem + (kt & 1) * G::kStageBytes + xb;
+    const char* ys = smem + (kt & 1) * G::kStageBytes + GemmXTile::kBytes + yb;
+    // 4 k-steps x (2 y^T fragments, 4 x fragments, 8 products); the next
+    // k-step's six fragments are read while this one's products run.
+    auto read_a = [&](int kk, int j) {
+      return tr_frag(ys + GemmYTile::off(16 * kk, 2 * (wn0 + 32 * j)), kYHi);
+    };
+    auto read_b = [&](int kk, int i) {
+      return *reinterpret_cast<const bf16x8*>(xs + GemmXTile::off(wm0 + 32 * i, 32 * kk));
+    };
+    bf16x8 fa[2][2], fb[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) fa[0][j] = read_a(0, j);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fb[0][i] = read_b(0, i);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int c = kk & 1;
+      if (kk + 1 < 4) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) fa[c ^ 1][j] = read_a(kk + 1, j);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fb[c ^ 1][i] = read_b(kk + 1, i);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mma32(fa[c][j], fb[c][i], acc[j][i]);
+    }
+    // First fragments, then per k-step: one MFMA per read of the next step's
+    // six fragments (two of them a pair of transposed reads), then the rest.
+#pragma unroll
+    for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      if (kk + 1 < 4) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      }
+    }
+  }
+
+  // Epilogue: acc[j][i] is a C^T tile; register r of lane (l32, g) is
+  // C[m0 + wm0 + 32 i + l32][n0 + wn0 + 32 j + (r / 4) * 8 + g * 4 + r % 4].
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + wm0 + 32 * i + l32;
+      if (m >= M) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn0 + 32 * j + 8 * q + 4 * g;
+        if (n >= N) continue;  // N % 8 == 0: a quad is either all in or all out
+        TO* dst = out + (int64_t)m * N + n;
+        if constexpr (sizeof(TO) == 2) {
+          *reinterpret_cast<bf16x4*>(dst) = bf16x4{(bf16)acc[j][i][4 * q], (bf16)acc[j][i][4 * q + 1],
+                                                   (bf16)acc[j][i][4 * q + 2], (bf16)acc[j][i][4 * q + 3]};
+        } else {
+          *reinterpret_cast<f32x4*>(dst) =
+              f32x4{acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]};
+        }
+      }
+    }
+  }
+}
+
+template <typename TO>
+int launch_gemm_dma(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  typedef Gemm2 G;
+  const int64_t tiles_m = cdiv(M, G::BM), tiles_n = cdiv(N, G::BN);
+  auto kern = gemm_dma_kernel<TO>;
+  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::kLds);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n)), dim3(G::kThreads), G::kLds, stream,
+                     static_cast<const bf16*>(x), static_cast<const bf16*>(y), static_cast<TO*>(out), (int)M, (int)N,
+                     (int)K, (int)tiles_m, (int)tiles_n);
+  return check_launch("ferrite_matmul");
+}
+
 }  // namespace
 }  // namespace ferrite
 
@@ -254,6 +452,16 @@ extern "C" int ferrite_hip_matmul(const void* x, const void* y, void* out, int64
   if (!x || !y || !out) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_matmul: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (in_dtype == FERRITE_BF16) {
+    // DMA-fed kernel: whole 64-deep k steps, 16-byte y rows and pointers, and
+    // offsets that fit the 31-bit buffer range (256 rows of x, 64 rows of y).
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool dma_ok = k % Gemm2::BK == 0 && n % 8 == 0 && a16(x) && a16(y) && a16(out) && m <= 0x7fffffff &&
+                        n <= 0x7fffffff && 256 * k * 2 < 0x7ffffff0 && 64 * n * 2 < 0x7ffffff0 &&
+                        cdiv(m, (int64_t)Gemm2::BM) * cdiv(n, (int64_t)Gemm2::BN) <= 0x7fffffff;
+    if (dma_ok) {
+      if (out_dtype == FERRITE_BF16) return launch_gemm_dma<bf16>(x, y, out, m, n, k, s);
+      return launch_gemm_dma<float>(x, y, out, m, n, k, s);
+    }
     if (out_dtype == FERRITE_BF16) return launch_gemm<bf16, bf16, 256, 256, 64, 2, 2>(x, y, out, m, n, k, s);
     return launch_gemm<bf16, float, 256, 256, 64, 2, 2>(x, y, out, m, n, k, s);
   }
