@@ -113,3 +113,25 @@ def test_every_element_written_and_deterministic(dev):
         assert not torch.isnan(o).any()
         outs.append(o.clone())
     assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("m,k,n", [(300, 128, 264), (257, 192, 520), (1000, 512, 776), (64, 64, 8)])
+def test_bf16_dma_path_tails(dev, m, k, n):
+    """bf16 inputs with K a multiple of 64 and N a multiple of 8 take the DMA-fed kernel, whose
+    tiles are 256 x 256: rows past M and columns past N must read as zeros and never be stored.
+    Every output element is written (NaN-prefilled), f32 out matches the f64 product to the
+    accumulation bar, bf16 out is within one bf16 ulp of the exact product."""
+    x, y = uniform(23, (m, k), "bf16"), uniform(24, (k, n), "bf16")
+    xt, yt = to_dev(x, "bf16", dev), to_dev(y, "bf16", dev)
+    exact = omm.reference(x, y)
+    for out_code, tdt in ((_hip.F32, torch.float32), (_hip.BF16, torch.bfloat16)):
+        o = torch.full((m, n), float("nan"), dtype=tdt, device=dev)
+        _hip.check(_hip.lib().ferrite_hip_matmul(xt.data_ptr(), yt.data_ptr(), o.data_ptr(), m, n, k, _hip.BF16,
+                                                 out_code, _hip.stream_of(xt)), "matmul")
+        torch.cuda.synchronize()
+        got = to_np(o)
+        assert not np.isnan(got).any()
+        if tdt == torch.float32:
+            assert np.max(np.abs(got - exact)) <= 1e-5 * max(1.0, np.max(np.abs(exact))) * (1 + k / 64)
+        else:
+            assert np.all(np.abs(got - exact) <= bf16_ulp(exact) + 2.0 ** -20 * np.abs(x).sum(1, keepdims=True) @ np.abs(y).max(0, keepdims=True))
