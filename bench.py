@@ -56,6 +56,21 @@ def _events_time(fn, iters: int, warmup: int) -> float:
     return start.elapsed_time(end) * 1e-3 / iters
 
 
+def _settle(fn, seconds: float = 0.2) -> None:
+    """Run `fn` back to back for `seconds` before anything is timed. The shader clock needs a
+    few milliseconds of sustained load to reach its steady value; without this the first
+    kernel measured would be timed partly at the idle clock."""
+    import time
+
+    import torch
+
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(32):
+            fn()
+        torch.cuda.synchronize()
+
+
 def _traffic(kernel: str):
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), read from the committed summary."""
     if not os.path.exists(TRAFFIC_FILE):
@@ -110,6 +125,7 @@ def bench_attention(b, h, t, d, steps, warmup, seed=7):
         dkv()
         dqk()
 
+    _settle(fwd)
     t_fwd = _events_time(fwd, steps, warmup)
     t_delta = _events_time(dlt, steps, warmup)
     t_dkv = _events_time(dkv, steps, warmup)

@@ -847,6 +847,346 @@ __global__ __launch_bounds__(512, 2) void attn_fwd_pp_kernel(const bf16* __restr
 }
 
 // ===========================================================================
+// Forward, bf16, causal, D in {64, 128}, S % 64 == 0: software-pipelined waves
+// ===========================================================================
+// 256 query rows per workgroup; each wave owns RB blocks of 32 rows (RB = 1:
+// 8 waves, two per SIMD; RB = 2: 4 waves, one per SIMD). Instead of trading
+// phases with a partner wave, every wave overlaps its own work: stage j issues
+// the products S^T = K_{j+1} Q^T and O^T += V_{j-1}^T P_{j-1}^T, and the
+// softmax of tile j runs between those MFMAs on the VALU. One workgroup
+// barrier per stage orders the K and V rings, which use the ping-pong
+// kernel's LDS layouts and DMA.
+//
+// The softmax takes no per-tile row max: p = exp2(s c - m) with the running
+// m, and the lane's partial row sums double as the overflow test. When one
+// exceeds 2^8 or is not finite (always on the first tile, where m = -inf),
+// the wave redoes that tile: row max, m raised to it, O and l rescaled, p
+// recomputed. Every p that is kept is <= 2^8, the bound of the lazy rescale.
+
+// An empty asm that takes and returns `f`: the value is computed at this
+// point of the program, and later code may not be merged with its producer.
+__device__ __forceinline__ void pin(bf16x8& f) {
+  u32x4 w = __builtin_bit_cast(u32x4, f);
+  asm volatile("" : "+v"(w));
+  f = __builtin_bit_cast(bf16x8, w);
+}
+
+template <int D, int RB>
+struct FwdW {
+  static constexpr int kWaves = 8 / RB, kThreads = 64 * kWaves;
+  static constexpr int BQ = 256, BK = 64;
+  static constexpr int KS = D / 16, DT = D / 32;
+  typedef PpKTile<D> KT;
+  typedef PpVTile<D> VT;
+  static constexpr int kSlots = 3;
+  static constexpr int kLds = kSlots * (KT::kBytes + VT::kBytes);
+  // Who issues the ring's DMA, and when (measured on MI355X): with D = 128
+  // every wave issues its share right after the stage barrier; with D = 64
+  // the older half of the waves, which the SIMD arbiter favours and which
+  // therefore finish their stage first, issue all of it after their stage.
+  static constexpr bool kDmaLate = D == 64;
+  static constexpr int kDmaWaves = kDmaLate ? kWaves / 2 : kWaves;
+  static constexpr int kDma = KT::kBlocks / kDmaWaves;  // DMA instructions per tile and issuing wave
+  static constexpr int kAhead = 3;                      // fragments read ahead of their MFMAs
+  static_assert(KT::kBlocks == VT::kBlocks && kDma >= 1, "K and V tiles split evenly over the waves");
+};
+
+template <int D, int RB>
+__global__ __launch_bounds__((FwdW<D, RB>::kThreads), 1) void attn_fwd_sw_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, bf16* __restrict__ o,
+    float* __restrict__ lse, int bh_count, int S, int d, float scale_log2, int neg_q, int n_qtiles) {
+  typedef FwdW<D, RB> F;
+  typedef typename F::KT KT;
+  typedef typename F::VT VT;
+  constexpr int KS = F::KS, DT = F::DT;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char* const kring = smem;
+  char* const vring = smem + F::kSlots * KT::kBytes;
+
+  // Heaviest (last) query tiles first; all tiles of one head share an XCD
+  // when bh_count is a multiple of 8.
+  const int bh = blockIdx.x % bh_count;
+  const int qt = n_qtiles - 1 - (int)(blockIdx.x / bh_count);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int q0 = qt * F::BQ;
+  const int q0w = q0 + 32 * RB * wave;
+  // Tiles of 64 keys: n for the workgroup, n_w for this wave, whose last
+  // tile (keys from 64 (n_w - 1)) is its diagonal.
+  const int n = (min(q0 + F::BQ, S) - 1) / F::BK + 1;
+  const int n_w = q0w < S ? (q0w + 32 * RB - 1) / F::BK + 1 : 0;
+
+  const bf16* qb = q + (int64_t)bh * S * d;
+  const bf16* kb = k + (int64_t)bh * S * d;
+  const bf16* vb = v + (int64_t)bh * S * d;
+
+  // K_0 and K_1 go out first; stage j then loads K_{j+3} and V_{j+1}.
+  const bool dma_wave = wave < F::kDmaWaves;
+  const PpDma<KT, true, F::kDmaWaves> kdma(wave % F::kDmaWaves, d);
+  const PpDma<VT, false, F::kDmaWaves> vdma(wave % F::kDmaWaves, d);
+  if (dma_wave) {
+    kdma.issue(kb, 0, S, d, kring);
+    if (1 < n) kdma.issue(kb, F::BK, S, d, kring + KT::kBytes);
+  }
+
+  bf16x8 qf[RB][KS];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    if (neg_q)
+      load_row_frags<bf16, D, true, true>(qf[rb], qb, q0w + 32 * rb, S, d);
+    else
+      load_row_frags<bf16, D, true, false>(qf[rb], qb, q0w + 32 * rb, S, d);
+  }
+
+  const int kbase = KT::off(l32, g * 16);
+  const int vbase = VT::off((lane >> 5) * 16 + ((lane & 15) >> 2), 2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
+  // Diagonal tile: key kt*32 + g*16 + r of the tile is invisible to row
+  // rb*32 + l32 of the wave when r > lim[rb][kt].
+  int lim[RB][2];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) lim[rb][kt] = q0w % F::BK + rb * 32 + l32 - kt * 32 - g * 16;
+
+  f32x16 acc[RB][DT];  // O^T per row block: register r of tile u = dim u*32 + (r/4)*8 + g*4 + r%4
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int u = 0; u < DT; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[rb][u][r] = 0.f;
+  f32x16 s[2][2][RB];   // [buffer][key subtile][row block]: S^T of one tile
+  bf16x8 pf[2][RB][4];  // [buffer][row block][16-key chunk]: P^T fragments
+  float m[RB], neg_m[RB], lsum[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    m[rb] = -INFINITY;
+    neg_m[rb] = INFINITY;
+    lsum[rb] = 0.f;
+  }
+
+  // Stage j loads K_{j+3} and V_{j+1} into the slots that K_j and V_{j-2}
+  // left at its barrier.
+  auto dma = [&](int j) {
+    if (!dma_wave) return;
+    if (j + 3 < n) kdma.issue(kb, (j + 3) * F::BK, S, d, kring + ((j + 3) % F::kSlots) * KT::kBytes);
+    if (j + 1 < n) vdma.issue(vb, (j + 1) * F::BK, S, d, vring + ((j + 1) % F::kSlots) * VT::kBytes);
+  };
+
+  // Stage j with parity P = j & 1 (tile t lives in s[t & 1] and pf[t & 1]).
+  auto stage = [&](auto P_, auto QK_, auto SM_, auto MASK_, auto PV_, int j) {
+    constexpr int P = decltype(P_)::value;
+    constexpr bool QK = decltype(QK_)::value, SM = decltype(SM_)::value;
+    constexpr bool MASK = decltype(MASK_)::value, PV = decltype(PV_)::value;
+    f32x16(&sn)[2][RB] = s[1 - P];
+    f32x16(&sc)[2][RB] = s[P];
+    bf16x8(&pc)[RB][4] = pf[P];
+    bf16x8(&pp)[RB][4] = pf[1 - P];
+    const char* kp = kring + ((j + 1) % F::kSlots) * KT::kBytes + kbase;
+    const char* vp = vring + ((j + 2) % F::kSlots) * VT::kBytes + vbase;
+    constexpr int NFQ = QK ? 2 * KS : 0;  // K fragments (key subtile f % 2, k-chunk f / 2)
+    constexpr int NFV = PV ? 4 * DT : 0;  // V^T fragments (key chunk i / DT, dim tile i % DT)
+    constexpr int NF = NFQ + NFV;
+    auto read = [&](int f) -> bf16x8 {
+      if (f < NFQ) return *reinterpret_cast<const bf16x8*>(kp + KT::off(32 * (f & 1), (f >> 1) * 32));
+      const int i = f - NFQ, c = i / DT, u = i % DT;
+      return tr_frag(vp + VT::off((c >> 1) * 32 + (c & 1) * 8, u * 64), VT::off(4, 0));
+    };
+    // Product rb of fragment f.
+    auto prod1 = [&](int f, int rb, const bf16x8& a) {
+      if (f < NFQ) {
+        const int kt = f & 1, kc = f >> 1;
+        if (kc == 0)
+          sn[kt][rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[rb][0], f32x16{}, 0, 0, 0);
+        else
+          mma32(a, qf[rb][kc], sn[kt][rb]);
+      } else {
+        const int i = f - NFQ, c = i / DT, u = i % DT;
+        mma32(a, pp[rb][c], acc[rb][u]);
+      }
+    };
+    float t[RB][2];  // [row block][partial] sums of this tile's p in the lane
+    // Softmax element e of the lane: row block e / 32, key subtile (e / 16) % 2,
+    // register e % 16. Every 8 elements make one P^T fragment.
+    float p[8];
+    auto softmax_elem = [&](int e, const float(&nm)[RB]) {
+      const int rb = e >> 5, kt = (e >> 4) & 1, r = e & 15;
+      float x = sc[kt][rb][r];
+      if constexpr (MASK) x = r > lim[rb][kt] ? -INFINITY : x;
+      p[r & 7] = __builtin_amdgcn_exp2f(__builtin_fmaf(x, scale_log2, nm[rb]));
+      t[rb][r & 1] += p[r & 7];
+      if ((r & 7) == 7) {
+        bf16x8& f = pc[rb][2 * kt + (r >> 3)];
+        to_frag(p, f);
+        // Keep the conversion here: without the fence the compiler sinks it
+        // below the rare redo branch, which holds all p values live across it.
+        pin(f);
+      }
+    };
+    constexpr int NE = 32 * RB;  // softmax elements per lane
+    auto softmax = [&](const float(&nm)[RB]) {
+#pragma unroll
+      for (int e = 0; e < NE; ++e) softmax_elem(e, nm);
+    };
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) t[rb][0] = t[rb][1] = 0.f;
+
+    if constexpr (NF > 0) {
+      // The program order is the schedule: MFMA slot i carries the product
+      // i % RB of fragment i / RB, the LDS read of the fragment kAhead
+      // further on (at the fragment's first product) and an equal share of
+      // the softmax elements, fenced so that the scheduler keeps it so.
+      constexpr int NM = NF * RB;
+      static_assert(!SM || NE % NM == 0 || NM % NE == 0, "softmax elements spread evenly over the products");
+      bf16x8 buf[NF];
+#pragma unroll
+      for (int f = 0; f < F::kAhead && f < NF; ++f) buf[f] = read(f);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        const int f = i / RB, rb = i % RB;
+        if (rb == 0 && f + F::kAhead < NF) buf[f + F::kAhead] = read(f + F::kAhead);
+        prod1(f, rb, buf[f]);
+        if constexpr (SM) {
+          if constexpr (NE >= NM) {
+#pragma unroll
+            for (int e = i * (NE / NM); e < (i + 1) * (NE / NM); ++e) softmax_elem(e, neg_m);
+          } else {
+            if (i % (NM / NE) == 0) softmax_elem(i / (NM / NE), neg_m);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else if constexpr (SM) {
+      softmax(neg_m);
+    }
+
+    if constexpr (SM) {
+      bool bad = false;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) bad = bad || !(t[rb][0] + t[rb][1] <= 256.f);
+      if (__builtin_amdgcn_ballot_w64(bad)) {
+        // Redo the tile from the row max: raise m, rescale O and l.
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          float mx = -INFINITY;
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              float x = sc[kt][rb][r];
+              if constexpr (MASK) x = r > lim[rb][kt] ? -INFINITY : x;
+              mx = fmaxf(mx, x);
+            }
+          const float m_new = fmaxf(m[rb], lane32_max(mx) * scale_log2);
+          const float alpha = __builtin_amdgcn_exp2f(m[rb] - m_new);
+          m[rb] = m_new;
+          neg_m[rb] = -m_new;
+          lsum[rb] *= alpha;
+#pragma unroll
+          for (int u = 0; u < DT; ++u)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[rb][u][r] *= alpha;
+          t[rb][0] = t[rb][1] = 0.f;
+        }
+        softmax(neg_m);
+      }
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) lsum[rb] += t[rb][0] + t[rb][1];
+    }
+  };
+
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  // The workgroup passes stages j = -1 .. n; sync(j) opens stage j.
+  auto sync = [&](int j) {
+    // This wave's parts of K_{j+1} and V_{j-1} have landed; the loads issued
+    // by stage j - 1 (K_{j+2}, then V_j) may still be in flight.
+    const bool k_prev = dma_wave && j + 2 < n, v_prev = dma_wave && j >= 0 && j < n;
+    if (k_prev && v_prev)
+      wait_vmem<2 * F::kDma>();
+    else if (k_prev || v_prev)
+      wait_vmem<F::kDma>();
+    else
+      wait_vmem<0>();
+    // Every wave's parts have landed and every wave has left stage j - 1.
+    lds_barrier();
+    if (!F::kDmaLate) dma(j);
+  };
+  // Closes stage j.
+  auto close = [&](int j) {
+    if (F::kDmaLate) dma(j);
+  };
+  // This wave's stages: QK of tile 0; QK + softmax for tiles 0 .. n_w - 2
+  // (with PV from tile 1 on); the diagonal tile's masked softmax; the last PV.
+  sync(-1);
+  if (n_w > 0) stage(P1(), T_(), F_(), F_(), F_(), -1);
+  close(-1);
+  int j = 0;
+  if (n_w >= 2) {
+    sync(0);
+    stage(P0(), T_(), T_(), F_(), F_(), 0);
+    close(0);
+    for (j = 1; j + 2 < n_w; j += 2) {
+      sync(j);
+      stage(P1(), T_(), T_(), F_(), T_(), j);
+      close(j);
+      sync(j + 1);
+      stage(P0(), T_(), T_(), F_(), T_(), j + 1);
+      close(j + 1);
+    }
+    if (j + 1 < n_w) {
+      sync(j);
+      stage(P1(), T_(), T_(), F_(), T_(), j);
+      close(j);
+      ++j;
+    }
+  }
+  if (n_w == 1) {
+    sync(0);
+    stage(P0(), F_(), T_(), T_(), F_(), 0);
+    close(0);
+    sync(1);
+    stage(P1(), F_(), F_(), F_(), T_(), 1);
+    close(1);
+    j = 2;
+  } else if (n_w >= 2) {
+    if (j & 1) {
+      sync(j);
+      stage(P1(), F_(), T_(), T_(), T_(), j);
+      close(j);
+      sync(j + 1);
+      stage(P0(), F_(), F_(), F_(), T_(), j + 1);
+      close(j + 1);
+    } else {
+      sync(j);
+      stage(P0(), F_(), T_(), T_(), T_(), j);
+      close(j);
+      sync(j + 1);
+      stage(P1(), F_(), F_(), F_(), T_(), j + 1);
+      close(j + 1);
+    }
+    j += 2;
+  }
+  for (; j <= n; ++j) {
+    sync(j);
+    close(j);
+  }
+
+  if (n_w == 0) return;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int row = q0w + 32 * rb + l32;
+    const float l = lane32_sum(lsum[rb]);
+    store_acc_rows<bf16, D, true>(acc[rb], o + (int64_t)bh * S * d, row, S, d, 1.0f / l);
+    if (g == 0 && row < S) lse[(int64_t)bh * S + row] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
+  }
+}
+
+// ===========================================================================
 // delta = rowsum(f32 dO * f32 O)
 // ===========================================================================
 template <typename T>
@@ -1702,6 +2042,21 @@ int check_shape(const char* name, const Shape& s, int dtype, int causal, bool bw
 
 int pad_dim(int64_t d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
 
+template <int D, int RB = 1>
+int fwd_sw_launch(const void* q, const void* k, const void* v, void* o, float* lse, const Shape& s, float c, int neg_q,
+                  hipStream_t stream) {
+  typedef FwdW<D, RB> F;
+  const int64_t nq = cdiv(s.sq, F::BQ);
+  const int64_t bh = s.b * s.h;
+  if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: grid too large");
+  auto kern = attn_fwd_sw_kernel<D, RB>;
+  set_lds(kern, F::kLds);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
+                     static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<bf16*>(o), lse, (int)bh,
+                     (int)s.sq, (int)s.d, c, neg_q, (int)nq);
+  return check_launch("ferrite_flash_attention_fwd");
+}
+
 template <int D>
 int fwd_pp_launch(const void* q, const void* k, const void* v, void* o, float* lse, const Shape& s, int causal,
                   float c, int neg_q, hipStream_t stream) {
@@ -1732,7 +2087,10 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
   float c = scale * kLog2e;
   const int neg_q = c < 0.f;
   c = fmaxf(fabsf(c), 1e-30f);
-  if constexpr (sizeof(T) == 2 && AL && D <= 128) return fwd_pp_launch<D>(q, k, v, o, lse, s, causal, c, neg_q, stream);
+  if constexpr (sizeof(T) == 2 && AL && D <= 128) {
+    if (causal && s.sq == s.sk && s.sq % 64 == 0) return fwd_sw_launch<D>(q, k, v, o, lse, s, c, neg_q, stream);
+    return fwd_pp_launch<D>(q, k, v, o, lse, s, causal, c, neg_q, stream);
+  }
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(kThreads), F::kLds, stream, static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v), static_cast<T*>(o), lse, (int)bh, (int)s.sq,
                      (int)s.sk, (int)s.d, causal, c, neg_q, (int)nq);

@@ -180,6 +180,18 @@ def test_ragged_and_unaligned_via_abi(dev, b, h, sq, sk, d, dtype, causal, scale
     _abi_case(dev, b, h, sq, sk, d, dtype, causal, seed=31, scale=scale)
 
 
+@pytest.mark.parametrize("b,h,s,d", [
+    (1, 3, 64, 128),    # one key tile: the workgroup's last six waves have no rows
+    (2, 1, 192, 64),    # 192 rows: a partial 256-row query tile
+    (1, 2, 320, 128),   # 256 + 64 rows
+    (1, 1, 128, 64),
+    (1, 2, 128, 80),    # d padded 80 -> 128 on the 64-row-tile path
+])
+def test_causal_tile_edges_via_abi(dev, b, h, s, d):
+    """Causal bf16 lengths that are multiples of 64 but not of the 256-row query tile."""
+    _abi_case(dev, b, h, s, s, d, "bf16", True, seed=37, scale=1.0 / np.sqrt(d))
+
+
 @pytest.mark.parametrize("d", [64, 128])
 def test_rising_scores_force_rescales(dev, d):
     """Scores that grow along the key axis raise every row's running max by far more than 2^8
