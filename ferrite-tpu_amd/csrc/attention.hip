@@ -880,14 +880,8 @@ struct FwdW {
   typedef PpVTile<D> VT;
   static constexpr int kSlots = 3;
   static constexpr int kLds = kSlots * (KT::kBytes + VT::kBytes);
-  // Who issues the ring's DMA, and when (measured on MI355X): with D = 128
-  // every wave issues its share right after the stage barrier; with D = 64
-  // the older half of the waves, which the SIMD arbiter favours and which
-  // therefore finish their stage first, issue all of it after their stage.
-  static constexpr bool kDmaLate = D == 64;
-  static constexpr int kDmaWaves = kDmaLate ? kWaves / 2 : kWaves;
-  static constexpr int kDma = KT::kBlocks / kDmaWaves;  // DMA instructions per tile and issuing wave
-  static constexpr int kAhead = 3;                      // fragments read ahead of their MFMAs
+  static constexpr int kDma = KT::kBlocks / kWaves;  // DMA instructions per tile and wave
+  static constexpr int kAhead = 3;                   // fragments read ahead of their MFMAs
   static_assert(KT::kBlocks == VT::kBlocks && kDma >= 1, "K and V tiles split evenly over the waves");
 };
 
@@ -922,13 +916,10 @@ __global__ __launch_bounds__((FwdW<D, RB>::kThreads), 1) void attn_fwd_sw_kernel
   const bf16* vb = v + (int64_t)bh * S * d;
 
   // K_0 and K_1 go out first; stage j then loads K_{j+3} and V_{j+1}.
-  const bool dma_wave = wave < F::kDmaWaves;
-  const PpDma<KT, true, F::kDmaWaves> kdma(wave % F::kDmaWaves, d);
-  const PpDma<VT, false, F::kDmaWaves> vdma(wave % F::kDmaWaves, d);
-  if (dma_wave) {
-    kdma.issue(kb, 0, S, d, kring);
-    if (1 < n) kdma.issue(kb, F::BK, S, d, kring + KT::kBytes);
-  }
+  const PpDma<KT, true, F::kWaves> kdma(wave, d);
+  const PpDma<VT, false, F::kWaves> vdma(wave, d);
+  kdma.issue(kb, 0, S, d, kring);
+  kdma.issue(kb, F::BK, S, d, kring + KT::kBytes);
 
   bf16x8 qf[RB][KS];
 #pragma unroll
@@ -968,14 +959,25 @@ __global__ __launch_bounds__((FwdW<D, RB>::kThreads), 1) void attn_fwd_sw_kernel
 
   // Stage j loads K_{j+3} and V_{j+1} into the slots that K_j and V_{j-2}
   // left at its barrier.
+  // Stage j loads K_{j+3} and V_{j+1} into the slots that K_j and V_{j-2}
+  // left at its barrier; this wave's instruction qd is block qd of its K
+  // share, then block qd - kDma of its V share. Issued unconditionally: a
+  // tile past the end has an empty buffer range, so its instructions read
+  // nothing and write zeros into a slot nobody reads again.
+  auto dma_part = [&](int j, int qd) {
+    if (qd < F::kDma)
+      kdma.issue_one(kdma.rsrc_of(kb, (j + 3) * F::BK, S, d), kring + ((j + 3) % F::kSlots) * KT::kBytes, qd);
+    else
+      vdma.issue_one(vdma.rsrc_of(vb, (j + 1) * F::BK, S, d), vring + ((j + 1) % F::kSlots) * VT::kBytes,
+                     qd - F::kDma);
+  };
   auto dma = [&](int j) {
-    if (!dma_wave) return;
-    if (j + 3 < n) kdma.issue(kb, (j + 3) * F::BK, S, d, kring + ((j + 3) % F::kSlots) * KT::kBytes);
-    if (j + 1 < n) vdma.issue(vb, (j + 1) * F::BK, S, d, vring + ((j + 1) % F::kSlots) * VT::kBytes);
+#pragma unroll
+    for (int qd = 0; qd < 2 * F::kDma; ++qd) dma_part(j, qd);
   };
 
   // Stage j with parity P = j & 1 (tile t lives in s[t & 1] and pf[t & 1]).
-  auto stage = [&](auto P_, auto QK_, auto SM_, auto MASK_, auto PV_, int j) {
+  auto stage = [&](auto P_, auto QK_, auto SM_, auto MASK_, auto PV_, int j) __attribute__((always_inline)) {
     constexpr int P = decltype(P_)::value;
     constexpr bool QK = decltype(QK_)::value, SM = decltype(SM_)::value;
     constexpr bool MASK = decltype(MASK_)::value, PV = decltype(PV_)::value;
@@ -1037,7 +1039,11 @@ __global__ __launch_bounds__((FwdW<D, RB>::kThreads), 1) void attn_fwd_sw_kernel
       // i % RB of fragment i / RB, the LDS read of the fragment kAhead
       // further on (at the fragment's first product) and an equal share of
       // the softmax elements, fenced so that the scheduler keeps it so.
+      // The stage's DMA instructions go out one at a time between products
+      // (issued together, the eight waves queue behind each other in the
+      // CU's vector memory path), with no branch in the fenced slots.
       constexpr int NM = NF * RB;
+      constexpr int NQ = 2 * F::kDma;
       static_assert(!SM || NE % NM == 0 || NM % NE == 0, "softmax elements spread evenly over the products");
       bf16x8 buf[NF];
 #pragma unroll
@@ -1047,6 +1053,9 @@ __global__ __launch_bounds__((FwdW<D, RB>::kThreads), 1) void attn_fwd_sw_kernel
       for (int i = 0; i < NM; ++i) {
         const int f = i / RB, rb = i % RB;
         if (rb == 0 && f + F::kAhead < NF) buf[f + F::kAhead] = read(f + F::kAhead);
+#pragma unroll
+        for (int qd = 0; qd < NQ; ++qd)
+          if (i == (2 * qd + 1) * NM / (2 * NQ)) dma_part(j, qd);
         prod1(f, rb, buf[f]);
         if constexpr (SM) {
           if constexpr (NE >= NM) {
@@ -1058,8 +1067,9 @@ __global__ __launch_bounds__((FwdW<D, RB>::kThreads), 1) void attn_fwd_sw_kernel
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-    } else if constexpr (SM) {
-      softmax(neg_m);
+    } else {
+      dma(j);
+      if constexpr (SM) softmax(neg_m);
     }
 
     if constexpr (SM) {
@@ -1104,77 +1114,62 @@ __global__ __launch_bounds__((FwdW<D, RB>::kThreads), 1) void attn_fwd_sw_kernel
   // The workgroup passes stages j = -1 .. n; sync(j) opens stage j.
   auto sync = [&](int j) {
     // This wave's parts of K_{j+1} and V_{j-1} have landed; the loads issued
-    // by stage j - 1 (K_{j+2}, then V_j) may still be in flight.
-    const bool k_prev = dma_wave && j + 2 < n, v_prev = dma_wave && j >= 0 && j < n;
-    if (k_prev && v_prev)
+    // by stage j - 1 (or K_1 of the prologue) may still be in flight.
+    if (j >= 0)
       wait_vmem<2 * F::kDma>();
-    else if (k_prev || v_prev)
-      wait_vmem<F::kDma>();
     else
-      wait_vmem<0>();
+      wait_vmem<F::kDma>();
     // Every wave's parts have landed and every wave has left stage j - 1.
     lds_barrier();
-    if (!F::kDmaLate) dma(j);
-  };
-  // Closes stage j.
-  auto close = [&](int j) {
-    if (F::kDmaLate) dma(j);
   };
   // This wave's stages: QK of tile 0; QK + softmax for tiles 0 .. n_w - 2
   // (with PV from tile 1 on); the diagonal tile's masked softmax; the last PV.
   sync(-1);
-  if (n_w > 0) stage(P1(), T_(), F_(), F_(), F_(), -1);
-  close(-1);
+  if (n_w > 0)
+    stage(P1(), T_(), F_(), F_(), F_(), -1);
+  else
+    dma(-1);
   int j = 0;
   if (n_w >= 2) {
     sync(0);
     stage(P0(), T_(), T_(), F_(), F_(), 0);
-    close(0);
     for (j = 1; j + 2 < n_w; j += 2) {
       sync(j);
       stage(P1(), T_(), T_(), F_(), T_(), j);
-      close(j);
       sync(j + 1);
       stage(P0(), T_(), T_(), F_(), T_(), j + 1);
-      close(j + 1);
     }
     if (j + 1 < n_w) {
       sync(j);
       stage(P1(), T_(), T_(), F_(), T_(), j);
-      close(j);
       ++j;
     }
   }
   if (n_w == 1) {
     sync(0);
     stage(P0(), F_(), T_(), T_(), F_(), 0);
-    close(0);
     sync(1);
     stage(P1(), F_(), F_(), F_(), T_(), 1);
-    close(1);
     j = 2;
   } else if (n_w >= 2) {
     if (j & 1) {
       sync(j);
       stage(P1(), F_(), T_(), T_(), T_(), j);
-      close(j);
       sync(j + 1);
       stage(P0(), F_(), F_(), F_(), T_(), j + 1);
-      close(j + 1);
     } else {
       sync(j);
       stage(P0(), F_(), T_(), T_(), T_(), j);
-      close(j);
       sync(j + 1);
       stage(P1(), F_(), F_(), F_(), T_(), j + 1);
-      close(j + 1);
     }
     j += 2;
   }
   for (; j <= n; ++j) {
     sync(j);
-    close(j);
+    dma(j);
   }
+  wait_vmem<0>();
 
   if (n_w == 0) return;
 #pragma unroll
