@@ -465,6 +465,13 @@ extern "C" int ferrite_hip_matmul(const void* x, const void* y, void* out, int64
     if (out_dtype == FERRITE_BF16) return launch_gemm<bf16, bf16, 256, 256, 64, 2, 2>(x, y, out, m, n, k, s);
     return launch_gemm<bf16, float, 256, 256, 64, 2, 2>(x, y, out, m, n, k, s);
   }
+  // f32: 128 x 128 tiles of four waves reach ~80% of the fp32 MFMA peak at 4096^3; a
+  // problem with fewer such tiles than CUs (1000^3 has 64) runs 64 x 64 tiles of two
+  // waves instead, four times the workgroups (1000^3: 81 -> 50 us on MI355X).
+  if (cdiv(m, (int64_t)128) * cdiv(n, (int64_t)128) < 256) {
+    if (out_dtype == FERRITE_BF16) return launch_gemm<float, bf16, 64, 64, 32, 1, 2>(x, y, out, m, n, k, s);
+    return launch_gemm<float, float, 64, 64, 32, 1, 2>(x, y, out, m, n, k, s);
+  }
   if (out_dtype == FERRITE_BF16) return launch_gemm<float, bf16, 128, 128, 32, 2, 2>(x, y, out, m, n, k, s);
   return launch_gemm<float, float, 128, 128, 32, 2, 2>(x, y, out, m, n, k, s);
 }
