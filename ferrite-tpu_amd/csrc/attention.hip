@@ -1814,6 +1814,276 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_pp_kernel(const bf16* __restr
   store_acc_rows<bf16, D, true>(dva, dv + (int64_t)bh * Sk * d, kvrow, Sk, d, 1.0f);
 }
 
+// dK, dV, software-pipelined (the forward's scheme). Half-step h of a wave
+// (32 queries) first issues dV^T += dO^T P and dK^T += Q^T dS for half h - 1
+// and turns the S and dP of half h into P and dS on the VALU between those
+// products, then issues S = Q K^T and dP = dO V^T for half h + 1 into the same
+// S / dP registers. The program order is the schedule: slot i holds one
+// product, the LDS read of the product kAhead further on, a share of the VALU
+// work and a share of the DMA, and a scheduling fence closes it. One
+// workgroup barrier per 64-query tile (at odd half-steps); the DMA of tile
+// t + 3 goes out during the two half-steps after the barrier that frees its
+// slot.
+template <int D>
+__global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                            const bf16* __restrict__ v, const bf16* __restrict__ dout,
+                                                            const float* __restrict__ lse,
+                                                            const float* __restrict__ delta, bf16* __restrict__ dk,
+                                                            bf16* __restrict__ dv, int bh_count, int Sq, int Sk, int d,
+                                                            int causal, float scale, float scale_log2) {
+  typedef DkvPp<D> F;
+  typedef typename F::Tile Tile;
+  constexpr int KS = F::KS, DT = F::DT;
+  constexpr int kAhead = 3;
+  // Per wave and tile: Q blocks, dO blocks, lse, delta (every wave loads the
+  // two 256-byte statistics rows into the same place, so the count is uniform).
+  constexpr int kTileDma = 2 * F::kDma + 2;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  // Heaviest (first) key blocks first.
+  const int bh = blockIdx.x % bh_count;
+  const int kt = (int)(blockIdx.x / bh_count);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int k0 = kt * F::BKV;
+  const int k0w = k0 + 32 * wave;
+  const int kvrow = k0w + l32;
+
+  const bf16* qb = q + (int64_t)bh * Sq * d;
+  const bf16* dob = dout + (int64_t)bh * Sq * d;
+  const bf16* kb = k + (int64_t)bh * Sk * d;
+  const bf16* vb = v + (int64_t)bh * Sk * d;
+  const float* lseb = lse + (int64_t)bh * Sq;
+  const float* db = delta + (int64_t)bh * Sq;
+
+  // Query tiles first .. first + nt - 1 (tile t in ring slot t % kSlots),
+  // halves 0 .. nh - 1 (half x: tile x / 2, queries 32 (x % 2) .. of it).
+  const int first = causal ? k0 / F::BQ : 0;
+  const int nt = (Sq + F::BQ - 1) / F::BQ - first;
+  const int nh = 2 * nt;
+
+  bf16x8 kf[KS], vf[KS];
+  load_row_frags<bf16, D, true, false>(kf, kb, k0w, Sk, d);
+  load_row_frags<bf16, D, true, false>(vf, vb, k0w, Sk, d);
+
+  const PpDma<Tile, true> dma(wave, d);
+  auto slot = [&](int t) { return smem + (t % F::kSlots) * F::kSlotBytes; };
+  // DMA instruction qd of tile t. Tiles past the end have an empty buffer
+  // range: they read nothing and write zeros into a slot nobody reads again.
+  auto dma_part = [&](int t, int qd) {
+    char* sl = slot(t);
+    const int r0 = (first + t) * F::BQ;
+    if (qd < F::kDma)
+      dma.issue_one(dma.rsrc_of(qb, r0, Sq, d), sl, qd);
+    else if (qd < 2 * F::kDma)
+      dma.issue_one(dma.rsrc_of(dob, r0, Sq, d), sl + Tile::kBytes, qd - F::kDma);
+    else if (qd == 2 * F::kDma)
+      stat_dma(lseb, r0, Sq, sl + 2 * Tile::kBytes);
+    else
+      stat_dma(db, r0, Sq, sl + 2 * Tile::kBytes + 1024);
+  };
+  // Tiles 0 and 1 first; the two half-steps after barrier t load tile t + 3.
+#pragma unroll
+  for (int qd = 0; qd < kTileDma; ++qd) dma_part(0, qd);
+#pragma unroll
+  for (int qd = 0; qd < kTileDma; ++qd) dma_part(1, qd);
+
+  f32x16 dka[DT], dva[DT];
+#pragma unroll
+  for (int u = 0; u < DT; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dka[u][r] = 0.f;
+      dva[u][r] = 0.f;
+    }
+  const int rbase = Tile::row_base(lane);
+  const int tbase = Tile::tr_base(lane);
+
+  f32x16 sa, dpa;               // S and dP of one half (register r: query 16 g + r, key kvrow)
+  bf16x8 pf[2][2], dsf[2][2];  // [half parity][8-query chunk]: P and dS fragments
+
+  // Half-step h with parity P = h & 1.
+  auto stage = [&](auto P_, auto SDP_, auto SG_, auto MASK_, auto GRAD_, int h) __attribute__((always_inline)) {
+    constexpr int P = decltype(P_)::value;
+    constexpr bool SDP = decltype(SDP_)::value, SG = decltype(SG_)::value;
+    constexpr bool MASK = decltype(MASK_)::value, GRAD = decltype(GRAD_)::value;
+    f32x16& sn = sa;
+    f32x16& dpn = dpa;
+    const f32x16& sc = sa;
+    const f32x16& dpc = dpa;
+    bf16x8(&pc)[2] = pf[P];
+    bf16x8(&dsc)[2] = dsf[P];
+    const bf16x8(&pp)[2] = pf[1 - P];
+    const bf16x8(&dsp)[2] = dsf[1 - P];
+    // Tiles and halves: SDP reads half h + 1, SG half h, GRAD half h - 1.
+    const char* sl_n = slot((h + 1) >> 1);
+    const int half_n = (h + 1) & 1;
+    const char* sl_c = slot(h >> 1);
+    const int half_c = h & 1;
+    const char* sl_p = slot((h - 1) >> 1);
+    const int half_p = (h - 1) & 1;
+    constexpr int NS = SDP ? 2 * KS : 0;  // S (even) and dP (odd) products over the k-chunks
+    constexpr int NG = GRAD ? 4 * DT : 0;  // per output tile: two key chunks, dV (even) and dK (odd)
+    constexpr int NF = NS + NG;
+    // Products 0 .. NG - 1 are GRAD, then NS SDP products (which overwrite S
+    // and dP only after the softmax gradient has read them).
+    auto which = [](int f, int& i) -> bool {  // true: SDP product i, false: GRAD product i
+      if (f < NG) {
+        i = f;
+        return false;
+      }
+      i = f - NG;
+      return true;
+    };
+    auto read = [&](int f) -> bf16x8 {
+      int i;
+      if (which(f, i))
+        return *reinterpret_cast<const bf16x8*>(sl_n + ((i & 1) ? Tile::kBytes : 0) + rbase +
+                                                Tile::row_at(half_n, i >> 1));
+      return tr_frag(sl_p + ((i & 1) ? 0 : Tile::kBytes) + tbase + Tile::tr_at(half_p, (i >> 1) & 1, i >> 2),
+                     Tile::kTrHi);
+    };
+    auto prod = [&](int f, const bf16x8& a) {
+      int i;
+      if (which(f, i)) {
+        if (i < 2) {
+          if (i & 1)
+            dpn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, vf[0], f32x16{}, 0, 0, 0);
+          else
+            sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kf[0], f32x16{}, 0, 0, 0);
+        } else if (i & 1) {
+          mma32(a, vf[i >> 1], dpn);
+        } else {
+          mma32(a, kf[i >> 1], sn);
+        }
+      } else {
+        const int u = i >> 2, hh = (i >> 1) & 1;
+        if (i & 1)
+          mma32(a, dsp[hh], dka[u]);
+        else
+          mma32(a, pp[hh], dva[u]);
+      }
+    };
+    // Softmax gradient of half h: element r (query 16 g + r of the half).
+    const float* st = reinterpret_cast<const float*>(sl_c + 2 * Tile::kBytes) + 32 * half_c + 16 * g;
+    const int qh = (first + (h >> 1)) * F::BQ + 32 * half_c + 16 * g;
+    // lse and delta of queries 4 c .. 4 c + 3, read one group ahead of use.
+    f32x4 ls[2], dl[2];
+    auto read_stats = [&](int c) {
+      ls[c & 1] = *reinterpret_cast<const f32x4*>(st + 4 * c);
+      dl[c & 1] = *reinterpret_cast<const f32x4*>(st + 256 + 4 * c);
+    };
+    float pv[8], dsv[8];
+    auto sg_elem = [&](int r) {
+      if ((r & 3) == 0 && (r >> 2) + 1 < 4) read_stats((r >> 2) + 1);
+      const f32x4& l4 = ls[(r >> 2) & 1];
+      const f32x4& d4 = dl[(r >> 2) & 1];
+      float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, -l4[r & 3] * kLog2e));
+      if constexpr (MASK) p = (causal && kvrow > qh + r) ? 0.f : p;
+      pv[r & 7] = p;
+      dsv[r & 7] = p * (dpc[r] - d4[r & 3]);
+      if ((r & 7) == 7) {
+        to_frag(pv, pc[r >> 3]);
+        to_frag(dsv, dsc[r >> 3]);
+        pin(pc[r >> 3]);
+        pin(dsc[r >> 3]);
+      }
+    };
+    // DMA share: odd half-steps the first half of tile (h + 5) / 2's
+    // instructions, even half-steps the rest.
+    const int tdma = (h + 5) >> 1;
+    constexpr int QD0 = P ? 0 : kTileDma / 2;
+    constexpr int NQ = P ? kTileDma / 2 : kTileDma - kTileDma / 2;
+
+    if constexpr (SG) read_stats(0);
+    if constexpr (SG && NG == 0) {
+      // No GRAD products to hide it behind: the softmax gradient first.
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sg_elem(r);
+    }
+    if constexpr (NF > 0) {
+      bf16x8 buf[NF];
+#pragma unroll
+      for (int f = 0; f < kAhead && f < NF; ++f) buf[f] = read(f);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        if (f + kAhead < NF) buf[f + kAhead] = read(f + kAhead);
+#pragma unroll
+        for (int qd = 0; qd < NQ; ++qd)
+          if (f == (2 * qd + 1) * NF / (2 * NQ)) dma_part(tdma, QD0 + qd);
+        prod(f, buf[f]);
+        if constexpr (SG && NG > 0) {
+          // 16 elements over the NG GRAD products
+          if (f < NG) {
+            if constexpr (NG >= 16) {
+              if (f % (NG / 16) == 0) sg_elem(f / (NG / 16));
+            } else {
+#pragma unroll
+              for (int r = f * (16 / NG); r < (f + 1) * (16 / NG); ++r) sg_elem(r);
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int qd = 0; qd < NQ; ++qd) dma_part(tdma, QD0 + qd);
+    }
+  };
+
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  // Barrier t opens half-step 2t + 1: this wave's part of tile t + 1 has
+  // landed (tile t + 2 may be in flight) and every wave has finished half-step
+  // 2t, the last to read tile t - 1, whose slot now takes tile t + 3.
+  auto sync_tile = [&]() {
+    wait_vmem<kTileDma>();
+    lds_barrier();
+  };
+  // Half-step h: SDP for h + 1 < nh, SG for 0 <= h < nh, GRAD for 1 <= h <= nh
+  // (nh is even and >= 2). The causal mask can only touch halves 0 .. 3 of
+  // the sweep (the diagonal block): the first half-steps apply it on every
+  // wave, where it is a no-op for halves below the wave's keys.
+  sync_tile();
+  stage(P1(), T_(), F_(), F_(), F_(), -1);
+  stage(P0(), T_(), T_(), T_(), F_(), 0);
+  sync_tile();
+  if (nh == 2) {
+    stage(P1(), F_(), T_(), T_(), T_(), 1);
+    stage(P0(), F_(), F_(), F_(), T_(), 2);
+  } else {
+    stage(P1(), T_(), T_(), T_(), T_(), 1);
+    stage(P0(), T_(), T_(), T_(), T_(), 2);
+    sync_tile();
+    if (nh == 4) {
+      stage(P1(), F_(), T_(), T_(), T_(), 3);
+      stage(P0(), F_(), F_(), F_(), T_(), 4);
+    } else {
+      stage(P1(), T_(), T_(), T_(), T_(), 3);
+      stage(P0(), T_(), T_(), F_(), T_(), 4);
+      // Full, unmasked half-steps in pairs, then the last two.
+      int h = 5;
+      for (; h + 1 <= nh - 2; h += 2) {
+        sync_tile();
+        stage(P1(), T_(), T_(), F_(), T_(), h);
+        stage(P0(), T_(), T_(), F_(), T_(), h + 1);
+      }
+      sync_tile();
+      stage(P1(), F_(), T_(), F_(), T_(), nh - 1);
+      stage(P0(), F_(), F_(), F_(), T_(), nh);
+    }
+  }
+  wait_vmem<0>();
+
+  if (k0w >= Sk) return;
+  store_acc_rows<bf16, D, true>(dka, dk + (int64_t)bh * Sk * d, kvrow, Sk, d, scale);
+  store_acc_rows<bf16, D, true>(dva, dv + (int64_t)bh * Sk * d, kvrow, Sk, d, 1.0f);
+}
+
 template <int D>
 struct DqPp {
   static constexpr int kWaves = 8, kThreads = 64 * kWaves;
@@ -2132,7 +2402,7 @@ int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout,
   const int64_t nk = cdiv(s.sk, F::BKV);
   const int64_t bh = s.b * s.h;
   if (nk * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dkv: grid too large");
-  auto kern = attn_dkv_pp_kernel<D>;
+  auto kern = attn_dkv_sw_kernel<D>;
   set_lds(kern, F::kLds);
   hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
