@@ -1569,251 +1569,6 @@ __device__ __forceinline__ void stat_dma(const float* base, int r0, int nrows, c
                : "memory", "m0");
 }
 
-// dK, dV for 128 keys (32 per wave, K and V fragments in registers), sweeping
-// 64-query tiles from the diagonal on. Each tile is processed in two halves of
-// 32 queries; the S / dP products of the next half are issued while the VALU
-// turns the current half into P and dS, then dV^T += dO^T P and
-// dK^T += Q^T dS run from transposed reads of the same tiles.
-template <int D>
-__global__ __launch_bounds__(256, 1) void attn_dkv_pp_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
-                                                            const bf16* __restrict__ v, const bf16* __restrict__ dout,
-                                                            const float* __restrict__ lse,
-                                                            const float* __restrict__ delta, bf16* __restrict__ dk,
-                                                            bf16* __restrict__ dv, int bh_count, int Sq, int Sk, int d,
-                                                            int causal, float scale, float scale_log2) {
-  typedef DkvPp<D> F;
-  typedef typename F::Tile Tile;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-
-  // Heaviest (first) key blocks first.
-  const int bh = blockIdx.x % bh_count;
-  const int kt = (int)(blockIdx.x / bh_count);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int l32 = lane & 31, g = lane >> 5;
-  const int k0 = kt * F::BKV;
-  const int k0w = k0 + 32 * wave;
-  const int kvrow = k0w + l32;
-
-  const bf16* qb = q + (int64_t)bh * Sq * d;
-  const bf16* dob = dout + (int64_t)bh * Sq * d;
-  const bf16* kb = k + (int64_t)bh * Sk * d;
-  const bf16* vb = v + (int64_t)bh * Sk * d;
-  const float* lseb = lse + (int64_t)bh * Sq;
-  const float* db = delta + (int64_t)bh * Sq;
-
-  // Query tiles first .. first + nt - 1; tile t lives in ring slot t % kSlots.
-  const int first = causal ? k0 / F::BQ : 0;
-  const int nt = (Sq + F::BQ - 1) / F::BQ - first;
-
-  bf16x8 kf[F::KS], vf[F::KS];
-  load_row_frags<bf16, D, true, false>(kf, kb, k0w, Sk, d);
-  load_row_frags<bf16, D, true, false>(vf, vb, k0w, Sk, d);
-
-  const PpDma<Tile, true> dma(wave, d);
-  auto slot = [&](int t) { return smem + (t % F::kSlots) * F::kSlotBytes; };
-  auto issue_tile = [&](int t) {
-    char* sl = slot(t);
-    const int r0 = (first + t) * F::BQ;
-    dma.issue(qb, r0, Sq, d, sl);
-    dma.issue(dob, r0, Sq, d, sl + Tile::kBytes);
-    if (wave == 0) {
-      stat_dma(lseb, r0, Sq, sl + 2 * Tile::kBytes);
-      stat_dma(db, r0, Sq, sl + 2 * Tile::kBytes + 1024);
-    }
-  };
-  // The same loads in five parts (Q blocks 0-1, 2-3, dO blocks 0-1, 2-3,
-  // lse and delta), issued at different points of a tile so that the four
-  // waves do not queue 34 loads on the address unit at once.
-  auto issue_part = [&](int t, int part) {
-    char* sl = slot(t);
-    const int r0 = (first + t) * F::BQ;
-    if (part < 4) {
-      const bf16* base = part < 2 ? qb : dob;
-      char* lds = sl + (part < 2 ? 0 : Tile::kBytes);
-      const u32x4 rs = dma.rsrc_of(base, r0, Sq, d);
-      dma.issue_one(rs, lds, 2 * (part & 1));
-      dma.issue_one(rs, lds, 2 * (part & 1) + 1);
-    } else if (wave == 0) {
-      stat_dma(lseb, r0, Sq, sl + 2 * Tile::kBytes);
-      stat_dma(db, r0, Sq, sl + 2 * Tile::kBytes + 1024);
-    }
-  };
-  // The wave's loads for `tiles` more tiles may stay in flight.
-  auto wait_tiles = [&](int tiles) {
-    if (wave == 0) {
-      if (tiles >= 2) wait_vmem<2 * (2 * F::kDma + 2)>();
-      else if (tiles == 1) wait_vmem<2 * F::kDma + 2>();
-      else wait_vmem<0>();
-    } else {
-      if (tiles >= 2) wait_vmem<2 * (2 * F::kDma)>();
-      else if (tiles == 1) wait_vmem<2 * F::kDma>();
-      else wait_vmem<0>();
-    }
-  };
-
-  if (nt > 0) issue_tile(0);
-  if (nt > 1) issue_tile(1);
-  if (nt > 2) issue_tile(2);
-
-  f32x16 dka[F::DT], dva[F::DT];
-#pragma unroll
-  for (int u = 0; u < F::DT; ++u)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      dka[u][r] = 0.f;
-      dva[u][r] = 0.f;
-    }
-
-  const int rb = Tile::row_base(lane);
-  const int tb = Tile::tr_base(lane);
-
-  // P and dS of a half from its S and dP (MASK: zero above the diagonal).
-  auto softmax_grad = [&](const char* sl, int qt0, int half, const f32x16& s, const f32x16& dp, bf16x8 (&pf)[2],
-                          bf16x8 (&dsf)[2], auto mask_c) {
-    constexpr bool MASK = decltype(mask_c)::value;
-    const float* st = reinterpret_cast<const float*>(sl + 2 * Tile::kBytes) + 32 * half + 16 * g;
-    const int qh = qt0 + 32 * half + 16 * g;
-    float p[16], ds[16];
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const f32x4 ls = *reinterpret_cast<const f32x4*>(st + 4 * r4);
-      const f32x4 dl = *reinterpret_cast<const f32x4*>(st + 256 + 4 * r4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 4 * r4 + e;
-        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], scale_log2, -ls[e] * kLog2e));
-        if constexpr (MASK) pv = kvrow > qh + r ? 0.f : pv;
-        p[r] = pv;
-        ds[r] = pv * (dp[r] - dl[e]);
-      }
-    }
-    to_frag(p, pf[0]);
-    to_frag(p + 8, pf[1]);
-    to_frag(ds, dsf[0]);
-    to_frag(ds + 8, dsf[1]);
-  };
-
-  // S = Q K^T and dP = dO V^T for half `half` of the tile at `sl` (s[r] /
-  // dp[r] is query 32 half + 16 g + r of the tile, key kvrow), with the
-  // VALU work `valu` spread between the products. Row fragments are read
-  // kBwdAhead products ahead.
-  constexpr int kBwdAhead = 6;
-  auto sdp = [&](const char* sl, int half, f32x16& s, f32x16& dp, auto&& valu) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[r] = 0.f;
-      dp[r] = 0.f;
-    }
-    const char* qp = sl + rb;
-    const char* dp_ = sl + Tile::kBytes + rb;
-    auto read = [&](int i) {
-      return *reinterpret_cast<const bf16x8*>(((i & 1) ? dp_ : qp) + Tile::row_at(half, i >> 1));
-    };
-    constexpr int N = 2 * F::KS;  // S and dP products alternate over the k-chunks
-    bf16x8 buf[N];
-#pragma unroll
-    for (int i = 0; i < kBwdAhead; ++i) buf[i] = read(i);
-    valu();
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      if (i + kBwdAhead < N) buf[i + kBwdAhead] = read(i + kBwdAhead);
-      if (i & 1)
-        mma32(buf[i], vf[i >> 1], dp);
-      else
-        mma32(buf[i], kf[i >> 1], s);
-    }
-#pragma unroll
-    for (int i = 0; i < kBwdAhead; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (i + kBwdAhead < N) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
-    }
-  };
-
-  // dV^T += dO^T P, dK^T += Q^T dS for half `half` of the tile at `sl`;
-  // transposed fragments (two reads each) kBwdAheadTr products ahead.
-  constexpr int kBwdAheadTr = 4;
-  auto grad_kv = [&](const char* sl, int half, const bf16x8 (&pf)[2], const bf16x8 (&dsf)[2]) {
-    const char* qp = sl + tb;
-    const char* dp_ = sl + Tile::kBytes + tb;
-    // Product i: output tile u = i / 4, key chunk h = (i / 2) % 2; even: dV, odd: dK.
-    auto read = [&](int i) {
-      return tr_frag(((i & 1) ? qp : dp_) + Tile::tr_at(half, (i >> 1) & 1, i >> 2), Tile::kTrHi);
-    };
-    constexpr int N = 4 * F::DT;  // per output tile: two key chunks, dV and dK
-    bf16x8 buf[N];
-#pragma unroll
-    for (int i = 0; i < kBwdAheadTr; ++i) buf[i] = read(i);
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      if (i + kBwdAheadTr < N) buf[i + kBwdAheadTr] = read(i + kBwdAheadTr);
-      const int u = i >> 2, h = (i >> 1) & 1;
-      if (i & 1)
-        mma32(buf[i], dsf[h], dka[u]);
-      else
-        mma32(buf[i], pf[h], dva[u]);
-    }
-#pragma unroll
-    for (int i = 0; i < kBwdAheadTr; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (i + kBwdAheadTr < N) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-  };
-
-  f32x16 s0, dp0, s1, dp1;
-  bf16x8 pf[2], dsf[2];
-  auto nop = [] {};
-  if (nt > 0) {
-    wait_tiles(nt - 1 < 2 ? nt - 1 : 2);
-    lds_barrier();
-    sdp(slot(0), 0, s0, dp0, nop);
-  }
-  for (int t = 0; t < nt; ++t) {
-    const char* sl = slot(t);
-    const int qt0 = (first + t) * F::BQ;
-    // The causal mask touches only the halves that reach the diagonal.
-    const bool mask0 = causal && qt0 < k0w + 31;
-    const bool mask1 = causal && qt0 + 32 < k0w + 31;
-    // Half 0: P / dS between the S / dP products of half 1.
-    if (t > 0 && t + 2 < nt) {
-      issue_part(t + 2, 3);
-      issue_part(t + 2, 4);
-    }
-    if (mask0)
-      sdp(sl, 1, s1, dp1, [&] { softmax_grad(sl, qt0, 0, s0, dp0, pf, dsf, std::true_type{}); });
-    else
-      sdp(sl, 1, s1, dp1, [&] { softmax_grad(sl, qt0, 0, s0, dp0, pf, dsf, std::false_type{}); });
-    grad_kv(sl, 0, pf, dsf);
-    // Half 1, with the products of the next tile's first half.
-    if (t + 1 < nt) {
-      wait_tiles(t + 2 < nt ? 1 : 0);
-      lds_barrier();
-      if (t + 3 < nt) issue_part(t + 3, 0);
-      if (mask1)
-        sdp(slot(t + 1), 0, s0, dp0, [&] { softmax_grad(sl, qt0, 1, s1, dp1, pf, dsf, std::true_type{}); });
-      else
-        sdp(slot(t + 1), 0, s0, dp0, [&] { softmax_grad(sl, qt0, 1, s1, dp1, pf, dsf, std::false_type{}); });
-      if (t + 3 < nt) issue_part(t + 3, 1);
-    } else {
-      if (mask1)
-        softmax_grad(sl, qt0, 1, s1, dp1, pf, dsf, std::true_type{});
-      else
-        softmax_grad(sl, qt0, 1, s1, dp1, pf, dsf, std::false_type{});
-    }
-    grad_kv(sl, 1, pf, dsf);
-    if (t + 3 < nt) issue_part(t + 3, 2);
-  }
-
-  if (k0w >= Sk) return;
-  store_acc_rows<bf16, D, true>(dka, dk + (int64_t)bh * Sk * d, kvrow, Sk, d, scale);
-  store_acc_rows<bf16, D, true>(dva, dv + (int64_t)bh * Sk * d, kvrow, Sk, d, 1.0f);
-}
-
 // dK, dV, software-pipelined (the forward's scheme). Half-step h of a wave
 // (32 queries) first issues dV^T += dO^T P and dK^T += Q^T dS for half h - 1
 // and turns the S and dP of half h into P and dS on the VALU between those
