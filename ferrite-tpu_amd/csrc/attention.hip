@@ -31,6 +31,7 @@
 //    quantity, p stays <= 256, and the O rescale is skipped on almost every
 //    tile.
 //  * lse and delta are compact f32 [B, H, S].
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -871,10 +872,10 @@ __device__ __forceinline__ void pin(bf16x8& f) {
   f = __builtin_bit_cast(bf16x8, w);
 }
 
-template <int D, int RB>
+template <int D, int RB, int W>
 struct FwdW {
-  static constexpr int kWaves = 8 / RB, kThreads = 64 * kWaves;
-  static constexpr int BQ = 256, BK = 64;
+  static constexpr int kWaves = W, kThreads = 64 * kWaves;
+  static constexpr int BQ = 32 * RB * W, BK = 64;
   static constexpr int KS = D / 16, DT = D / 32;
   typedef PpKTile<D> KT;
   typedef PpVTile<D> VT;
@@ -885,11 +886,11 @@ struct FwdW {
   static_assert(KT::kBlocks == VT::kBlocks && kDma >= 1, "K and V tiles split evenly over the waves");
 };
 
-template <int D, int RB>
-__global__ __launch_bounds__((FwdW<D, RB>::kThreads), 1) void attn_fwd_sw_kernel(
+template <int D, int RB, int W, bool ZIG>
+__global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void attn_fwd_sw_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, bf16* __restrict__ o,
     float* __restrict__ lse, int bh_count, int S, int d, float scale_log2, int neg_q, int n_qtiles) {
-  typedef FwdW<D, RB> F;
+  typedef FwdW<D, RB, W> F;
   typedef typename F::KT KT;
   typedef typename F::VT VT;
   constexpr int KS = F::KS, DT = F::DT;
@@ -899,8 +900,12 @@ __global__ __launch_bounds__((FwdW<D, RB>::kThreads), 1) void attn_fwd_sw_kernel
 
   // Heaviest (last) query tiles first; all tiles of one head share an XCD
   // when bh_count is a multiple of 8.
+  // ZIG: the second half of the tiles in rising order, for a grid that is
+  // resident all at once (block b and block b + grid / 2 share a CU).
   const int bh = blockIdx.x % bh_count;
-  const int qt = n_qtiles - 1 - (int)(blockIdx.x / bh_count);
+  const int blk = (int)(blockIdx.x / bh_count);
+  const int half_q = n_qtiles / 2;
+  const int qt = !ZIG ? n_qtiles - 1 - blk : blk < n_qtiles - half_q ? n_qtiles - 1 - blk : blk - (n_qtiles - half_q);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
@@ -2035,6 +2040,20 @@ void set_lds(K kernel, int bytes) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Compute units of the current device, looked up once per device. Racing
+// first calls store the same value.
+int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 struct Shape {
   int64_t b, h, sq, sk, d;
 };
@@ -2062,14 +2081,14 @@ int check_shape(const char* name, const Shape& s, int dtype, int causal, bool bw
 
 int pad_dim(int64_t d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
 
-template <int D, int RB = 1>
+template <int D, int RB = 1, int W = 8, bool ZIG = false>
 int fwd_sw_launch(const void* q, const void* k, const void* v, void* o, float* lse, const Shape& s, float c, int neg_q,
                   hipStream_t stream) {
-  typedef FwdW<D, RB> F;
+  typedef FwdW<D, RB, W> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: grid too large");
-  auto kern = attn_fwd_sw_kernel<D, RB>;
+  auto kern = attn_fwd_sw_kernel<D, RB, W, ZIG>;
   set_lds(kern, F::kLds);
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<bf16*>(o), lse, (int)bh,
@@ -2108,7 +2127,21 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
   const int neg_q = c < 0.f;
   c = fmaxf(fabsf(c), 1e-30f);
   if constexpr (sizeof(T) == 2 && AL && D <= 128) {
-    if (causal && s.sq == s.sk && s.sq % 64 == 0) return fwd_sw_launch<D>(q, k, v, o, lse, s, c, neg_q, stream);
+    if (causal && s.sq == s.sk && s.sq % 64 == 0) {
+      if constexpr (D == 64) {
+        // 128-row workgroups of 4 waves, two per CU (51 KB of LDS each): the
+        // two workgroups on a CU hide each other's barriers and tails. When
+        // the whole grid is resident at once, the second half of the grid
+        // takes the light tiles in rising order so that each CU pairs a long
+        // and a short tile (1x8x8192x64: 120 -> 91 us on MI355X).
+        typedef FwdW<64, 1, 4> F4;
+        const bool one_round = cdiv(s.sq, F4::BQ) * s.b * s.h <= 2 * (int64_t)cu_count();
+        return one_round ? fwd_sw_launch<D, 1, 4, true>(q, k, v, o, lse, s, c, neg_q, stream)
+                         : fwd_sw_launch<D, 1, 4, false>(q, k, v, o, lse, s, c, neg_q, stream);
+      } else {
+        return fwd_sw_launch<D>(q, k, v, o, lse, s, c, neg_q, stream);
+      }
+    }
     return fwd_pp_launch<D>(q, k, v, o, lse, s, causal, c, neg_q, stream);
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(kThreads), F::kLds, stream, static_cast<const T*>(q),
