@@ -51,7 +51,7 @@ __device__ __forceinline__ int perm_row(int r) {
 
 // Inverse of perm_row: the logical row held by physical row `p` (bits 4,3,2 of
 // the row inside its 32-row block rotate the other way).
-__device__ __forceinline__ int perm_src(int p) {
+__host__ __device__ constexpr int perm_src(int p) {
   return (p & ~31) | (((p >> 2) & 1) << 4) | (((p >> 4) & 1) << 3) | (((p >> 3) & 1) << 2) | (p & 3);
 }
 
@@ -501,7 +501,7 @@ struct PpKTile {
   }
   static __host__ __device__ constexpr int block_off(int b) { return b * kStride; }
   // Row that lane L of the instruction filling block b loads.
-  static __device__ __forceinline__ int dma_row(int b, int L) { return b + (L / kChunks) * kBlocks; }
+  static __host__ __device__ constexpr int dma_row(int b, int L) { return b + (L / kChunks) * kBlocks; }
   static __device__ __forceinline__ bool dma_lane(int) { return true; }
 };
 
@@ -522,7 +522,7 @@ struct PpVTile {
     return ((r & 3) + 4 * (r / (4 * kRowsPerBlock))) * kStride + ((r >> 2) % kRowsPerBlock) * kRowBytes + byte;
   }
   static __host__ __device__ constexpr int block_off(int b) { return b * kStride; }
-  static __device__ __forceinline__ int dma_row(int b, int L) {
+  static __host__ __device__ constexpr int dma_row(int b, int L) {
     return (b & 3) + 4 * (L / kChunks) + 4 * kRowsPerBlock * (b >> 2);
   }
   static __device__ __forceinline__ bool dma_lane(int) { return true; }
@@ -530,21 +530,27 @@ struct PpVTile {
 
 // One wave's share of the DMA of a 64-row bf16 tile with d == D: GROUP waves
 // split the blocks, wave gw taking blocks gw + GROUP i. PERM loads physical
-// row r from logical row perm_src(r).
+// row r from logical row perm_src(r). A lane's source row for instruction i is
+// its row for instruction 0 plus a wave- and lane-independent delta (the bits
+// that i sets are disjoint from the wave's and the lane's, and perm_src only
+// permutes bits), so one VGPR offset serves all instructions; instruction i
+// moves the buffer window instead: base + delta, range - delta.
 template <class Layout, bool PERM, int GROUP = 4>
 struct PpDma {
   static constexpr int kPerWave = Layout::kBlocks / GROUP;
-  uint32_t voff[kPerWave];
+  uint32_t voff;
   int gw;
+
+  static constexpr int delta_rows(int i) {
+    return PERM ? perm_src(Layout::dma_row(GROUP * i, 0)) - perm_src(Layout::dma_row(0, 0))
+                : Layout::dma_row(GROUP * i, 0) - Layout::dma_row(0, 0);
+  }
 
   __device__ __forceinline__ PpDma(int gw_, int d) : gw(gw_) {
     const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int i = 0; i < kPerWave; ++i) {
-      const int r = Layout::dma_row(gw + GROUP * i, lane);
-      const int src = PERM ? perm_src(r) : r;
-      voff[i] = Layout::dma_lane(lane) ? (uint32_t)((src * d + (lane % Layout::kChunks) * 8) * 2) : 0x80000000u;
-    }
+    const int r = Layout::dma_row(gw, lane);
+    const int src = PERM ? perm_src(r) : r;
+    voff = Layout::dma_lane(lane) ? (uint32_t)((src * d + (lane % Layout::kChunks) * 8) * 2) : 0x80000000u;
   }
 
   // Buffer descriptor of rows [r0, nrows) of `base` (rows past nrows read as zeros).
@@ -555,11 +561,13 @@ struct PpDma {
                  (uint32_t)__builtin_amdgcn_readfirstlane((int)((addr >> 32) & 0xffffu)),
                  (uint32_t)__builtin_amdgcn_readfirstlane(rows_left * d * 2), 0x00020000u};
   }
-  // The i-th of this wave's instructions for the tile at `lds`.
-  __device__ __forceinline__ void issue_one(const u32x4& rsrc, char* lds, int i) const {
+  // The i-th of this wave's instructions for rows [r0, r0 + 64) of `base`
+  // into the tile at `lds`: the window starts delta_rows(i) rows later.
+  __device__ __forceinline__ void issue_one(const bf16* base, int r0, int nrows, int d, char* lds, int i) const {
     const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane(
         (int)(uint32_t)reinterpret_cast<uintptr_t>(lds + Layout::block_off(gw + GROUP * i)));
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff[i]), "s"(rsrc)
+    const u32x4 rs = rsrc_of(base, r0 + delta_rows(i), nrows, d);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(rs)
                  : "memory", "m0");
   }
 
@@ -568,20 +576,8 @@ struct PpDma {
   // wait insertion does not tie every later LDS read to these loads; the
   // kernel orders them itself with explicit vmcnt waits and barriers.
   __device__ __forceinline__ void issue(const bf16* base, int r0, int nrows, int d, char* lds) const {
-    const int rows_left = nrows - r0 > 0 ? nrows - r0 : 0;
-    // Every operand is wave-uniform; readfirstlane keeps them in SGPRs.
-    const uint64_t addr = reinterpret_cast<uint64_t>(base + (int64_t)r0 * d);
-    const u32x4 rsrc = {(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
-                        (uint32_t)__builtin_amdgcn_readfirstlane((int)((addr >> 32) & 0xffffu)),
-                        (uint32_t)__builtin_amdgcn_readfirstlane(rows_left * d * 2), 0x00020000u};
 #pragma unroll
-    for (int i = 0; i < kPerWave; ++i) {
-      const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane(
-          (int)(uint32_t)reinterpret_cast<uintptr_t>(lds + Layout::block_off(gw + GROUP * i)));
-      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff[i]),
-                   "s"(rsrc)
-                   : "memory", "m0");
-    }
+    for (int i = 0; i < kPerWave; ++i) issue_one(base, r0, nrows, d, lds, i);
   }
 };
 
@@ -971,10 +967,9 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
   // nothing and write zeros into a slot nobody reads again.
   auto dma_part = [&](int j, int qd) {
     if (qd < F::kDma)
-      kdma.issue_one(kdma.rsrc_of(kb, (j + 3) * F::BK, S, d), kring + ((j + 3) % F::kSlots) * KT::kBytes, qd);
+      kdma.issue_one(kb, (j + 3) * F::BK, S, d, kring + ((j + 3) % F::kSlots) * KT::kBytes, qd);
     else
-      vdma.issue_one(vdma.rsrc_of(vb, (j + 1) * F::BK, S, d), vring + ((j + 1) % F::kSlots) * VT::kBytes,
-                     qd - F::kDma);
+      vdma.issue_one(vb, (j + 1) * F::BK, S, d, vring + ((j + 1) % F::kSlots) * VT::kBytes, qd - F::kDma);
   };
   auto dma = [&](int j) {
 #pragma unroll
@@ -991,7 +986,7 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
     bf16x8(&pc)[RB][4] = pf[P];
     bf16x8(&pp)[RB][4] = pf[1 - P];
     const char* kp = kring + ((j + 1) % F::kSlots) * KT::kBytes + kbase;
-    const char* vp = vring + ((j + 2) % F::kSlots) * VT::kBytes + vbase;
+    const char* vp = vring + ((j - 1 + F::kSlots) % F::kSlots) * VT::kBytes + vbase;
     constexpr int NFQ = QK ? 2 * KS : 0;  // K fragments (key subtile f % 2, k-chunk f / 2)
     constexpr int NFV = PV ? 4 * DT : 0;  // V^T fragments (key chunk i / DT, dim tile i % DT)
     constexpr int NF = NFQ + NFV;
@@ -1532,7 +1527,7 @@ struct BwdTile {
   // With 128-byte rows a block holds its four rows in its first 512 bytes;
   // lanes 32-63 of its DMA instruction are switched off (they write zeros
   // into the unused half).
-  static __device__ __forceinline__ int dma_row(int b, int L) { return b + 16 * (L / kChunks); }
+  static __host__ __device__ constexpr int dma_row(int b, int L) { return b + 16 * (L / kChunks); }
   static __device__ __forceinline__ bool dma_lane(int L) { return L / kChunks < 4; }
   // Row fragment (physical rows 32 half + l32, bytes 32 kk + 16 g): lane base
   // plus row_at(half, kk).
@@ -1635,9 +1630,9 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
     char* sl = slot(t);
     const int r0 = (first + t) * F::BQ;
     if (qd < F::kDma)
-      dma.issue_one(dma.rsrc_of(qb, r0, Sq, d), sl, qd);
+      dma.issue_one(qb, r0, Sq, d, sl, qd);
     else if (qd < 2 * F::kDma)
-      dma.issue_one(dma.rsrc_of(dob, r0, Sq, d), sl + Tile::kBytes, qd - F::kDma);
+      dma.issue_one(dob, r0, Sq, d, sl + Tile::kBytes, qd - F::kDma);
     else if (qd == 2 * F::kDma)
       stat_dma(lseb, r0, Sq, sl + 2 * Tile::kBytes);
     else
