@@ -13,6 +13,8 @@ backward (delta, dK/dV, dQ), the long-context variant (B=1, H=8, T=8192, d=64),
 fused add+RMSNorm ([4096,1024] bf16, timed over 24 rotating buffer sets so the
 working set exceeds the 256 MB Infinity Cache) and the blocked matmul (bf16
 4096^3, f32 1000^3). Each carries its roofline fraction against MI355X peaks.
+"gpt_train_step" times the caller of these kernels: one forward+backward+AdamW
+step of the 12-layer GPT of BASELINE config 5 (bf16 parameters, batch 8 x 1024).
 
 cpu_baseline: the CPU oracle (numpy f32, the reference's materialised
 impl='xla' math) timed on this host's cores on a bounded sample of the same
@@ -222,6 +224,49 @@ def bench_matmul(steps, warmup):
     return out
 
 
+def bench_gpt_train(steps, warmup, linear_routes=("pallas", "xla")):
+    """One GPT train step (forward + backward + AdamW) of BASELINE config 5: 12 layers, d_model 768,
+    12 heads of 64, MLP 3072, vocab 32768, seq 1024, batch 8, bf16 parameters, tokens U[0, vocab).
+    Attention and norms run on the HIP kernels; the linear layers on the HIP matmul ("pallas")
+    or on torch's GEMM ("xla"). FLOPs are the reference's analytic count (gpt.py:155-163)."""
+    import torch
+
+    from ferrite.model.gpt import GPTConfig, flops_per_token, init_params, param_count
+    from ferrite.model.train import TrainConfig, adamw_init, build_train_step
+
+    dev = torch.device("cuda:0")
+    b = 8
+    base = GPTConfig(vocab_size=32768, seq_len=1024, d_model=768, n_head=12, n_layer=12, d_ff=3072)
+    g = torch.Generator().manual_seed(11)
+    x = torch.randint(0, base.vocab_size, (b, base.seq_len), generator=g).to(dev)
+    y = torch.randint(0, base.vocab_size, (b, base.seq_len), generator=g).to(dev)
+    out = {}
+    for route in linear_routes:
+        cfg = base.replace(linear=route)
+        params = init_params(0, cfg, device=dev, param_dtype=torch.bfloat16)
+        n_nonembed = param_count(params) - params["tok_emb"].numel() - params["pos_emb"].numel()
+        flops = 3 * flops_per_token(cfg, n_nonembed)["total"] * b * cfg.seq_len
+        opt = adamw_init(params)
+        step = build_train_step(cfg, TrainConfig(steps=1000, warmup=10, lr=3e-4))
+        losses = []
+
+        def one():
+            nonlocal params, opt
+            params, opt, loss, _ = step(params, opt, x, y)
+            losses.append(loss)
+
+        t = _events_time(one, steps, warmup)
+        out[f"linear_{route}"] = {
+            "ms_per_step": t * 1e3, "tokens_per_s": b * cfg.seq_len / t, "tflops": flops / t / 1e12,
+            "mfu_bf16": flops / t / 1e12 / PEAK_BF16_TFLOPS, "train_flops_per_step": flops,
+            "params": param_count(params), "params_nonembed": n_nonembed,
+            "loss_first": float(losses[0]), "loss_last": float(losses[-1]),
+        }
+        del params, opt, step, losses
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_copy(nbytes: int = 256 << 20, iters: int = 5):
     """A plain device-to-device copy of `nbytes`: reads and writes exactly nbytes, so FETCH_SIZE and
     WRITE_SIZE of its dispatch calibrate the byte counters; also a ceiling for streaming kernels."""
@@ -266,7 +311,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["attn", "rmsnorm", "matmul", "all"], default="all")
+    ap.add_argument("--only", choices=["attn", "rmsnorm", "matmul", "gpt", "all"], default="all")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (the HBM byte-counter calibration for rocprofv3 --pmc)")
     a = ap.parse_args(argv)
@@ -290,6 +335,8 @@ def main(argv=None):
         kernels["add_rmsnorm"] = bench_rmsnorm(4096, 1024, a.steps, a.warmup)
     if a.only in ("matmul", "all"):
         kernels["matmul"] = bench_matmul(max(a.steps // 2, 3), 2)
+    if a.only in ("gpt", "all"):
+        kernels["gpt_train_step"] = bench_gpt_train(max(a.steps // 2, 3), 2)
 
     att = kernels.get("attention")
     if att is not None:
