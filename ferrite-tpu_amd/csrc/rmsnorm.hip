@@ -298,6 +298,221 @@ int dispatch(const void* x, const void* r, const void* w, void* h, void* y, int6
   return launch<float, float, RES>(x, r, w, h, y, rows, dim, eps, s);
 }
 
+
+// ---------------------------------------------------------------------------
+// Backward (rmsnorm.py:159-166, and :148-153 for the fused add):
+//   inv = rsqrt(mean(h^2) + eps),  xhat = h * inv,  dxhat = dy * w
+//   dh  = inv * (dxhat - xhat * mean(dxhat * xhat))  [+ dh_direct]
+//   dw  = sum over rows of dy * xhat
+// mean(dxhat * xhat) is evaluated as inv * mean(dxhat * h), so one pass with two
+// wave reductions per row gives both statistics. All arithmetic is f32.
+//
+// dw is deterministic: each workgroup accumulates its rows' dy * xhat in
+// registers (every lane owns the same columns on every row), its four waves
+// combine through LDS into one partial row of the workspace, and a second
+// kernel sums the partial rows in a fixed order.
+// ---------------------------------------------------------------------------
+
+constexpr int kBwdMaxParts = 512;  // partial dw rows (workgroups of the row pass)
+
+template <typename TX, typename TW, typename TO, bool DIRECT, int VPL>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_rows_kernel(const TX* __restrict__ h, const TW* __restrict__ w,
+                                                              const TX* __restrict__ dy, const TX* __restrict__ dd,
+                                                              TO* __restrict__ dh, float* __restrict__ partial,
+                                                              int64_t rows, int dim, float inv_dim, float eps) {
+  extern __shared__ float red[];  // [4][dim]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nchunks = dim / kChunk;
+  float wv[VPL][kChunk], acc[VPL][kChunk];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nchunks) load8(w + c * kChunk, wv[i]);
+#pragma unroll
+    for (int e = 0; e < kChunk; ++e) acc[i][e] = 0.f;
+  }
+  for (int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + wave; row < rows; row += (int64_t)gridDim.x * kRowsPerBlock) {
+    const int64_t off = row * dim;
+    Raw8<TX> hr[VPL], gr[VPL], dr[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nchunks) {
+        ld8_nt(h + off + c * kChunk, hr[i]);
+        ld8_nt(dy + off + c * kChunk, gr[i]);
+        if constexpr (DIRECT) ld8_nt(dd + off + c * kChunk, dr[i]);
+      }
+    }
+    float hv[VPL][kChunk], gv[VPL][kChunk];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      if (lane + 64 * i < nchunks) {
+        unpack8(hr[i], hv[i]);
+        unpack8(gr[i], gv[i]);
+#pragma unroll
+        for (int e = 0; e < kChunk; ++e) {
+          s1 += hv[i][e] * hv[i][e];
+          s2 += (gv[i][e] * wv[i][e]) * hv[i][e];
+        }
+      }
+    }
+    s1 = wave_sum(s1);
+    s2 = wave_sum(s2);
+    const float inv = __builtin_amdgcn_rsqf(s1 * inv_dim + eps);
+    const float mean = inv * s2 * inv_dim;  // mean(dxhat * xhat)
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nchunks) {
+        float dv[kChunk], out[kChunk];
+        if constexpr (DIRECT) unpack8(dr[i], dv);
+#pragma unroll
+        for (int e = 0; e < kChunk; ++e) {
+          const float xh = hv[i][e] * inv;
+          out[e] = inv * (gv[i][e] * wv[i][e] - xh * mean);
+          if constexpr (DIRECT) out[e] += dv[e];
+          acc[i][e] += gv[i][e] * xh;
+        }
+        st8_nt(dh + off + c * kChunk, out);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nchunks) store8(red + wave * dim + c * kChunk, acc[i]);
+  }
+  __syncthreads();
+  for (int col = threadIdx.x; col < dim; col += blockDim.x)
+    partial[(int64_t)blockIdx.x * dim + col] = (red[col] + red[dim + col]) + (red[2 * dim + col] + red[3 * dim + col]);
+}
+
+// General row pass (any dim or alignment): one wave per row, two sweeps. The
+// per-row inv goes to the workspace for the column pass below.
+template <typename TX, typename TW, typename TO, bool DIRECT>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_rows_generic_kernel(const TX* __restrict__ h,
+                                                                      const TW* __restrict__ w,
+                                                                      const TX* __restrict__ dy,
+                                                                      const TX* __restrict__ dd, TO* __restrict__ dh,
+                                                                      float* __restrict__ inv_rows, int64_t rows,
+                                                                      int64_t dim, float inv_dim, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t off = row * dim;
+  float s1 = 0.f, s2 = 0.f;
+  for (int64_t e = lane; e < dim; e += 64) {
+    const float hv = Elem<TX>::to_f32(h[off + e]);
+    s1 += hv * hv;
+    s2 += (Elem<TX>::to_f32(dy[off + e]) * Elem<TW>::to_f32(w[e])) * hv;
+  }
+  s1 = wave_sum(s1);
+  s2 = wave_sum(s2);
+  const float inv = __builtin_amdgcn_rsqf(s1 * inv_dim + eps);
+  const float mean = inv * s2 * inv_dim;
+  if (lane == 0) inv_rows[row] = inv;
+  for (int64_t e = lane; e < dim; e += 64) {
+    const float xh = Elem<TX>::to_f32(h[off + e]) * inv;
+    float o = inv * (Elem<TX>::to_f32(dy[off + e]) * Elem<TW>::to_f32(w[e]) - xh * mean);
+    if constexpr (DIRECT) o += Elem<TX>::to_f32(dd[off + e]);
+    dh[off + e] = Elem<TO>::from_f32(o);
+  }
+}
+
+// Column pass of the general path: partial[p, col] = sum over rows r = p (mod P)
+// of dy[r, col] * h[r, col] * inv[r]. Threads own columns, so each row read is
+// coalesced.
+template <typename TX>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_cols_kernel(const TX* __restrict__ h, const TX* __restrict__ dy,
+                                                              const float* __restrict__ inv_rows,
+                                                              float* __restrict__ partial, int64_t rows,
+                                                              int64_t dim) {
+  const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (col >= dim) return;
+  float acc = 0.f;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y)
+    acc += Elem<TX>::to_f32(dy[r * dim + col]) * (Elem<TX>::to_f32(h[r * dim + col]) * inv_rows[r]);
+  partial[(int64_t)blockIdx.y * dim + col] = acc;
+}
+
+// dw[col] = sum of the partial rows, in order; cast to the weight's dtype.
+template <typename TW>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_dw_kernel(const float* __restrict__ partial, TW* __restrict__ dw,
+                                                            int nparts, int64_t dim) {
+  const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (col >= dim) return;
+  float acc = 0.f;
+  for (int p = 0; p < nparts; ++p) acc += partial[(int64_t)p * dim + col];
+  dw[col] = Elem<TW>::from_f32(acc);
+}
+
+// Layout of the caller's workspace: kBwdMaxParts partial rows of dim floats,
+// then one float per row (general path only).
+int64_t bwd_workspace_bytes(int64_t rows, int64_t dim) { return ((int64_t)kBwdMaxParts * dim + rows) * 4; }
+
+template <typename TX, typename TW, typename TO, bool DIRECT>
+int bwd_launch(const void* h, const void* w, const void* dy, const void* dd, void* dh, void* dw, void* ws,
+               int64_t rows, int64_t dim, float eps, hipStream_t stream) {
+  const float inv_dim = (float)(1.0 / (double)dim);
+  const TX* hp = static_cast<const TX*>(h);
+  const TX* gp = static_cast<const TX*>(dy);
+  const TX* dp = static_cast<const TX*>(dd);
+  const TW* wp = static_cast<const TW*>(w);
+  TO* op = static_cast<TO*>(dh);
+  float* partial = static_cast<float*>(ws);
+  int nparts = 0;
+  auto aligned16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const bool fast = dim % kChunk == 0 && dim <= 64 * kChunk * 8 && aligned16(h) && aligned16(dy) && aligned16(w) &&
+                    aligned16(dh) && (!DIRECT || aligned16(dd));
+  if (rows > 0 && fast) {
+    // At least 4 rows per wave; at most kBwdMaxParts workgroups (two per CU).
+    nparts = (int)std::min<int64_t>(cdiv(rows, (int64_t)kRowsPerBlock * 4), kBwdMaxParts);
+    const int vpl = (int)cdiv(dim / kChunk, 64);
+    const size_t lds = (size_t)kRowsPerBlock * dim * sizeof(float);
+#define FERRITE_RMS_BWD_CASE(V)                                                                                    \
+  hipLaunchKernelGGL((rmsnorm_bwd_rows_kernel<TX, TW, TO, DIRECT, V>), dim3(nparts), dim3(256), lds, stream, hp, wp, \
+                     gp, dp, op, partial, rows, (int)dim, inv_dim, eps)
+    if (vpl <= 1)
+      FERRITE_RMS_BWD_CASE(1);
+    else if (vpl <= 2)
+      FERRITE_RMS_BWD_CASE(2);
+    else if (vpl <= 4)
+      FERRITE_RMS_BWD_CASE(4);
+    else
+      FERRITE_RMS_BWD_CASE(8);
+#undef FERRITE_RMS_BWD_CASE
+  } else if (rows > 0) {
+    float* inv_rows = partial + (int64_t)kBwdMaxParts * dim;
+    const int64_t blocks = cdiv(rows, kRowsPerBlock);
+    if (blocks > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "rmsnorm_bwd: too many rows");
+    hipLaunchKernelGGL((rmsnorm_bwd_rows_generic_kernel<TX, TW, TO, DIRECT>), dim3((unsigned)blocks), dim3(256), 0,
+                       stream, hp, wp, gp, dp, op, inv_rows, rows, dim, inv_dim, eps);
+    nparts = (int)std::min<int64_t>(rows, kBwdMaxParts);
+    const int64_t cblocks = cdiv(dim, 256);
+    if (cblocks > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "rmsnorm_bwd: dim too large");
+    hipLaunchKernelGGL((rmsnorm_bwd_cols_kernel<TX>), dim3((unsigned)cblocks, (unsigned)nparts), dim3(256), 0, stream,
+                       hp, gp, inv_rows, partial, rows, dim);
+  }
+  hipLaunchKernelGGL((rmsnorm_bwd_dw_kernel<TW>), dim3((unsigned)cdiv(dim, 256)), dim3(256), 0, stream, partial,
+                     static_cast<TW*>(dw), nparts, dim);
+  return check_launch("ferrite_rmsnorm_bwd");
+}
+
+template <typename TX, typename TW>
+int bwd_dispatch_out(const void* h, const void* w, const void* dy, const void* dd, void* dh, void* dw, void* ws,
+                     int64_t rows, int64_t dim, int dh_dtype, float eps, hipStream_t s) {
+  if (dh_dtype == FERRITE_F32) {
+    return dd ? bwd_launch<TX, TW, float, true>(h, w, dy, dd, dh, dw, ws, rows, dim, eps, s)
+              : bwd_launch<TX, TW, float, false>(h, w, dy, dd, dh, dw, ws, rows, dim, eps, s);
+  }
+  if constexpr (sizeof(TX) == 2) {
+    return dd ? bwd_launch<TX, TW, TX, true>(h, w, dy, dd, dh, dw, ws, rows, dim, eps, s)
+              : bwd_launch<TX, TW, TX, false>(h, w, dy, dd, dh, dw, ws, rows, dim, eps, s);
+  }
+  return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_rmsnorm_bwd: a bf16 dh needs bf16 inputs");
+}
+
 }  // namespace
 }  // namespace ferrite
 
@@ -310,4 +525,30 @@ extern "C" int ferrite_hip_add_rmsnorm(const void* x, const void* residual, cons
 extern "C" int ferrite_hip_rmsnorm(const void* x, const void* weight, void* y, int64_t rows, int64_t dim,
                                    int x_dtype, int w_dtype, float eps, void* stream) {
   return ferrite::dispatch<false>(x, nullptr, weight, nullptr, y, rows, dim, x_dtype, w_dtype, eps, stream);
+}
+
+extern "C" int64_t ferrite_hip_rmsnorm_bwd_workspace(int64_t rows, int64_t dim) {
+  if (rows < 0 || dim < 1) return -1;
+  return ferrite::bwd_workspace_bytes(rows, dim);
+}
+
+extern "C" int ferrite_hip_rmsnorm_bwd(const void* h, const void* weight, const void* dy, const void* dh_direct,
+                                       void* dh, void* dweight, void* workspace, int64_t rows, int64_t dim,
+                                       int x_dtype, int w_dtype, int dh_dtype, float eps, void* stream) {
+  using namespace ferrite;
+  const char* name = "ferrite_hip_rmsnorm_bwd";
+  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype) || !valid_dtype(dh_dtype))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": dtype must be FERRITE_F32 or FERRITE_BF16");
+  if (rows < 0 || dim < 1) return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": need rows >= 0 and dim >= 1");
+  if (!weight || !dweight || !workspace || (rows > 0 && (!h || !dy || !dh)))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x_dtype == FERRITE_BF16) {
+    if (w_dtype == FERRITE_BF16)
+      return bwd_dispatch_out<bf16, bf16>(h, weight, dy, dh_direct, dh, dweight, workspace, rows, dim, dh_dtype, eps, s);
+    return bwd_dispatch_out<bf16, float>(h, weight, dy, dh_direct, dh, dweight, workspace, rows, dim, dh_dtype, eps, s);
+  }
+  if (w_dtype == FERRITE_BF16)
+    return bwd_dispatch_out<float, bf16>(h, weight, dy, dh_direct, dh, dweight, workspace, rows, dim, dh_dtype, eps, s);
+  return bwd_dispatch_out<float, float>(h, weight, dy, dh_direct, dh, dweight, workspace, rows, dim, dh_dtype, eps, s);
 }

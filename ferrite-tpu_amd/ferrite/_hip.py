@@ -32,7 +32,18 @@ SIGNATURES: dict[str, tuple] = {
     "ferrite_hip_version": (ctypes.c_char_p, []),
     "ferrite_hip_add_rmsnorm": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_f32, _vp]),
     "ferrite_hip_rmsnorm": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_f32, _vp]),
+    "ferrite_hip_rmsnorm_bwd_workspace": (_c_i64, [_c_i64, _c_i64]),
+    "ferrite_hip_rmsnorm_bwd": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_f32, _vp],
+    ),
     "ferrite_hip_matmul": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _vp]),
+    "ferrite_hip_adamw_workspace": (_c_i64, [_c_i64]),
+    "ferrite_hip_adamw": (
+        _c_int,
+        [_c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32,
+         _c_i64, _vp, _vp, _vp],
+    ),
     "ferrite_hip_attn_fwd": (
         _c_int,
         [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f32, _vp],

@@ -3,8 +3,10 @@
 Reference: src/ferrite/kernels/rmsnorm.py. Same public API and ValueErrors.
 The forward is one HIP kernel (csrc/rmsnorm.hip: ferrite_hip_add_rmsnorm /
 ferrite_hip_rmsnorm) that reads x and residual once, writes h and y once and
-keeps the statistics in f32. As in the reference (rmsnorm.py:9-12, :159-166),
-the backward is plain tensor math in f32, here torch ops on the same device.
+keeps the statistics in f32. The backward (rmsnorm.py:159-166, an XLA fusion in
+the reference) is a HIP kernel too (ferrite_hip_rmsnorm_bwd): one pass over h,
+dy and the fused add's direct gradient that writes dh, plus a fixed-order
+reduction of dweight.
 """
 
 from __future__ import annotations
@@ -59,13 +61,24 @@ def _kernel(x2d, r2d, w, eps: float, block_rows):
     return h.to(out_dtype), y.to(out_dtype)
 
 
-def _rmsnorm_bwd_math(h, w, dy, eps):
-    """Analytic RMSNorm backward in f32 (rmsnorm.py:159-166). y = h * inv * w, inv = rsqrt(mean(h^2) + eps)."""
-    inv = torch.rsqrt(torch.mean(h * h, dim=-1, keepdim=True) + eps)
-    xhat = h * inv
-    dw = torch.sum(dy * xhat, dim=0)
-    dxhat = dy * w
-    dh = inv * (dxhat - xhat * torch.mean(dxhat * xhat, dim=-1, keepdim=True))
+def _bwd_kernel(h2d, w, dy, dd, eps: float, dh_dtype):
+    """(dh, dw) of the analytic backward on the HIP kernel; `dd` is the fused add's direct
+    gradient (or None). dh comes back in `dh_dtype` (h's dtype or float32), dw in w's dtype."""
+    _hip.require_gpu(h2d, w, dy)
+    h2d, dy, w = h2d.contiguous(), dy.to(h2d.dtype).contiguous(), w.contiguous()
+    if dd is not None:
+        dd = dd.to(h2d.dtype).contiguous()
+    rows, dim = h2d.shape
+    lib = _hip.lib()
+    dh = torch.empty((rows, dim), dtype=dh_dtype, device=h2d.device)
+    dw = torch.empty_like(w)
+    ws = torch.empty((lib.ferrite_hip_rmsnorm_bwd_workspace(rows, dim) + 3) // 4, dtype=torch.float32, device=h2d.device)
+    rc = lib.ferrite_hip_rmsnorm_bwd(
+        h2d.data_ptr(), w.data_ptr(), dy.data_ptr(), _hip.ptr(dd), dh.data_ptr(), dw.data_ptr(), ws.data_ptr(),
+        rows, dim, _hip.dtype_code(h2d.dtype), _hip.dtype_code(w.dtype), _hip.dtype_code(dh_dtype), float(eps),
+        _hip.stream_of(h2d),
+    )
+    _hip.check(rc, "ferrite_rmsnorm_bwd")
     return dh, dw
 
 
@@ -82,8 +95,8 @@ class _Norm(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         x2d, w = ctx.saved_tensors
-        dx, dw = _rmsnorm_bwd_math(x2d.float(), w.float(), dy.float(), ctx.eps)
-        return dx.to(x2d.dtype), dw.to(w.dtype), None, None
+        dx, dw = _bwd_kernel(x2d, w, dy, None, ctx.eps, x2d.dtype)
+        return dx, dw, None, None
 
 
 class _AddNorm(torch.autograd.Function):
@@ -95,14 +108,21 @@ class _AddNorm(torch.autograd.Function):
         ctx.save_for_backward(h, w)
         ctx.eps = eps
         ctx.r_dtype = r2d.dtype
+        ctx.set_materialize_grads(False)  # an unused h (the last norm's) costs no zero tensor
         return h, y
 
     @staticmethod
     def backward(ctx, dh_direct, dy):
         h, w = ctx.saved_tensors
-        dh, dw = _rmsnorm_bwd_math(h.float(), w.float(), dy.float(), ctx.eps)
-        dh = dh + dh_direct.float()
-        return dh.to(h.dtype), dh.to(ctx.r_dtype), dw.to(w.dtype), None, None
+        if dy is None:
+            dy = torch.zeros_like(h)
+        # dh in h's dtype serves both inputs when the residual has it too; otherwise keep f32
+        # and round once per input, as the reference's casts of the f32 dh do.
+        same = ctx.r_dtype == h.dtype
+        dh, dw = _bwd_kernel(h, w, dy, dh_direct, ctx.eps, h.dtype if same else torch.float32)
+        if same:
+            return dh, dh, dw, None, None
+        return dh.to(h.dtype), dh.to(ctx.r_dtype), dw, None, None
 
 
 def rmsnorm(x, weight, *, residual=None, eps: float = 1e-6, block_rows: int | None = None):

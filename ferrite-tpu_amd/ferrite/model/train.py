@@ -10,9 +10,11 @@ Device placement: one process drives one GPU. The reference shards the batch
 over a 1-D data mesh and lets XLA insert the gradient all-reduce
 (train.py:80-99); this build trains on a single device, and a multi-GPU run
 would add one all-reduce of the gradient list per step between the backward and
-``adamw_update``. The optimiser runs as torch multi-tensor (``_foreach``)
-kernels in f32; with bf16 parameters the moments stay f32 and each update is
-rounded once into the parameter.
+``adamw_update``. The optimiser runs on the fused HIP kernel
+(``optimizer="fused"``, csrc/optim.hip: one pass over g, p, m, v per step) or
+as torch multi-tensor (``_foreach``) ops (``optimizer="foreach"``, also on CPU);
+both compute in f32, and with bf16 parameters the moments stay f32 and each
+update is rounded once into the parameter.
 """
 
 from __future__ import annotations
@@ -48,6 +50,11 @@ class TrainConfig:
     data: str = "tinyshakespeare"
     out: str | None = None
     save_params: str | None = None
+    optimizer: str = "fused"  # "fused" (HIP kernel) | "foreach" (torch multi-tensor ops)
+
+    def __post_init__(self):
+        if self.optimizer not in ("fused", "foreach"):
+            raise ValueError(f"optimizer must be 'fused' or 'foreach', got {self.optimizer!r}")
 
 
 def default_device() -> torch.device:
@@ -89,6 +96,14 @@ def adamw_update(params, grads, state, cfg: TrainConfig, b1: float = 0.9, b2: fl
     the pre-clip norm as a 0-d device tensor, so the step needs no host sync."""
     step = state["step"] + 1
     lr = lr_at(step, cfg)
+    if cfg.optimizer == "fused":
+        from ferrite.kernels.adamw import fused_adamw_
+
+        p = leaves(params)
+        gnorm = fused_adamw_(p, leaves(grads), leaves(state["m"]), leaves(state["v"]), [t.ndim >= 2 for t in p],
+                             lr=lr, beta1=b1, beta2=b2, eps=eps, weight_decay=cfg.weight_decay,
+                             max_grad_norm=cfg.clip, step=step)
+        return params, {"m": state["m"], "v": state["v"], "step": step}, gnorm
     p = leaves(params)
     g = [t.float() for t in leaves(grads)]
     m = leaves(state["m"])

@@ -22,7 +22,10 @@
  *   ferrite_hip_attn_bwd_dq   flash_attention.py:224-243, :281-306 ("ferrite_flash_attention_bwd_dq")
  *   ferrite_hip_add_rmsnorm   rmsnorm.py:52-56, :77-110  ("ferrite_add_rmsnorm")
  *   ferrite_hip_rmsnorm       rmsnorm.py:46-49, :77-110  ("ferrite_rmsnorm")
+ *   ferrite_hip_rmsnorm_bwd   rmsnorm.py:159-166, :128-131, :148-153 (the custom_vjp backward of
+ *                                                          _norm/_add_norm, XLA fusions in the reference)
  *   ferrite_hip_matmul        matmul.py:27-38, :52-86    ("ferrite_matmul")
+ *   ferrite_hip_adamw         ../model/train.py:59-74    (adamw_update, XLA fusions in the reference)
  *
  * The one layout change against the reference: the softmax statistics
  * (logsumexp `lse` and `delta`) are compact f32 [B, H, S] arrays instead of the
@@ -67,6 +70,23 @@ int ferrite_hip_rmsnorm(const void* x, const void* weight, void* y, int64_t rows
                         int w_dtype, float eps, void* stream);
 
 /*
+ * RMSNorm backward (rmsnorm.py:159-166), with the fused add's direct term
+ * (rmsnorm.py:148-153):
+ *   inv = rsqrt(mean(h^2) + eps);  xhat = h * inv;  dxhat = dy * weight
+ *   dh  = inv * (dxhat - xhat * mean(dxhat * xhat)) + dh_direct
+ *   dweight = sum over rows of dy * xhat
+ * h, dy, dh_direct: [rows, dim] of x_dtype (dh_direct may be NULL: no direct
+ * term); weight, dweight: [dim] of w_dtype; dh: [rows, dim] of dh_dtype (x_dtype,
+ * or FERRITE_F32). Statistics and sums are f32; dweight is summed in a fixed
+ * order (deterministic). `workspace` is device memory of
+ * ferrite_hip_rmsnorm_bwd_workspace(rows, dim) bytes owned by the caller.
+ */
+int64_t ferrite_hip_rmsnorm_bwd_workspace(int64_t rows, int64_t dim);
+int ferrite_hip_rmsnorm_bwd(const void* h, const void* weight, const void* dy, const void* dh_direct, void* dh,
+                            void* dweight, void* workspace, int64_t rows, int64_t dim, int x_dtype, int w_dtype,
+                            int dh_dtype, float eps, void* stream);
+
+/*
  * out[M, N] = x[M, K] @ y[K, N] with f32 accumulation (matmul.py:27-38, :52-86).
  * in_dtype FERRITE_BF16 uses bf16 MFMA; FERRITE_F32 uses fp32 MFMA (true fp32
  * products, the reference's Precision.HIGHEST, _compat.py:17-25). Ragged shapes
@@ -76,6 +96,25 @@ int ferrite_hip_rmsnorm(const void* x, const void* weight, void* y, int64_t rows
  */
 int ferrite_hip_matmul(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k, int in_dtype,
                        int out_dtype, void* stream);
+
+/*
+ * One AdamW step over n_tensors parameter tensors (../model/train.py:59-74):
+ *   gnorm = sqrt(sum over all tensors of sum(g^2))   (f32, fixed summation order)
+ *   g *= min(1, max_grad_norm / (gnorm + 1e-6))
+ *   m = beta1*m + (1-beta1)*g;  v = beta2*v + (1-beta2)*g*g
+ *   p -= lr * ((m/bc1) / (sqrt(v/bc2) + eps) + (decay[i] ? weight_decay : 0) * p)
+ * with bc = 1 - beta^step. params[i] (param_dtype) and exp_avg[i], exp_avg_sq[i]
+ * (f32) are updated in place; grads[i] (grad_dtype) are read. The pointer, numel
+ * and decay arrays are host memory; the tensors are device memory. grad_norm
+ * (device f32 scalar, may be NULL) receives the pre-clip gnorm. `workspace` is
+ * device memory of ferrite_hip_adamw_workspace(n_tensors) bytes. No host
+ * synchronisation: the clip scale stays on the device.
+ */
+int64_t ferrite_hip_adamw_workspace(int64_t n_tensors);
+int ferrite_hip_adamw(int64_t n_tensors, void* const* params, const void* const* grads, float* const* exp_avg,
+                      float* const* exp_avg_sq, const int64_t* numel, const int32_t* decay, int param_dtype,
+                      int grad_dtype, float lr, float beta1, float beta2, float eps, float weight_decay,
+                      float max_grad_norm, int64_t step, float* grad_norm, void* workspace, void* stream);
 
 /*
  * Flash attention forward (flash_attention.py:91-175).

@@ -25,7 +25,7 @@ def _declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     declared = _declared_symbols()
-    assert len(declared) == 9
+    assert len(declared) == 13
     out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH], capture_output=True, text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s(\w+)", out))
     missing = [s for s in declared if s not in exported]
@@ -42,6 +42,24 @@ def test_abi_argument_checks_return_codes():
     assert "M, N, K" in _hip.last_error()
     assert lib.ferrite_hip_matmul(None, None, None, 4, 4, 4, 7, _hip.BF16, None) == 1
     assert "dtype" in _hip.last_error()
+    # RMSNorm backward: workspace query, dtype, shape and null-pointer checks
+    assert lib.ferrite_hip_rmsnorm_bwd_workspace(8192, 768) == (512 * 768 + 8192) * 4
+    assert lib.ferrite_hip_rmsnorm_bwd_workspace(-1, 768) == -1
+    assert lib.ferrite_hip_rmsnorm_bwd(1, 1, 1, None, 1, 1, 1, 4, 8, _hip.BF16, 5, _hip.BF16, 1e-6, None) == 1
+    assert "dtype" in _hip.last_error()
+    assert lib.ferrite_hip_rmsnorm_bwd(1, 1, 1, None, 1, 1, 1, 4, 0, _hip.BF16, _hip.F32, _hip.BF16, 1e-6, None) == 1
+    assert lib.ferrite_hip_rmsnorm_bwd(1, 1, None, None, 1, 1, 1, 4, 8, _hip.BF16, _hip.F32, _hip.BF16, 1e-6, None) == 1
+    assert "null" in _hip.last_error()
+    assert lib.ferrite_hip_rmsnorm_bwd(1, 1, 1, None, 1, 1, 1, 4, 8, _hip.F32, _hip.F32, _hip.BF16, 1e-6, None) == 1
+    # AdamW: workspace query and argument checks (host arrays are inspected before any launch)
+    assert lib.ferrite_hip_adamw_workspace(75) == (3 * 512 + 4) * 4
+    assert lib.ferrite_hip_adamw_workspace(-1) == -1
+    args = [None] * 6 + [_hip.BF16, _hip.BF16, 1e-3, 0.9, 0.95, 1e-8, 0.1, 1.0]
+    assert lib.ferrite_hip_adamw(1, *args, 1, None, 1, None) == 1
+    assert "null" in _hip.last_error()
+    assert lib.ferrite_hip_adamw(0, *args, 0, None, 1, None) == 1
+    assert "step" in _hip.last_error()
+    assert lib.ferrite_hip_adamw(0, *args[:6], 9, _hip.BF16, *args[8:], 1, None, 1, None) == 1
     # causal needs sq == sk
     assert lib.ferrite_hip_attn_fwd(1, 1, 1, 1, 1, 1, 1, 128, 256, 64, _hip.BF16, 1, 0.125, None) == 1
     assert "sq == sk" in _hip.last_error()

@@ -115,7 +115,7 @@ def test_first_adamw_step_closed_form():
     p0 = {k: v.clone() for k, v in params.items() if k != "layers"}
     c0 = params["layers"][0]["c"].clone()
     gsave = {k: v.clone() for k, v in grads.items() if k != "layers"}
-    cfg = TrainConfig(lr=1e-2, warmup=4, steps=10, weight_decay=0.1, clip=0.5)
+    cfg = TrainConfig(lr=1e-2, warmup=4, steps=10, weight_decay=0.1, clip=0.5, optimizer="foreach")
     state = adamw_init(params)
     params, state, gnorm = adamw_update(params, grads, state, cfg)
     lr1 = lr_at(1, cfg)
@@ -134,7 +134,8 @@ def test_bf16_params_keep_f32_moments():
     state = adamw_init(params)
     assert state["m"]["w"].dtype == torch.float32
     before = params["w"].clone()
-    adamw_update(params, {"w": torch.randn(8, 8).to(torch.bfloat16)}, state, TrainConfig(lr=1e-2, warmup=1))
+    adamw_update(params, {"w": torch.randn(8, 8).to(torch.bfloat16)}, state,
+                 TrainConfig(lr=1e-2, warmup=1, optimizer="foreach"))
     assert params["w"].dtype == torch.bfloat16 and not torch.equal(params["w"], before)
 
 
@@ -159,6 +160,11 @@ def test_kernel_route_refuses_cpu_tensors():
     params = init_params(0, TINY.replace(n_layer=1))
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         forward(params, torch.zeros((1, 128), dtype=torch.long), TINY.replace(n_layer=1))
+    grads = {k: v for k, v in params.items()}
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        adamw_update(params, grads, adamw_init(params), TrainConfig())  # the fused optimiser is HIP-only
+    with pytest.raises(ValueError):
+        TrainConfig(optimizer="sgd")
 
 
 def test_config_validates_routes():
@@ -171,7 +177,7 @@ def test_config_validates_routes():
 def test_short_training_run_reduces_loss_on_cpu(tmp_path):
     cfg = TINY.replace(seq_len=64, d_model=64, n_head=1, n_layer=1, d_ff=128, **XLA)
     tcfg = TrainConfig(steps=12, batch=8, lr=3e-3, warmup=2, log_every=100, data="synthetic",
-                       out=str(tmp_path / "r.json"), save_params=str(tmp_path / "p.npz"))
+                       out=str(tmp_path / "r.json"), save_params=str(tmp_path / "p.npz"), optimizer="foreach")
     res = train(cfg, tcfg, verbose=False, device="cpu")
     assert res["loss_last"] < res["loss_first"]
     assert res["tokens_per_second"] > 0 and res["mfu"] is None

@@ -130,3 +130,86 @@ def test_every_element_written_and_deterministic(dev):
         assert not torch.isnan(h).any() and not torch.isnan(y).any()
         outs.append((h.clone(), y.clone()))
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+def _bwd_abi(h, w, dy, dd, dh_dtype, dim_slice=None):
+    """Run ferrite_hip_rmsnorm_bwd on device tensors; NaN-prefilled outputs."""
+    rows, dim = h.shape
+    lib = _hip.lib()
+    dh = torch.full((rows, dim), float("nan"), dtype=dh_dtype, device=h.device)
+    dw = torch.full_like(w, float("nan"))
+    ws = torch.full(((lib.ferrite_hip_rmsnorm_bwd_workspace(rows, dim) + 3) // 4,), float("nan"), device=h.device)
+    rc = lib.ferrite_hip_rmsnorm_bwd(h.data_ptr(), w.data_ptr(), dy.data_ptr(), _hip.ptr(dd), dh.data_ptr(),
+                                     dw.data_ptr(), ws.data_ptr(), rows, dim, _hip.dtype_code(h.dtype),
+                                     _hip.dtype_code(w.dtype), _hip.dtype_code(dh_dtype), 1e-6, _hip.stream_of(h))
+    _hip.check(rc, "rmsnorm_bwd")
+    torch.cuda.synchronize()
+    return dh, dw
+
+
+@pytest.mark.parametrize("rows,dim,dtype,direct", [
+    (8192, 768, "bf16", True),    # the GPT's residual stream: row pass, VPL 2
+    (8192, 768, "bf16", False),
+    (4096, 1024, "bf16", True),
+    (333, 4096, "f32", True),     # VPL 8, ragged row count
+    (77, 64, "f32", False),       # VPL 1 with idle lanes
+    (50, 100, "f32", True),       # dim % 8 != 0: general row pass + column pass
+    (19, 5000, "bf16", False),    # dim above the register path: general
+    (3, 768, "bf16", True),       # fewer rows than waves
+])
+def test_bwd_kernel_matches_oracle(dev, rows, dim, dtype, direct):
+    """dh and dweight of ferrite_hip_rmsnorm_bwd against the f64 analytic backward
+    (rmsnorm.py:159-166, + the direct term of :148-153). f32: 1e-4 relative to the
+    gradient scale; bf16 dh: within one bf16 ulp (+1e-6 absolute) of the exact value; dweight
+    (f32 output, f32 sums): 1e-4 relative. Every element is written and reruns are bitwise equal."""
+    h = normal(30 + rows % 7, (rows, dim), dtype)
+    w = normal(31, (dim,), "f32", loc=1.0, scale=0.1)
+    dy = normal(32, (rows, dim), dtype)
+    dd = normal(33, (rows, dim), dtype) if direct else None
+    ht, wt, gt = to_dev(h, dtype, dev), to_dev(w, "f32", dev), to_dev(dy, dtype, dev)
+    dt = to_dev(dd, dtype, dev) if direct else None
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    dh, dw = _bwd_abi(ht, wt, gt, dt, tdt)
+    dh2, dw2 = _bwd_abi(ht, wt, gt, dt, tdt)
+    assert not torch.isnan(dh).any() and not torch.isnan(dw).any()
+    assert torch.equal(dh, dh2) and torch.equal(dw, dw2)
+    ref_dh, ref_dw = orms.rmsnorm_bwd(h, w, dy)
+    if direct:
+        ref_dh = ref_dh + dd
+    got = to_np(dh).astype(np.float64)
+    if dtype == "bf16":
+        assert np.all(np.abs(got - ref_dh) <= bf16_ulp(ref_dh.astype(np.float32)) + 1e-6)
+    else:
+        assert max_abs(got, ref_dh) <= 1e-4 * max(1.0, np.abs(ref_dh).max())
+    assert max_abs(to_np(dw), ref_dw) <= 1e-4 * max(1.0, np.abs(ref_dw).max())
+
+
+def test_bwd_kernel_f32_dh_from_bf16_and_zero_rows(dev):
+    """dh in f32 from bf16 inputs (the mixed-residual case) and rows == 0 (dweight is zero)."""
+    h, dy = normal(40, (64, 256), "bf16"), normal(41, (64, 256), "bf16")
+    w = normal(42, (256,), "bf16", loc=1.0, scale=0.1)
+    dh, dw = _bwd_abi(to_dev(h, "bf16", dev), to_dev(w, "bf16", dev), to_dev(dy, "bf16", dev), None, torch.float32)
+    ref_dh, ref_dw = orms.rmsnorm_bwd(h, w, dy)
+    assert dh.dtype == torch.float32 and max_abs(to_np(dh), ref_dh) <= 1e-4 * np.abs(ref_dh).max()
+    assert np.all(np.abs(to_np(dw) - ref_dw) <= bf16_ulp(ref_dw.astype(np.float32)) + 1e-6)
+    empty = torch.empty((0, 256), dtype=torch.bfloat16, device=dev)
+    _, dw0 = _bwd_abi(empty, to_dev(w, "bf16", dev), empty, None, torch.bfloat16)
+    assert torch.count_nonzero(dw0) == 0
+
+
+def test_bf16_autograd_uses_the_kernel(dev):
+    """Through rmsnorm(...).backward() in bf16 with an f32 weight (the GPT's layout): dx, dr and
+    dweight within the bf16 bar of the f64 backward of the rounded h."""
+    x, r = normal(50, (512, 768), "bf16"), normal(51, (512, 768), "bf16")
+    w = normal(52, (768,), "f32", loc=1.0, scale=0.1)
+    cot_y, cot_h = normal(53, (512, 768), "bf16"), normal(54, (512, 768), "bf16")
+    xt, rt = to_dev(x, "bf16", dev).requires_grad_(), to_dev(r, "bf16", dev).requires_grad_()
+    wt = to_dev(w, "f32", dev).requires_grad_()
+    h, y = rmsnorm(xt, wt, residual=rt)
+    torch.autograd.backward([y, h], [to_dev(cot_y, "bf16", dev), to_dev(cot_h, "bf16", dev)])
+    hh = round_bf16(x + r)
+    ref_dh, ref_dw = orms.rmsnorm_bwd(hh, w, cot_y)
+    ref_dh = ref_dh + cot_h
+    for g in (xt.grad, rt.grad):
+        assert max_abs(to_np(g), ref_dh) <= 2e-2
+    assert max_abs(to_np(wt.grad), ref_dw) <= 1e-3 * np.abs(ref_dw).max()
