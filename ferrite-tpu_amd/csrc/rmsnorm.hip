@@ -436,15 +436,32 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_cols_kernel(const TX* __restr
   partial[(int64_t)blockIdx.y * dim + col] = acc;
 }
 
-// dw[col] = sum of the partial rows, in order; cast to the weight's dtype.
+// dw[col] = sum of the partial rows; cast to the weight's dtype. A block owns
+// 64 columns; its 16 waves each sum every 16th partial row (in increasing
+// order), and wave 0 adds the 16 results in order, so the sum is deterministic
+// and every wave keeps several independent loads in flight.
+constexpr int kDwCols = 64, kDwGroups = 16;
+
 template <typename TW>
-__global__ __launch_bounds__(256) void rmsnorm_bwd_dw_kernel(const float* __restrict__ partial, TW* __restrict__ dw,
-                                                            int nparts, int64_t dim) {
-  const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (col >= dim) return;
+__global__ __launch_bounds__(kDwCols* kDwGroups) void rmsnorm_bwd_dw_kernel(const float* __restrict__ partial,
+                                                                           TW* __restrict__ dw, int nparts,
+                                                                           int64_t dim) {
+  __shared__ float red[kDwGroups][kDwCols];
+  const int c = threadIdx.x % kDwCols, grp = threadIdx.x / kDwCols;
+  const int64_t col = (int64_t)blockIdx.x * kDwCols + c;
   float acc = 0.f;
-  for (int p = 0; p < nparts; ++p) acc += partial[(int64_t)p * dim + col];
-  dw[col] = Elem<TW>::from_f32(acc);
+  if (col < dim) {
+#pragma unroll 8
+    for (int p = grp; p < nparts; p += kDwGroups) acc += partial[(int64_t)p * dim + col];
+  }
+  red[grp][c] = acc;
+  __syncthreads();
+  if (grp == 0 && col < dim) {
+    float sum = 0.f;
+#pragma unroll
+    for (int g = 0; g < kDwGroups; ++g) sum += red[g][c];
+    dw[col] = Elem<TW>::from_f32(sum);
+  }
 }
 
 // Layout of the caller's workspace: kBwdMaxParts partial rows of dim floats,
@@ -494,8 +511,8 @@ int bwd_launch(const void* h, const void* w, const void* dy, const void* dd, voi
     hipLaunchKernelGGL((rmsnorm_bwd_cols_kernel<TX>), dim3((unsigned)cblocks, (unsigned)nparts), dim3(256), 0, stream,
                        hp, gp, inv_rows, partial, rows, dim);
   }
-  hipLaunchKernelGGL((rmsnorm_bwd_dw_kernel<TW>), dim3((unsigned)cdiv(dim, 256)), dim3(256), 0, stream, partial,
-                     static_cast<TW*>(dw), nparts, dim);
+  hipLaunchKernelGGL((rmsnorm_bwd_dw_kernel<TW>), dim3((unsigned)cdiv(dim, kDwCols)), dim3(kDwCols * kDwGroups), 0,
+                     stream, partial, static_cast<TW*>(dw), nparts, dim);
   return check_launch("ferrite_rmsnorm_bwd");
 }
 

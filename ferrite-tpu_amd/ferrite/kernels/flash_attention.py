@@ -123,6 +123,8 @@ class _Flash(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, causal: bool, scale: float, bs: BlockSizes):
+        # The kernels read dense [B, H, S, D]; the dense copies are what the backward re-reads.
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         out, lse = _flash_forward(q, k, v, causal=causal, scale=scale, bs=bs)
         ctx.save_for_backward(q, k, v, out, lse)
         ctx.causal, ctx.scale, ctx.bs = causal, scale, bs

@@ -51,9 +51,12 @@ class GPTConfig:
     linear: str = "xla"  # "xla" (torch/hipBLASLt) | "pallas" (HIP matmul)
     dtype: torch.dtype = torch.bfloat16
     eps: float = 1e-6
+    # Loss of loss_fn (not a reference field): "pallas" = HIP cross-entropy fused with the
+    # tied head's backward, "xla" = torch cross_entropy on the f32 logits.
+    loss: str = "pallas"
 
     def __post_init__(self):
-        for field in ("attention", "norm", "linear"):
+        for field in ("attention", "norm", "linear", "loss"):
             if getattr(self, field) not in ROUTES:
                 raise ValueError(f"{field} must be one of {ROUTES}, got {getattr(self, field)!r}")
 
@@ -225,8 +228,31 @@ class _TiedLogits(torch.autograd.Function):
         return dy, demb
 
 
-def forward(params, tokens, cfg: GPTConfig):
-    """tokens [B, S] (int) -> logits [B, S, vocab] f32 (gpt.py:124-144)."""
+class _TiedHeadLoss(torch.autograd.Function):
+    """Mean cross-entropy of the tied head's f32 logits (gpt.py:143, :147-152) on the HIP
+    loss kernels. The logits stay inside: the backward kernel turns them straight into
+    the cotangent in the operand dtype, which then feeds the two head products."""
+
+    @staticmethod
+    def forward(ctx, y2, emb, targets):
+        from ferrite.kernels.cross_entropy import cross_entropy_rows
+
+        logits = _dot_f32(y2, emb.t())
+        loss, lse = cross_entropy_rows(logits, targets)
+        ctx.save_for_backward(y2, emb, logits, targets, lse)
+        return loss.mean()
+
+    @staticmethod
+    def backward(ctx, dloss):
+        from ferrite.kernels.cross_entropy import cross_entropy_grad
+
+        y2, emb, logits, targets, lse = ctx.saved_tensors
+        g = cross_entropy_grad(logits, targets, lse, dloss, 1.0 / logits.shape[0], y2.dtype)
+        return torch.mm(g, emb), torch.mm(g.t(), y2), None
+
+
+def _trunk(params, tokens, cfg: GPTConfig):
+    """tokens [B, S] -> final normed hidden states [B*S, d] in cfg.dtype (gpt.py:124-142)."""
     b, s = tokens.shape
     if s > cfg.seq_len:
         raise ValueError(f"sequence {s} longer than cfg.seq_len={cfg.seq_len}")
@@ -238,18 +264,29 @@ def forward(params, tokens, cfg: GPTConfig):
         else:
             h, y = _norm(pending, layer["ln1"], h, cfg)
         qkv = _linear(y, layer["wqkv"], cfg).reshape(b, s, 3, cfg.n_head, cfg.head_dim)
-        q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))  # [B, H, S, hd]
+        # one head-major copy for q, k and v together: [3, B, H, S, hd]
+        q, k, v = qkv.permute(2, 0, 3, 1, 4).contiguous().unbind(0)
         a = _attention(q, k, v, cfg).transpose(1, 2).reshape(b, s, cfg.d_model)
         a = _linear(a, layer["wo"], cfg)
         h, y2 = _norm(a, layer["ln2"], h, cfg)
         pending = _linear(F.gelu(_linear(y2, layer["w1"], cfg), approximate="tanh"), layer["w2"], cfg)
     _, y = _norm(pending, params["ln_f"], h, cfg)
-    logits = _TiedLogits.apply(y.reshape(-1, cfg.d_model), params["tok_emb"].to(cfg.dtype))
+    return y.reshape(-1, cfg.d_model)
+
+
+def forward(params, tokens, cfg: GPTConfig):
+    """tokens [B, S] (int) -> logits [B, S, vocab] f32 (gpt.py:124-144)."""
+    b, s = tokens.shape
+    y = _trunk(params, tokens, cfg)
+    logits = _TiedLogits.apply(y, params["tok_emb"].to(cfg.dtype))
     return logits.reshape(b, s, cfg.vocab_size)
 
 
 def loss_fn(params, tokens, targets, cfg: GPTConfig):
     """Mean next-token cross-entropy in f32 (gpt.py:147-152)."""
+    if cfg.loss == "pallas":
+        y = _trunk(params, tokens, cfg)
+        return _TiedHeadLoss.apply(y, params["tok_emb"].to(cfg.dtype), targets.reshape(-1).long())
     logits = forward(params, tokens, cfg)
     return F.cross_entropy(logits.reshape(-1, cfg.vocab_size), targets.reshape(-1).long())
 

@@ -26,6 +26,7 @@
  *                                                          _norm/_add_norm, XLA fusions in the reference)
  *   ferrite_hip_matmul        matmul.py:27-38, :52-86    ("ferrite_matmul")
  *   ferrite_hip_adamw         ../model/train.py:59-74    (adamw_update, XLA fusions in the reference)
+ *   ferrite_hip_cross_entropy_fwd/_bwd ../model/gpt.py:147-152 (loss_fn and its autodiff, XLA in the reference)
  *
  * The one layout change against the reference: the softmax statistics
  * (logsumexp `lse` and `delta`) are compact f32 [B, H, S] arrays instead of the
@@ -96,6 +97,23 @@ int ferrite_hip_rmsnorm_bwd(const void* h, const void* weight, const void* dy, c
  */
 int ferrite_hip_matmul(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k, int in_dtype,
                        int out_dtype, void* stream);
+
+/*
+ * Softmax cross-entropy of f32 logits [n, v] against int64 targets [n]
+ * (../model/gpt.py:147-152): lse[i] = logsumexp_j logits[i, j] and
+ * loss[i] = lse[i] - logits[i, targets[i]] (NaN for a target outside [0, v)),
+ * both f32 [n]. The mean over rows is the caller's.
+ */
+int ferrite_hip_cross_entropy_fwd(const float* logits, const int64_t* targets, float* loss, float* lse, int64_t n,
+                                  int64_t v, void* stream);
+
+/*
+ * Gradient of scale * sum_i loss[i] w.r.t. the logits, times the device scalar
+ * *dloss: grad[i, j] = (exp(logits[i, j] - lse[i]) - [j == targets[i]]) * (*dloss) * scale,
+ * written as grad_dtype [n, v]. lse from ferrite_hip_cross_entropy_fwd.
+ */
+int ferrite_hip_cross_entropy_bwd(const float* logits, const int64_t* targets, const float* lse, const float* dloss,
+                                  float scale, void* grad, int64_t n, int64_t v, int grad_dtype, void* stream);
 
 /*
  * One AdamW step over n_tensors parameter tensors (../model/train.py:59-74):

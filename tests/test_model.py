@@ -20,7 +20,7 @@ from ferrite.model.gpt import GPTConfig, forward, init_params, leaves, loss_fn, 
 from ferrite.model.train import TrainConfig, adamw_init, adamw_update, load_params, lr_at, train
 
 TINY = GPTConfig(vocab_size=256, seq_len=128, d_model=256, n_head=2, n_layer=2, d_ff=512, dtype=torch.float32)
-XLA = dict(attention="xla", norm="xla", linear="xla")
+XLA = dict(attention="xla", norm="xla", linear="xla", loss="xla")
 
 
 def test_param_count_matches_formula():

@@ -19,7 +19,7 @@ from ferrite.model.train import TrainConfig, adamw_init, build_train_step, train
 pytestmark = pytest.mark.gpu
 
 TINY = GPTConfig(vocab_size=256, seq_len=128, d_model=256, n_head=2, n_layer=2, d_ff=512, dtype=torch.float32)
-XLA = dict(attention="xla", norm="xla", linear="xla")
+XLA = dict(attention="xla", norm="xla", linear="xla", loss="xla")
 
 
 def _tokens(dev, b=2, s=128, vocab=256, seed=1):
