@@ -133,7 +133,7 @@ class _Flash(torch.autograd.Function):
     @staticmethod
     def backward(ctx, do):
         q, k, v, out, lse = ctx.saved_tensors
-        do = do.to(out.dtype)
+        do = do.to(out.dtype).contiguous()
         delta = _flash_delta(out, do)
         dq, dk, dv = _flash_backward(q, k, v, do, lse, delta, causal=ctx.causal, scale=ctx.scale, bs=ctx.bs)
         return dq, dk, dv, None, None, None

@@ -30,6 +30,7 @@ import torch.nn.functional as F
 
 from ferrite import platform
 from ferrite.kernels.flash_attention import BlockSizes, flash_attention, flash_attention_reference
+from ferrite.kernels.heads import merge_heads, split_heads
 from ferrite.kernels.matmul import matmul
 from ferrite.kernels.rmsnorm import rmsnorm, rmsnorm_reference
 
@@ -187,6 +188,23 @@ def _attention(q, k, v, cfg: GPTConfig):
     return flash_attention_reference(q, k, v, causal=True)
 
 
+def _split_heads(qkv, cfg: GPTConfig):
+    """[B, S, 3d] -> q, k, v as dense [B, H, S, hd] (gpt.py:137). The kernel route moves them
+    with the HIP layout kernel; the torch route permutes."""
+    b, s, _ = qkv.shape
+    if cfg.attention == "pallas":
+        return split_heads(qkv, 3, cfg.n_head)
+    return qkv.reshape(b, s, 3, cfg.n_head, cfg.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
+
+
+def _merge_heads(a, cfg: GPTConfig):
+    """[B, H, S, hd] -> [B, S, d] (gpt.py:138)."""
+    b, _, s, _ = a.shape
+    if cfg.attention == "pallas":
+        return merge_heads(a)
+    return a.transpose(1, 2).reshape(b, s, cfg.d_model)
+
+
 _MM_F32_OUT: dict[str, bool] = {}
 
 
@@ -263,10 +281,9 @@ def _trunk(params, tokens, cfg: GPTConfig):
             y = _norm(h, layer["ln1"], None, cfg)
         else:
             h, y = _norm(pending, layer["ln1"], h, cfg)
-        qkv = _linear(y, layer["wqkv"], cfg).reshape(b, s, 3, cfg.n_head, cfg.head_dim)
-        # one head-major copy for q, k and v together: [3, B, H, S, hd]
-        q, k, v = qkv.permute(2, 0, 3, 1, 4).contiguous().unbind(0)
-        a = _attention(q, k, v, cfg).transpose(1, 2).reshape(b, s, cfg.d_model)
+        qkv = _linear(y, layer["wqkv"], cfg)  # [B, S, 3 * d]: rows (q|k|v, head, hd)
+        q, k, v = _split_heads(qkv, cfg)  # [B, H, S, hd] each
+        a = _merge_heads(_attention(q, k, v, cfg), cfg)  # [B, S, d]
         a = _linear(a, layer["wo"], cfg)
         h, y2 = _norm(a, layer["ln2"], h, cfg)
         pending = _linear(F.gelu(_linear(y2, layer["w1"], cfg), approximate="tanh"), layer["w2"], cfg)

@@ -27,6 +27,7 @@
  *   ferrite_hip_matmul        matmul.py:27-38, :52-86    ("ferrite_matmul")
  *   ferrite_hip_adamw         ../model/train.py:59-74    (adamw_update, XLA fusions in the reference)
  *   ferrite_hip_cross_entropy_fwd/_bwd ../model/gpt.py:147-152 (loss_fn and its autodiff, XLA in the reference)
+ *   ferrite_hip_heads_split/_merge ../model/gpt.py:137-138 (the head transposes, XLA copies in the reference)
  *
  * The one layout change against the reference: the softmax statistics
  * (logsumexp `lse` and `delta`) are compact f32 [B, H, S] arrays instead of the
@@ -97,6 +98,16 @@ int ferrite_hip_rmsnorm_bwd(const void* h, const void* weight, const void* dy, c
  */
 int ferrite_hip_matmul(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k, int in_dtype,
                        int out_dtype, void* stream);
+
+/*
+ * Head layout changes. heads_split: tokens [B, S, groups, H, D] -> groups
+ * tensors heads[g] of [B, H, S, D]; heads_merge is the inverse. `heads` is a
+ * host array of `groups` (1..4) device pointers; all tensors dense, of `dtype`.
+ */
+int ferrite_hip_heads_split(const void* tokens, void* const* heads, int64_t b, int64_t s, int64_t groups, int64_t h,
+                            int64_t d, int dtype, void* stream);
+int ferrite_hip_heads_merge(void* const* heads, void* tokens, int64_t b, int64_t s, int64_t groups, int64_t h,
+                            int64_t d, int dtype, void* stream);
 
 /*
  * Softmax cross-entropy of f32 logits [n, v] against int64 targets [n]

@@ -25,7 +25,7 @@ def _declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     declared = _declared_symbols()
-    assert len(declared) == 15
+    assert len(declared) == 17
     out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH], capture_output=True, text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s(\w+)", out))
     missing = [s for s in declared if s not in exported]
@@ -60,6 +60,12 @@ def test_abi_argument_checks_return_codes():
     assert lib.ferrite_hip_adamw(0, *args, 0, None, 1, None) == 1
     assert "step" in _hip.last_error()
     assert lib.ferrite_hip_adamw(0, *args[:6], 9, _hip.BF16, *args[8:], 1, None, 1, None) == 1
+    # head layout: group count, dtype and null checks; empty is a no-op
+    assert lib.ferrite_hip_heads_split(None, None, 0, 4, 3, 2, 8, _hip.BF16, None) == 0
+    assert lib.ferrite_hip_heads_split(1, 1, 2, 4, 5, 2, 8, _hip.BF16, None) == 1
+    assert lib.ferrite_hip_heads_merge(1, 1, 2, 4, 3, 2, 8, 4, None) == 1
+    assert lib.ferrite_hip_heads_merge(None, 1, 2, 4, 3, 2, 8, _hip.BF16, None) == 1
+    assert "null" in _hip.last_error()
     # cross-entropy: shape, dtype and null checks; n == 0 is a no-op
     assert lib.ferrite_hip_cross_entropy_fwd(None, None, None, None, 0, 8, None) == 0
     assert lib.ferrite_hip_cross_entropy_fwd(1, 1, 1, 1, 4, 0, None) == 1
