@@ -224,11 +224,13 @@ def bench_matmul(steps, warmup):
     return out
 
 
-def bench_gpt_train(steps, warmup, linear_routes=("pallas", "xla")):
+def bench_gpt_train(steps, warmup, linear_routes=("pallas", "xla"), modes=("graph", "eager")):
     """One GPT train step (forward + backward + AdamW) of BASELINE config 5: 12 layers, d_model 768,
     12 heads of 64, MLP 3072, vocab 32768, seq 1024, batch 8, bf16 parameters, tokens U[0, vocab).
-    Attention and norms run on the HIP kernels; the linear layers on the HIP matmul ("pallas")
-    or on torch's GEMM ("xla"). FLOPs are the reference's analytic count (gpt.py:155-163)."""
+    Attention, norms, loss, head layout and AdamW run on the HIP kernels; the linear layers on the
+    HIP matmul ("pallas") or on torch's GEMM ("xla"). "graph" replays the step from a captured HIP
+    graph, "eager" launches it from Python. FLOPs are the reference's analytic count
+    (gpt.py:155-163)."""
     import torch
 
     from ferrite.model.gpt import GPTConfig, flops_per_token, init_params, param_count
@@ -242,28 +244,30 @@ def bench_gpt_train(steps, warmup, linear_routes=("pallas", "xla")):
     y = torch.randint(0, base.vocab_size, (b, base.seq_len), generator=g).to(dev)
     out = {}
     for route in linear_routes:
-        cfg = base.replace(linear=route)
-        params = init_params(0, cfg, device=dev, param_dtype=torch.bfloat16)
-        n_nonembed = param_count(params) - params["tok_emb"].numel() - params["pos_emb"].numel()
-        flops = 3 * flops_per_token(cfg, n_nonembed)["total"] * b * cfg.seq_len
-        opt = adamw_init(params)
-        step = build_train_step(cfg, TrainConfig(steps=1000, warmup=10, lr=3e-4))
-        losses = []
+        for mode in modes:
+            cfg = base.replace(linear=route)
+            params = init_params(0, cfg, device=dev, param_dtype=torch.bfloat16)
+            n_nonembed = param_count(params) - params["tok_emb"].numel() - params["pos_emb"].numel()
+            flops = 3 * flops_per_token(cfg, n_nonembed)["total"] * b * cfg.seq_len
+            opt = adamw_init(params)
+            step = build_train_step(cfg, TrainConfig(steps=1000, warmup=10, lr=3e-4), graph=mode == "graph")
+            losses = []
 
-        def one():
-            nonlocal params, opt
-            params, opt, loss, _ = step(params, opt, x, y)
-            losses.append(loss)
+            def one():
+                nonlocal params, opt
+                params, opt, loss, _ = step(params, opt, x, y)
+                losses.append(loss)
 
-        t = _events_time(one, steps, warmup)
-        out[f"linear_{route}"] = {
-            "ms_per_step": t * 1e3, "tokens_per_s": b * cfg.seq_len / t, "tflops": flops / t / 1e12,
-            "mfu_bf16": flops / t / 1e12 / PEAK_BF16_TFLOPS, "train_flops_per_step": flops,
-            "params": param_count(params), "params_nonembed": n_nonembed,
-            "loss_first": float(losses[0]), "loss_last": float(losses[-1]),
-        }
-        del params, opt, step, losses
-        torch.cuda.empty_cache()
+            t = _events_time(one, steps, max(warmup, 3))
+            out[f"linear_{route}_{mode}"] = {
+                "ms_per_step": t * 1e3, "tokens_per_s": b * cfg.seq_len / t, "tflops": flops / t / 1e12,
+                "mfu_bf16": flops / t / 1e12 / PEAK_BF16_TFLOPS, "train_flops_per_step": flops,
+                "params": param_count(params), "params_nonembed": n_nonembed,
+                "loss_first": float(losses[0]), "loss_last": float(losses[-1]),
+            }
+            del params, opt, step, losses
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
     return out
 
 

@@ -20,6 +20,8 @@
 // c of row n lives at chunk c ^ ((n ^ (n >> 3)) & 7). Fragment reads (32
 // consecutive rows, same chunk) and the transposed staging writes (rows 8
 // apart, same chunk) both land on distinct banks.
+#include <algorithm>
+
 #include "common.h"
 
 namespace ferrite {
@@ -283,26 +285,74 @@ struct GemmYTile {
 struct Gemm2 {
   static constexpr int kWaves = 8, kThreads = 64 * kWaves;
   static constexpr int BM = 256, BN = 256, BK = 64;
-  static constexpr int kStageBytes = GemmXTile::kBytes + GemmYTile::kBytes;
-  static constexpr int kLds = 2 * kStageBytes;
   static constexpr int kDma = 32 / kWaves;  // instructions per wave per stage, for x and for y
 };
 
-template <typename TO>
+// Each operand tile is 256 free indices (m for x, n for y) by 64 k. An operand
+// stored k-contiguous (x as [M,K], or y given transposed as [N,K]) is staged in
+// the GemmXTile layout and read with plain 16-byte reads; one stored
+// free-index-contiguous (y as [K,N], or x given transposed as [K,M]) is staged
+// in the GemmYTile layout and read with transposing reads. Both reads hand the
+// MFMA the same fragment: lane l32 = free index, lane group g = 8 k values.
+template <bool KCONTIG>
+struct OperandTile {
+  static constexpr int kBytes = KCONTIG ? GemmXTile::kBytes : GemmYTile::kBytes;
+  static constexpr int kReads = KCONTIG ? 1 : 2;  // LDS read instructions per fragment
+  static __host__ __device__ constexpr int block_off(int i) {
+    return KCONTIG ? GemmXTile::block_off(i) : GemmYTile::block_off(i);
+  }
+  // Lane's byte offset for DMA instruction i, relative to the tile's first element in
+  // global memory (ld = leading dimension in elements); 0x80000000 (past any buffer
+  // range, so the lane writes zeros) for free indices past `nfree`.
+  static __device__ __forceinline__ uint32_t dma_off(int i, int lane, int ld, int free0, int nfree) {
+    if constexpr (KCONTIG) {
+      const int r = GemmXTile::dma_row(i, lane);
+      return free0 + r < nfree ? (uint32_t)(((int64_t)r * ld + (lane & 7) * 8) * 2) : 0x80000000u;
+    } else {
+      const int r = GemmYTile::dma_row(i, lane);
+      const int c = (lane & 31) * 8;
+      return free0 + c < nfree ? (uint32_t)(((int64_t)r * ld + c) * 2) : 0x80000000u;
+    }
+  }
+  // Lane base for fragment reads.
+  static __device__ __forceinline__ int lane_base(int lane) {
+    const int l32 = lane & 31, g = lane >> 5;
+    if constexpr (KCONTIG)
+      return GemmXTile::off(l32, 16 * g);
+    else
+      return GemmYTile::off(8 * g + ((lane & 15) >> 2), 2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
+  }
+  // Fragment of free indices f0 .. f0 + 31 (f0 % 32 == 0) and k = 16 kk + (0..15).
+  static __device__ __forceinline__ bf16x8 read(const char* base, int kk, int f0) {
+    if constexpr (KCONTIG)
+      return *reinterpret_cast<const bf16x8*>(base + GemmXTile::off(f0, 32 * kk));
+    else
+      return tr_frag(base + GemmYTile::off(16 * kk, 2 * f0), GemmYTile::off(4, 0));
+  }
+};
+
+// out[M,N] (or, with a K split, the f32 partial slab of K slice blockIdx.x / tiles)
+// = x . y over this slice. XT: x is given transposed, stored [K,M]; YT: y is given
+// transposed, stored [N,K].
+template <typename TO, bool XT, bool YT>
 __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict__ x, const bf16* __restrict__ y,
                                                           TO* __restrict__ out, int M, int N, int K, int tiles_m,
-                                                          int tiles_n) {
+                                                          int tiles_n, int kslice) {
   typedef Gemm2 G;
+  typedef OperandTile<!XT> XTl;
+  typedef OperandTile<YT> YTl;
+  constexpr int kStageBytes = XTl::kBytes + YTl::kBytes;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int lane = threadIdx.x & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
-  // Tiles of one XCD (blocks are dealt to the 8 XCDs round robin) are made
-  // consecutive and ordered in groups of 4 tile rows, so an XCD's L2 holds
-  // few x and y panels.
-  const int nblocks = tiles_m * tiles_n;
-  int v = blockIdx.x;
-  if (nblocks % 8 == 0) v = (blockIdx.x % 8) * (nblocks / 8) + blockIdx.x / 8;
+  // K slice (slowest-varying block index), then the tile. Tiles of one XCD
+  // (blocks are dealt to the 8 XCDs round robin) are made consecutive and ordered
+  // in groups of 4 tile rows, so an XCD's L2 holds few x and y panels.
+  const int ntiles = tiles_m * tiles_n;
+  const int slice = blockIdx.x / ntiles;
+  int v = blockIdx.x - slice * ntiles;
+  if (ntiles % 8 == 0) v = (v % 8) * (ntiles / 8) + v / 8;
   constexpr int kGroup = 4;
   const int group = v / (kGroup * tiles_n);
   const int first_m = group * kGroup;
@@ -311,28 +361,26 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
   const int tn = (v % (kGroup * tiles_n)) / gsize;
   const int m0 = tm * G::BM, n0 = tn * G::BN;
   const int wm0 = (wave >> 2) * 128, wn0 = (wave & 3) * 64;
+  const int kbeg = slice * kslice;
+  const int nk = min(K - kbeg, kslice) / G::BK;
+  out += (int64_t)slice * M * N;
 
-  // Per-lane DMA offsets; rows past M and columns past N read as zeros.
+  // Per-lane DMA offsets; free indices past M or N read as zeros.
   uint32_t xoff[G::kDma], yoff[G::kDma];
 #pragma unroll
   for (int i = 0; i < G::kDma; ++i) {
-    const int xi = wave + 8 * i;
-    const int xr = GemmXTile::dma_row(xi, lane);
-    xoff[i] = m0 + xr < M ? (uint32_t)(((int64_t)xr * K + (lane & 7) * 8) * 2) : 0x80000000u;
-    const int yb = wave + 8 * i;
-    const int yr = GemmYTile::dma_row(yb, lane);
-    const int yc = (lane & 31) * 8;
-    yoff[i] = n0 + yc < N ? (uint32_t)(((int64_t)yr * N + yc) * 2) : 0x80000000u;
+    xoff[i] = XTl::dma_off(wave + 8 * i, lane, XT ? M : K, m0, M);
+    yoff[i] = YTl::dma_off(wave + 8 * i, lane, YT ? K : N, n0, N);
   }
   auto issue = [&](int kt) {
-    char* st = smem + (kt & 1) * G::kStageBytes;
-    const int k0 = kt * G::BK;
-    const u32x4 rx = buffer_rsrc(x + (int64_t)m0 * K + k0, 0x7ffffff0u);
-    const u32x4 ry = buffer_rsrc(y + (int64_t)k0 * N + n0, 0x7ffffff0u);
+    char* st = smem + (kt & 1) * kStageBytes;
+    const int k0 = kbeg + kt * G::BK;
+    const u32x4 rx = buffer_rsrc(XT ? x + (int64_t)k0 * M + m0 : x + (int64_t)m0 * K + k0, 0x7ffffff0u);
+    const u32x4 ry = buffer_rsrc(YT ? y + (int64_t)n0 * K + k0 : y + (int64_t)k0 * N + n0, 0x7ffffff0u);
 #pragma unroll
     for (int i = 0; i < G::kDma; ++i) {
-      dma16(rx, st + GemmXTile::block_off(wave + 8 * i), xoff[i]);
-      dma16(ry, st + GemmXTile::kBytes + GemmYTile::block_off(wave + 8 * i), yoff[i]);
+      dma16(rx, st + XTl::block_off(wave + 8 * i), xoff[i]);
+      dma16(ry, st + XTl::kBytes + YTl::block_off(wave + 8 * i), yoff[i]);
     }
   };
 
@@ -344,58 +392,54 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
 
-  // Lane bases: x row fragment (row l32, bytes 16 g) and y^T fragment (rows
-  // 8 g + (0..3), columns 16 ((lane / 16) % 2) + 4 (lane % 4)).
-  const int xb = GemmXTile::off(l32, 16 * g);
-  const int yb = GemmYTile::off(8 * g + ((lane & 15) >> 2), 2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
-  constexpr int kYHi = GemmYTile::off(4, 0);
+  const int xb = XTl::lane_base(lane);
+  const int yb = YTl::lane_base(lane);
+  // LDS read instructions per k-step of 16: 2 y fragments (A operand) and 4 x fragments (B).
+  constexpr int kReads = 2 * YTl::kReads + 4 * XTl::kReads;
+  static_assert(kReads <= 16, "at most two reads per product");
 
-  const int nk = K / G::BK;
   issue(0);
   for (int kt = 0; kt < nk; ++kt) {
     wait_vmem<0>();
     lds_barrier();
     if (kt + 1 < nk) issue(kt + 1);
-    const char* xs = smem + (kt & 1) * G::kStageBytes + xb;
-    const char* ys = smem + (kt & 1) * G::kStageBytes + GemmXTile::kBytes + yb;
-    // 4 k-steps x (2 y^T fragments, 4 x fragments, 8 products); the next
+    const char* xs = smem + (kt & 1) * kStageBytes + xb;
+    const char* ys = smem + (kt & 1) * kStageBytes + XTl::kBytes + yb;
+    // 4 k-steps x (2 y fragments, 4 x fragments, 8 products); the next
     // k-step's six fragments are read while this one's products run.
-    auto read_a = [&](int kk, int j) {
-      return tr_frag(ys + GemmYTile::off(16 * kk, 2 * (wn0 + 32 * j)), kYHi);
-    };
-    auto read_b = [&](int kk, int i) {
-      return *reinterpret_cast<const bf16x8*>(xs + GemmXTile::off(wm0 + 32 * i, 32 * kk));
-    };
     bf16x8 fa[2][2], fb[2][4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) fa[0][j] = read_a(0, j);
+    for (int j = 0; j < 2; ++j) fa[0][j] = YTl::read(ys, 0, wn0 + 32 * j);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fb[0][i] = read_b(0, i);
+    for (int i = 0; i < 4; ++i) fb[0][i] = XTl::read(xs, 0, wm0 + 32 * i);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int c = kk & 1;
       if (kk + 1 < 4) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) fa[c ^ 1][j] = read_a(kk + 1, j);
+        for (int j = 0; j < 2; ++j) fa[c ^ 1][j] = YTl::read(ys, kk + 1, wn0 + 32 * j);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fb[c ^ 1][i] = read_b(kk + 1, i);
+        for (int i = 0; i < 4; ++i) fb[c ^ 1][i] = XTl::read(xs, kk + 1, wm0 + 32 * i);
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mma32(fa[c][j], fb[c][i], acc[j][i]);
     }
-    // First fragments, then per k-step: one MFMA per read of the next step's
-    // six fragments (two of them a pair of transposed reads), then the rest.
-#pragma unroll
-    for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    // First fragments, then per k-step: the next step's reads spread over this
+    // step's eight MFMAs, then the last step's products.
+    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       if (kk + 1 < 4) {
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          const int nr = kReads / 8 + (r < kReads % 8 ? 1 : 0);  // 0..2 (kReads <= 12)
+          if (nr == 2)
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          else if (nr == 1)
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
       } else {
         __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
@@ -428,40 +472,119 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
   }
 }
 
+// out = sum over the K slices of the f32 partial slabs, in slice order
+// (deterministic), cast to TO. MN % 4 == 0.
 template <typename TO>
-int launch_gemm_dma(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, TO* __restrict__ out,
+                                                                int64_t mn, int slices) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= mn) return;
+  f32x4 acc = *reinterpret_cast<const f32x4*>(part + i);
+  for (int s = 1; s < slices; ++s) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(part + (int64_t)s * mn + i);
+    acc += v;
+  }
+  if constexpr (sizeof(TO) == 2)
+    *reinterpret_cast<bf16x4*>(out + i) = bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+  else
+    *reinterpret_cast<f32x4*>(out + i) = acc;
+}
+
+// K slices for a problem with few output tiles: enough slices to give every CU a
+// workgroup, each at least 512 deep; 1 when the tiles already fill most CUs or
+// the f32 partials would outweigh the work.
+int splitk_slices(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = cdiv(M, (int64_t)Gemm2::BM) * cdiv(N, (int64_t)Gemm2::BN);
+  if (tiles >= 64) return 1;
+  int64_t s = std::min<int64_t>({cdiv(256, tiles), K / 512, (int64_t)16});
+  if (s < 2) return 1;
+  const int64_t kslice = cdiv(cdiv(K, s), (int64_t)Gemm2::BK) * Gemm2::BK;
+  return (int)cdiv(K, kslice);
+}
+
+int64_t splitk_workspace(int64_t M, int64_t N, int64_t K) {
+  const int s = splitk_slices(M, N, K);
+  return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
+}
+
+template <typename TO, bool XT, bool YT>
+int launch_gemm_dma_t(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, void* ws,
+                      int64_t ws_bytes, hipStream_t stream) {
   typedef Gemm2 G;
   const int64_t tiles_m = cdiv(M, G::BM), tiles_n = cdiv(N, G::BN);
-  auto kern = gemm_dma_kernel<TO>;
-  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::kLds);
-  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n)), dim3(G::kThreads), G::kLds, stream,
-                     static_cast<const bf16*>(x), static_cast<const bf16*>(y), static_cast<TO*>(out), (int)M, (int)N,
-                     (int)K, (int)tiles_m, (int)tiles_n);
+  int slices = splitk_slices(M, N, K);
+  if (slices > 1 && (ws == nullptr || ws_bytes < splitk_workspace(M, N, K) || (M * N) % 4 != 0 ||
+                     (reinterpret_cast<uintptr_t>(ws) & 15) != 0))
+    slices = 1;
+  const int kslice = slices > 1 ? (int)(cdiv(cdiv(K, slices), (int64_t)G::BK) * G::BK) : (int)K;
+  constexpr int kLds = 2 * (OperandTile<!XT>::kBytes + OperandTile<YT>::kBytes);
+  const dim3 grid((unsigned)(tiles_m * tiles_n * slices));
+  if (slices == 1) {
+    auto kern = gemm_dma_kernel<TO, XT, YT>;
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    hipLaunchKernelGGL(kern, grid, dim3(G::kThreads), kLds, stream, static_cast<const bf16*>(x),
+                       static_cast<const bf16*>(y), static_cast<TO*>(out), (int)M, (int)N, (int)K, (int)tiles_m,
+                       (int)tiles_n, kslice);
+  } else {
+    auto kern = gemm_dma_kernel<float, XT, YT>;
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    hipLaunchKernelGGL(kern, grid, dim3(G::kThreads), kLds, stream, static_cast<const bf16*>(x),
+                       static_cast<const bf16*>(y), static_cast<float*>(ws), (int)M, (int)N, (int)K, (int)tiles_m,
+                       (int)tiles_n, kslice);
+    const int64_t mn = M * N;
+    hipLaunchKernelGGL((gemm_splitk_reduce_kernel<TO>), dim3((unsigned)cdiv(mn / 4, 256)), dim3(256), 0, stream,
+                       static_cast<const float*>(ws), static_cast<TO*>(out), mn, slices);
+  }
   return check_launch("ferrite_matmul");
+}
+
+template <typename TO>
+int launch_gemm_dma(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, bool xt, bool yt,
+                    void* ws, int64_t ws_bytes, hipStream_t stream) {
+  if (xt && yt) return launch_gemm_dma_t<TO, true, true>(x, y, out, M, N, K, ws, ws_bytes, stream);
+  if (xt) return launch_gemm_dma_t<TO, true, false>(x, y, out, M, N, K, ws, ws_bytes, stream);
+  if (yt) return launch_gemm_dma_t<TO, false, true>(x, y, out, M, N, K, ws, ws_bytes, stream);
+  return launch_gemm_dma_t<TO, false, false>(x, y, out, M, N, K, ws, ws_bytes, stream);
+}
+
+// Whether the DMA-fed kernel takes this problem: whole 64-deep k steps, N % 8 == 0 (and
+// M % 8 == 0 for a transposed x), 16-byte pointers, and every lane offset inside the 31-bit
+// buffer range (256 free rows of a k-contiguous operand, 64 k-rows of the other).
+bool dma_ok(const void* x, const void* y, const void* out, int64_t m, int64_t n, int64_t k, bool xt, bool yt) {
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  auto fits = [](int64_t bytes) { return bytes < 0x7ffffff0; };
+  return k % Gemm2::BK == 0 && n % 8 == 0 && (!xt || m % 8 == 0) && a16(x) && a16(y) && a16(out) &&
+         m <= 0x7fffffff && n <= 0x7fffffff && k <= 0x7fffffff && fits(xt ? 64 * m * 2 : 256 * k * 2) &&
+         fits(yt ? 256 * k * 2 : 64 * n * 2) && cdiv(m, (int64_t)Gemm2::BM) * cdiv(n, (int64_t)Gemm2::BN) * 16 <= 0x7fffffff;
 }
 
 }  // namespace
 }  // namespace ferrite
 
-extern "C" int ferrite_hip_matmul(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k,
-                                  int in_dtype, int out_dtype, void* stream) {
+extern "C" int64_t ferrite_hip_matmul_workspace(int64_t m, int64_t n, int64_t k, int in_dtype) {
+  if (m < 1 || n < 1 || k < 1) return -1;
+  return in_dtype == FERRITE_BF16 ? ferrite::splitk_workspace(m, n, k) : 0;
+}
+
+extern "C" int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k,
+                                     int x_t, int y_t, int in_dtype, int out_dtype, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
   using namespace ferrite;
   if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype))
     return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_matmul: dtype must be FERRITE_F32 or FERRITE_BF16");
   if (m < 1 || n < 1 || k < 1) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_matmul: need M, N, K >= 1");
   if (!x || !y || !out) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_matmul: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool xt = x_t != 0, yt = y_t != 0;
+  if (in_dtype == FERRITE_BF16 && dma_ok(x, y, out, m, n, k, xt, yt)) {
+    if (out_dtype == FERRITE_BF16) return launch_gemm_dma<bf16>(x, y, out, m, n, k, xt, yt, workspace, workspace_bytes, s);
+    return launch_gemm_dma<float>(x, y, out, m, n, k, xt, yt, workspace, workspace_bytes, s);
+  }
+  if (xt || yt)
+    return fail(FERRITE_ERR_INVALID_ARGUMENT,
+                "ferrite_hip_matmul: transposed operands need bf16, K % 64 == 0, N % 8 == 0, M % 8 == 0 for a "
+                "transposed x, and 16-byte aligned pointers");
   if (in_dtype == FERRITE_BF16) {
-    // DMA-fed kernel: whole 64-deep k steps, 16-byte y rows and pointers, and
-    // offsets that fit the 31-bit buffer range (256 rows of x, 64 rows of y).
-    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-    const bool dma_ok = k % Gemm2::BK == 0 && n % 8 == 0 && a16(x) && a16(y) && a16(out) && m <= 0x7fffffff &&
-                        n <= 0x7fffffff && 256 * k * 2 < 0x7ffffff0 && 64 * n * 2 < 0x7ffffff0 &&
-                        cdiv(m, (int64_t)Gemm2::BM) * cdiv(n, (int64_t)Gemm2::BN) <= 0x7fffffff;
-    if (dma_ok) {
-      if (out_dtype == FERRITE_BF16) return launch_gemm_dma<bf16>(x, y, out, m, n, k, s);
-      return launch_gemm_dma<float>(x, y, out, m, n, k, s);
-    }
     if (out_dtype == FERRITE_BF16) return launch_gemm<bf16, bf16, 256, 256, 64, 2, 2>(x, y, out, m, n, k, s);
     return launch_gemm<bf16, float, 256, 256, 64, 2, 2>(x, y, out, m, n, k, s);
   }
@@ -474,4 +597,9 @@ extern "C" int ferrite_hip_matmul(const void* x, const void* y, void* out, int64
   }
   if (out_dtype == FERRITE_BF16) return launch_gemm<float, bf16, 128, 128, 32, 2, 2>(x, y, out, m, n, k, s);
   return launch_gemm<float, float, 128, 128, 32, 2, 2>(x, y, out, m, n, k, s);
+}
+
+extern "C" int ferrite_hip_matmul(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k,
+                                  int in_dtype, int out_dtype, void* stream) {
+  return ferrite_hip_matmul_ex(x, y, out, m, n, k, 0, 0, in_dtype, out_dtype, nullptr, 0, stream);
 }

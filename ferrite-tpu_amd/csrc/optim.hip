@@ -139,8 +139,13 @@ __device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v,
 
 template <typename TP, typename TG>
 __global__ __launch_bounds__(kAdamThreads) void adamw_update_kernel(AdamGroup grp, const float* __restrict__ scale_ptr,
-                                                                   AdamHyper hp) {
+                                                                   AdamHyper hp, const float* __restrict__ step_scalars) {
   const float scale = *scale_ptr;
+  if (step_scalars) {  // per-step values from device memory (a captured graph replays fixed arguments)
+    hp.lr = step_scalars[0];
+    hp.bc1 = step_scalars[1];
+    hp.bc2 = step_scalars[2];
+  }
   const int64_t total = grp.tile0[grp.count];
   for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
     const int i = tensor_of(grp, t);
@@ -200,8 +205,8 @@ AdamGroup make_group(int64_t first, int count, void* const* params, const void* 
 
 template <typename TP, typename TG>
 int adamw_launch(int64_t nt, void* const* params, const void* const* grads, float* const* m, float* const* v,
-                 const int64_t* numel, const int32_t* decay, const AdamHyper& hp, float weight_decay,
-                 float max_norm, float* norm_out, float* ws, hipStream_t stream) {
+                 const int64_t* numel, const int32_t* decay, const AdamHyper& hp, const float* step_scalars,
+                 float weight_decay, float max_norm, float* norm_out, float* ws, hipStream_t stream) {
   const int64_t ng = adam_groups(nt);
   float* partial = ws;
   float* scale = ws + ng * kAdamNormBlocks;
@@ -221,7 +226,8 @@ int adamw_launch(int64_t nt, void* const* params, const void* const* grads, floa
     const int64_t tiles = grp.tile0[count];
     if (tiles == 0) continue;
     const unsigned blocks = (unsigned)std::min<int64_t>(tiles, 2048);
-    hipLaunchKernelGGL((adamw_update_kernel<TP, TG>), dim3(blocks), dim3(kAdamThreads), 0, stream, grp, scale, hp);
+    hipLaunchKernelGGL((adamw_update_kernel<TP, TG>), dim3(blocks), dim3(kAdamThreads), 0, stream, grp, scale, hp,
+                       step_scalars);
   }
   return check_launch("ferrite_adamw");
 }
@@ -238,12 +244,12 @@ extern "C" int ferrite_hip_adamw(int64_t n_tensors, void* const* params, const v
                                  float* const* exp_avg, float* const* exp_avg_sq, const int64_t* numel,
                                  const int32_t* decay, int param_dtype, int grad_dtype, float lr, float beta1,
                                  float beta2, float eps, float weight_decay, float max_grad_norm, int64_t step,
-                                 float* grad_norm, void* workspace, void* stream) {
+                                 const float* step_scalars, float* grad_norm, void* workspace, void* stream) {
   using namespace ferrite;
   const char* name = "ferrite_hip_adamw";
   if (!valid_dtype(param_dtype) || !valid_dtype(grad_dtype))
     return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": dtype must be FERRITE_F32 or FERRITE_BF16");
-  if (n_tensors < 0 || step < 1)
+  if (n_tensors < 0 || (step < 1 && !step_scalars))
     return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": need n_tensors >= 0 and step >= 1");
   if (!workspace || (n_tensors > 0 && (!params || !grads || !exp_avg || !exp_avg_sq || !numel || !decay)))
     return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": null pointer");
@@ -260,20 +266,18 @@ extern "C" int ferrite_hip_adamw(int64_t n_tensors, void* const* params, const v
   hp.b2 = beta2;
   hp.one_minus_b2 = (float)(1.0 - (double)beta2);
   hp.eps = eps;
-  hp.bc1 = (float)(1.0 - pow((double)beta1, (double)step));
-  hp.bc2 = (float)(1.0 - pow((double)beta2, (double)step));
+  hp.bc1 = step_scalars ? 1.f : (float)(1.0 - pow((double)beta1, (double)step));
+  hp.bc2 = step_scalars ? 1.f : (float)(1.0 - pow((double)beta2, (double)step));
   float* ws = static_cast<float*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
+#define FERRITE_ADAMW_LAUNCH(TP, TG)                                                                           \
+  return adamw_launch<TP, TG>(n_tensors, params, grads, exp_avg, exp_avg_sq, numel, decay, hp, step_scalars,   \
+                              weight_decay, max_grad_norm, grad_norm, ws, s)
   if (param_dtype == FERRITE_BF16) {
-    if (grad_dtype == FERRITE_BF16)
-      return adamw_launch<bf16, bf16>(n_tensors, params, grads, exp_avg, exp_avg_sq, numel, decay, hp, weight_decay,
-                                      max_grad_norm, grad_norm, ws, s);
-    return adamw_launch<bf16, float>(n_tensors, params, grads, exp_avg, exp_avg_sq, numel, decay, hp, weight_decay,
-                                     max_grad_norm, grad_norm, ws, s);
+    if (grad_dtype == FERRITE_BF16) FERRITE_ADAMW_LAUNCH(bf16, bf16);
+    FERRITE_ADAMW_LAUNCH(bf16, float);
   }
-  if (grad_dtype == FERRITE_BF16)
-    return adamw_launch<float, bf16>(n_tensors, params, grads, exp_avg, exp_avg_sq, numel, decay, hp, weight_decay,
-                                     max_grad_norm, grad_norm, ws, s);
-  return adamw_launch<float, float>(n_tensors, params, grads, exp_avg, exp_avg_sq, numel, decay, hp, weight_decay,
-                                    max_grad_norm, grad_norm, ws, s);
+  if (grad_dtype == FERRITE_BF16) FERRITE_ADAMW_LAUNCH(float, bf16);
+  FERRITE_ADAMW_LAUNCH(float, float);
+#undef FERRITE_ADAMW_LAUNCH
 }

@@ -38,6 +38,11 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_f32, _vp],
     ),
     "ferrite_hip_matmul": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _vp]),
+    "ferrite_hip_matmul_workspace": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_int]),
+    "ferrite_hip_matmul_ex": (
+        _c_int,
+        [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _c_i64, _vp],
+    ),
     "ferrite_hip_heads_split": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _vp]),
     "ferrite_hip_heads_merge": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _vp]),
     "ferrite_hip_cross_entropy_fwd": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _vp]),
@@ -46,7 +51,7 @@ SIGNATURES: dict[str, tuple] = {
     "ferrite_hip_adamw": (
         _c_int,
         [_c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32,
-         _c_i64, _vp, _vp, _vp],
+         _c_i64, _vp, _vp, _vp, _vp],
     ),
     "ferrite_hip_attn_fwd": (
         _c_int,

@@ -22,12 +22,16 @@ def _ptrs(tensors) -> ctypes.c_void_p:
 
 
 def fused_adamw_(params, grads, exp_avg, exp_avg_sq, decay, *, lr: float, beta1: float, beta2: float, eps: float,
-                 weight_decay: float, max_grad_norm: float, step: int) -> torch.Tensor:
+                 weight_decay: float, max_grad_norm: float, step: int, step_scalars: torch.Tensor | None = None,
+                 grad_norm: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Update ``params``, ``exp_avg`` and ``exp_avg_sq`` in place; return the pre-clip global
     gradient norm as a 0-d f32 device tensor.
 
     ``params``: same-dtype (f32 or bf16) contiguous device tensors; ``grads``: matching shapes,
-    one dtype; moments: f32 like ``params``; ``decay``: per-tensor bools (weight decay on)."""
+    one dtype; moments: f32 like ``params``; ``decay``: per-tensor bools (weight decay on).
+    ``step_scalars`` (f32 device tensor [3] = lr, 1 - beta1^step, 1 - beta2^step) replaces
+    ``lr`` and ``step`` at run time, for replay inside a captured graph; ``grad_norm`` and
+    ``workspace`` may be given to reuse buffers across calls."""
     n = len(params)
     if not (len(grads) == len(exp_avg) == len(exp_avg_sq) == len(decay) == n):
         raise ValueError("params, grads, moments and decay flags must have the same length")
@@ -45,8 +49,12 @@ def fused_adamw_(params, grads, exp_avg, exp_avg_sq, decay, *, lr: float, beta1:
     grads = [g.contiguous() for g in grads]
     lib = _hip.lib()
     dev = params[0].device
-    ws = torch.empty(((lib.ferrite_hip_adamw_workspace(n) + 3) // 4,), dtype=torch.float32, device=dev)
-    gnorm = torch.empty((), dtype=torch.float32, device=dev)
+    ws_floats = (lib.ferrite_hip_adamw_workspace(n) + 3) // 4
+    ws = workspace if workspace is not None and workspace.numel() >= ws_floats else torch.empty(
+        (ws_floats,), dtype=torch.float32, device=dev)
+    gnorm = grad_norm if grad_norm is not None else torch.empty((), dtype=torch.float32, device=dev)
+    if step_scalars is not None and (step_scalars.dtype != torch.float32 or step_scalars.numel() < 3):
+        raise ValueError("step_scalars must be a float32 device tensor of 3 values")
     pp, _a = _ptrs(params)
     gp, _b = _ptrs(grads)
     mp, _c = _ptrs(exp_avg)
@@ -56,7 +64,8 @@ def fused_adamw_(params, grads, exp_avg, exp_avg_sq, decay, *, lr: float, beta1:
     rc = lib.ferrite_hip_adamw(
         n, pp, gp, mp, vp, ctypes.cast(numel, ctypes.c_void_p), ctypes.cast(flags, ctypes.c_void_p),
         _hip.dtype_code(pdt), _hip.dtype_code(gdt), float(lr), float(beta1), float(beta2), float(eps),
-        float(weight_decay), float(max_grad_norm), int(step), gnorm.data_ptr(), ws.data_ptr(), _hip.stream_of(params[0]),
+        float(weight_decay), float(max_grad_norm), int(step), _hip.ptr(step_scalars), gnorm.data_ptr(), ws.data_ptr(),
+        _hip.stream_of(params[0]),
     )
     _hip.check(rc, "ferrite_adamw")
     return gnorm

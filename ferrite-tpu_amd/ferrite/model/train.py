@@ -145,9 +145,15 @@ def value_and_grad(params, x, y, cfg: GPTConfig):
     return loss.detach(), unflatten(params, list(grads))
 
 
-def build_train_step(model_cfg: GPTConfig, train_cfg: TrainConfig):
+def build_train_step(model_cfg: GPTConfig, train_cfg: TrainConfig, *, graph: bool = False):
     """``step(params, opt, x, y) -> (params, opt, loss, gnorm)``: forward, backward, AdamW
-    (train.py:84-99, on one device)."""
+    (train.py:84-99, on one device).
+
+    ``graph=True`` returns a :class:`GraphedTrainStep`: the same step captured once into a HIP
+    graph and replayed, which removes the host's per-kernel launch cost (the role ``jax.jit``
+    plays for the reference)."""
+    if graph:
+        return GraphedTrainStep(model_cfg, train_cfg)
 
     def step(params, opt, x, y):
         loss, grads = value_and_grad(params, x, y, model_cfg)
@@ -155,6 +161,85 @@ def build_train_step(model_cfg: GPTConfig, train_cfg: TrainConfig):
         return params, opt, loss, gnorm
 
     return step
+
+
+class GraphedTrainStep:
+    """The training step captured into a HIP graph and replayed (fused AdamW only).
+
+    The first ``warmup`` calls run eagerly on a side stream (library handles, the autograd
+    engine and the allocator settle there). The next call captures forward, backward and the
+    AdamW update into a graph and replays it; later calls only replay. Everything the graph
+    touches has a fixed address: the parameter and moment tensors, static token buffers the
+    inputs are copied into, the loss and gradient-norm outputs, and a device vector holding
+    the step's learning rate and bias corrections, refreshed before each replay (the update
+    kernel reads them from memory, so the replayed arguments can stay fixed). Parameters and
+    moments are updated in place, so ``params`` and ``opt`` must be the same trees on every call.
+    The returned loss of a replayed step is the graph's output tensor, overwritten by the next
+    replay: read it (or clone it) before calling again.
+    """
+
+    def __init__(self, model_cfg: GPTConfig, train_cfg: TrainConfig, warmup: int = 2, b1: float = 0.9,
+                 b2: float = 0.95, eps: float = 1e-8):
+        if train_cfg.optimizer != "fused":
+            raise ValueError("a graphed step needs optimizer='fused' (its update reads per-step values from memory)")
+        self.model_cfg, self.train_cfg = model_cfg, train_cfg
+        self.warmup, self.b1, self.b2, self.eps = warmup, b1, b2, eps
+        self.graph = None
+        self.calls = 0
+
+    def _setup(self, params, opt, x, y):
+        dev = x.device
+        self.x, self.y = torch.empty_like(x), torch.empty_like(y)
+        self.scalars = torch.zeros(3, dtype=torch.float32, device=dev)
+        self.gnorm = torch.zeros((), dtype=torch.float32, device=dev)
+        self.ps = leaves(params)
+        for t in self.ps:
+            t.requires_grad_(True)
+        self.ms, self.vs = leaves(opt["m"]), leaves(opt["v"])
+        self.decay = [t.ndim >= 2 for t in self.ps]
+        from ferrite import _hip
+
+        n = len(self.ps)
+        self.ws = torch.empty(((_hip.lib().ferrite_hip_adamw_workspace(n) + 3) // 4,), dtype=torch.float32, device=dev)
+        self.side = torch.cuda.Stream(device=dev)
+
+    def _body(self):
+        """One step on the static buffers; returns the loss tensor."""
+        from ferrite.kernels.adamw import fused_adamw_
+
+        loss = loss_fn(self.params, self.x, self.y, self.model_cfg)
+        grads = torch.autograd.grad(loss, self.ps)
+        fused_adamw_(self.ps, list(grads), self.ms, self.vs, self.decay, lr=0.0, beta1=self.b1, beta2=self.b2,
+                     eps=self.eps, weight_decay=self.train_cfg.weight_decay, max_grad_norm=self.train_cfg.clip,
+                     step=1, step_scalars=self.scalars, grad_norm=self.gnorm, workspace=self.ws)
+        return loss.detach()
+
+    def __call__(self, params, opt, x, y):
+        if self.calls == 0:
+            self.params = params
+            self._setup(params, opt, x, y)
+        step = opt["step"] + 1
+        # per-step values as fill kernels on the stream (no host buffer to race with the GPU)
+        self.scalars[0].fill_(lr_at(step, self.train_cfg))
+        self.scalars[1].fill_(1.0 - self.b1**step)
+        self.scalars[2].fill_(1.0 - self.b2**step)
+        self.x.copy_(x, non_blocking=True)
+        self.y.copy_(y, non_blocking=True)
+        if self.calls < self.warmup:
+            self.side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(self.side):
+                loss = self._body()
+            torch.cuda.current_stream().wait_stream(self.side)
+        else:
+            if self.graph is None:
+                torch.cuda.synchronize()
+                self.graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(self.graph):
+                    self.loss = self._body()
+            self.graph.replay()
+            loss = self.loss
+        self.calls += 1
+        return params, {"m": opt["m"], "v": opt["v"], "step": step}, loss, self.gnorm
 
 
 def train(model_cfg: GPTConfig, train_cfg: TrainConfig, *, verbose: bool = True, device=None) -> dict[str, Any]:

@@ -25,6 +25,7 @@
  *   ferrite_hip_rmsnorm_bwd   rmsnorm.py:159-166, :128-131, :148-153 (the custom_vjp backward of
  *                                                          _norm/_add_norm, XLA fusions in the reference)
  *   ferrite_hip_matmul        matmul.py:27-38, :52-86    ("ferrite_matmul")
+ *   ferrite_hip_matmul_ex     matmul.py:99-104 (the VJP's products, transposed operands read in place)
  *   ferrite_hip_adamw         ../model/train.py:59-74    (adamw_update, XLA fusions in the reference)
  *   ferrite_hip_cross_entropy_fwd/_bwd ../model/gpt.py:147-152 (loss_fn and its autodiff, XLA in the reference)
  *   ferrite_hip_heads_split/_merge ../model/gpt.py:137-138 (the head transposes, XLA copies in the reference)
@@ -100,6 +101,23 @@ int ferrite_hip_matmul(const void* x, const void* y, void* out, int64_t m, int64
                        int out_dtype, void* stream);
 
 /*
+ * The matmul with operands that may be given transposed, and an optional
+ * K split (matmul.py:99-104, the VJP's products: dx = g @ y^T and dy = x^T @ g
+ * without materialised transposes). out[M, N] = op(x) @ op(y):
+ *   x_t == 0: x is [M, K];  x_t != 0: x holds x^T, stored [K, M]
+ *   y_t == 0: y is [K, N];  y_t != 0: y holds y^T, stored [N, K]
+ * Transposed operands need bf16, K % 64 == 0, N % 8 == 0 (M % 8 == 0 when x_t)
+ * and 16-byte aligned pointers; otherwise the call fails with
+ * FERRITE_ERR_INVALID_ARGUMENT. With a workspace of at least
+ * ferrite_hip_matmul_workspace(m, n, k, in_dtype) bytes (0 = the shape does not
+ * split), a bf16 problem with few output tiles splits K across workgroups and
+ * sums the f32 partials in a fixed order (deterministic); with NULL it does not split.
+ */
+int64_t ferrite_hip_matmul_workspace(int64_t m, int64_t n, int64_t k, int in_dtype);
+int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k, int x_t, int y_t,
+                          int in_dtype, int out_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Head layout changes. heads_split: tokens [B, S, groups, H, D] -> groups
  * tensors heads[g] of [B, H, S, D]; heads_merge is the inverse. `heads` is a
  * host array of `groups` (1..4) device pointers; all tensors dense, of `dtype`.
@@ -132,7 +150,10 @@ int ferrite_hip_cross_entropy_bwd(const float* logits, const int64_t* targets, c
  *   g *= min(1, max_grad_norm / (gnorm + 1e-6))
  *   m = beta1*m + (1-beta1)*g;  v = beta2*v + (1-beta2)*g*g
  *   p -= lr * ((m/bc1) / (sqrt(v/bc2) + eps) + (decay[i] ? weight_decay : 0) * p)
- * with bc = 1 - beta^step. params[i] (param_dtype) and exp_avg[i], exp_avg_sq[i]
+ * with bc = 1 - beta^step. If step_scalars (device f32[3]) is not NULL, lr, bc1
+ * and bc2 are read from it at run time instead ({lr, 1 - beta1^step,
+ * 1 - beta2^step}; `lr` and `step` are then ignored), so a captured graph can
+ * replay the call with each step's values. params[i] (param_dtype) and exp_avg[i], exp_avg_sq[i]
  * (f32) are updated in place; grads[i] (grad_dtype) are read. The pointer, numel
  * and decay arrays are host memory; the tensors are device memory. grad_norm
  * (device f32 scalar, may be NULL) receives the pre-clip gnorm. `workspace` is
@@ -143,7 +164,8 @@ int64_t ferrite_hip_adamw_workspace(int64_t n_tensors);
 int ferrite_hip_adamw(int64_t n_tensors, void* const* params, const void* const* grads, float* const* exp_avg,
                       float* const* exp_avg_sq, const int64_t* numel, const int32_t* decay, int param_dtype,
                       int grad_dtype, float lr, float beta1, float beta2, float eps, float weight_decay,
-                      float max_grad_norm, int64_t step, float* grad_norm, void* workspace, void* stream);
+                      float max_grad_norm, int64_t step, const float* step_scalars, float* grad_norm,
+                      void* workspace, void* stream);
 
 /*
  * Flash attention forward (flash_attention.py:91-175).

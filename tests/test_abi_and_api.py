@@ -25,7 +25,7 @@ def _declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     declared = _declared_symbols()
-    assert len(declared) == 17
+    assert len(declared) == 19
     out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH], capture_output=True, text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s(\w+)", out))
     missing = [s for s in declared if s not in exported]
@@ -55,11 +55,11 @@ def test_abi_argument_checks_return_codes():
     assert lib.ferrite_hip_adamw_workspace(75) == (3 * 512 + 4) * 4
     assert lib.ferrite_hip_adamw_workspace(-1) == -1
     args = [None] * 6 + [_hip.BF16, _hip.BF16, 1e-3, 0.9, 0.95, 1e-8, 0.1, 1.0]
-    assert lib.ferrite_hip_adamw(1, *args, 1, None, 1, None) == 1
+    assert lib.ferrite_hip_adamw(1, *args, 1, None, None, 1, None) == 1
     assert "null" in _hip.last_error()
-    assert lib.ferrite_hip_adamw(0, *args, 0, None, 1, None) == 1
+    assert lib.ferrite_hip_adamw(0, *args, 0, None, None, 1, None) == 1
     assert "step" in _hip.last_error()
-    assert lib.ferrite_hip_adamw(0, *args[:6], 9, _hip.BF16, *args[8:], 1, None, 1, None) == 1
+    assert lib.ferrite_hip_adamw(0, *args[:6], 9, _hip.BF16, *args[8:], 1, None, None, 1, None) == 1
     # head layout: group count, dtype and null checks; empty is a no-op
     assert lib.ferrite_hip_heads_split(None, None, 0, 4, 3, 2, 8, _hip.BF16, None) == 0
     assert lib.ferrite_hip_heads_split(1, 1, 2, 4, 5, 2, 8, _hip.BF16, None) == 1

@@ -135,3 +135,87 @@ def test_bf16_dma_path_tails(dev, m, k, n):
             assert np.max(np.abs(got - exact)) <= 1e-5 * max(1.0, np.max(np.abs(exact))) * (1 + k / 64)
         else:
             assert np.all(np.abs(got - exact) <= bf16_ulp(exact) + 2.0 ** -20 * np.abs(x).sum(1, keepdims=True) @ np.abs(y).max(0, keepdims=True))
+
+
+_EXACT = {}
+
+
+def _exact_case(m, n, k):
+    """Seeded bf16 operands, their f64 product and the f32 accumulation bound (cached per shape)."""
+    if (m, n, k) not in _EXACT:
+        a = uniform(40 + m % 13, (m, k), "bf16")
+        b = uniform(41 + n % 11, (k, n), "bf16")
+        bound = 2.0**-20 * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)) + 1e-30
+        _EXACT.clear()
+        _EXACT[(m, n, k)] = (a, b, omm.reference(a, b), bound)
+    return _EXACT[(m, n, k)]
+
+
+def _mm_ex(xs, ys, m, n, k, x_t, y_t, out_dtype, workspace=True):
+    """ferrite_hip_matmul_ex through the C ABI on NaN-prefilled output."""
+    lib = _hip.lib()
+    out = torch.full((m, n), float("nan"), dtype=out_dtype, device=xs.device)
+    ws_bytes = lib.ferrite_hip_matmul_workspace(m, n, k, _hip.BF16) if workspace else 0
+    ws = torch.full(((ws_bytes + 3) // 4,), float("nan"), device=xs.device) if ws_bytes > 0 else None
+    rc = lib.ferrite_hip_matmul_ex(xs.data_ptr(), ys.data_ptr(), out.data_ptr(), m, n, k, int(x_t), int(y_t), _hip.BF16,
+                                   _hip.dtype_code(out_dtype), _hip.ptr(ws), max(ws_bytes, 0), _hip.stream_of(xs))
+    _hip.check(rc, "matmul_ex")
+    torch.cuda.synchronize()
+    return out, ws_bytes
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (768, 3072, 8192),   # a GPT weight gradient: 36 tiles, K split 8 ways
+    (768, 768, 4096),    # 9 tiles, K split 8 ways (512 deep)
+    (520, 264, 1024),    # ragged tile edges, K split
+    (1024, 2304, 768),   # 36 tiles but K too short to split
+    (8192, 768, 512),    # enough tiles: no split
+])
+@pytest.mark.parametrize("x_t,y_t", [(False, False), (True, False), (False, True), (True, True)])
+def test_transposed_operands_and_k_split(dev, m, n, k, x_t, y_t):
+    """out = op(x) @ op(y) with x and/or y read transposed in place, against the f64 product of the
+    same bf16 values: f32 output within the f32 accumulation bound, bf16 output within one bf16 ulp
+    of the exact product plus that bound. Every element is written, reruns are bitwise equal,
+    and the split and unsplit kernels agree to the f32 bound."""
+    a, b, exact, bound = _exact_case(m, n, k)
+    xs = to_dev(a.T.copy() if x_t else a, "bf16", dev)
+    ys = to_dev(b.T.copy() if y_t else b, "bf16", dev)
+    o32, ws_bytes = _mm_ex(xs, ys, m, n, k, x_t, y_t, torch.float32)
+    assert not torch.isnan(o32).any()
+    assert np.all(np.abs(to_np(o32).astype(np.float64) - exact) <= bound)
+    again, _ = _mm_ex(xs, ys, m, n, k, x_t, y_t, torch.float32)
+    assert torch.equal(o32, again)
+    nosplit, _ = _mm_ex(xs, ys, m, n, k, x_t, y_t, torch.float32, workspace=False)
+    assert np.all(np.abs(to_np(nosplit).astype(np.float64) - exact) <= bound)
+    o16, _ = _mm_ex(xs, ys, m, n, k, x_t, y_t, torch.bfloat16)
+    assert np.all(np.abs(to_np(o16).astype(np.float64) - exact) <= bf16_ulp(exact) + bound)
+    if m * n <= 768 * 768 and k >= 4096:
+        assert ws_bytes > 0  # the small-output shapes do split
+
+
+def test_transposed_operand_rules(dev):
+    """Transposed operands outside the DMA kernel's rule return an error; the Python wrapper
+    transposes into a copy instead (the VJP then still matches)."""
+    lib = _hip.lib()
+    x = torch.zeros(64, 100, device=dev, dtype=torch.bfloat16)  # K = 100: not a multiple of 64
+    y = torch.zeros(100, 64, device=dev, dtype=torch.bfloat16)
+    out = torch.empty(64, 64, device=dev, dtype=torch.bfloat16)
+    rc = lib.ferrite_hip_matmul_ex(x.data_ptr(), y.data_ptr(), out.data_ptr(), 64, 64, 100, 0, 1, _hip.BF16, _hip.BF16,
+                                   None, 0, _hip.stream_of(x))
+    assert rc == 1 and "transposed" in _hip.last_error()
+
+
+@pytest.mark.parametrize("m,k,n", [(1024, 768, 2304), (1000, 136, 72)])
+def test_vjp_reads_transposes_in_place(dev, m, k, n):
+    """Gradients of matmul through autograd (dx = g y^T, dy = x^T g on the transposed-operand
+    kernel, or on copies for shapes outside its rule) against f64 products of the same bf16 values,
+    held to the bf16 output bar (one ulp plus the f32 accumulation bound)."""
+    a, b, gg = normal(50, (m, k), "bf16"), normal(51, (k, n), "bf16"), normal(52, (m, n), "bf16")
+    xt, yt = to_dev(a, "bf16", dev).requires_grad_(), to_dev(b, "bf16", dev).requires_grad_()
+    matmul(xt, yt).backward(to_dev(gg, "bf16", dev))
+    for got, ex, absb in ((xt.grad, gg.astype(np.float64) @ b.T.astype(np.float64),
+                           np.abs(gg).astype(np.float64) @ np.abs(b.T).astype(np.float64)),
+                          (yt.grad, a.T.astype(np.float64) @ gg.astype(np.float64),
+                           np.abs(a.T).astype(np.float64) @ np.abs(gg).astype(np.float64))):
+        g64 = to_np(got).astype(np.float64)
+        assert np.all(np.abs(g64 - ex) <= bf16_ulp(ex) + 2.0**-20 * absb + 1e-30)

@@ -116,3 +116,41 @@ def test_baseline_train_step_config(dev):
     assert math.isfinite(float(gnorm)) and float(gnorm) > 0
     for (name, t), b in zip(named_leaves(params), before):
         assert not torch.equal(t, b), name
+
+
+@pytest.mark.parametrize("linear", ["pallas", "xla"])
+def test_graphed_step_matches_eager(dev, linear):
+    """The HIP-graph train step against the eager one, one step at a time from the same state:
+    before every step the eager tree is set to the graphed run's parameters and moments, then both
+    take the step on the same tokens (two eager warm-up calls, the capture, then replays with
+    eager work and synchronisations in between). Each step's loss, gradient norm, parameters
+    and moments must agree to 1e-6. A step moves parameters by ~lr = 3e-3 and the schedule's
+    lr changes by ~1e-4 per step here, so stale per-step values or a corrupted replay would
+    fail by orders of magnitude. (The runs are not compared as whole trajectories: the tied
+    head's products run on the library GEMM, and Adam amplifies last-bit differences of
+    near-cancelling moments over steps.)"""
+    cfg = GPTConfig(vocab_size=256, seq_len=128, d_model=256, n_head=2, n_layer=2, d_ff=512, linear=linear)
+    tcfg = TrainConfig(steps=10, warmup=2, lr=3e-3)
+    pa, pb = init_params(4, cfg, device=dev), init_params(4, cfg, device=dev)
+    sa, sb = adamw_init(pa), adamw_init(pb)
+    eager = build_train_step(cfg, tcfg)
+    graphed = build_train_step(cfg, tcfg, graph=True)
+    g = torch.Generator().manual_seed(6)
+    for i in range(6):
+        with torch.no_grad():
+            for a, b in zip(leaves(pa) + leaves(sa["m"]) + leaves(sa["v"]), leaves(pb) + leaves(sb["m"]) + leaves(sb["v"])):
+                a.copy_(b)
+        sa["step"] = sb["step"]
+        x = torch.randint(0, 256, (4, 128), generator=g).to(dev)
+        y = torch.randint(0, 256, (4, 128), generator=g).to(dev)
+        pa, sa, la, na = eager(pa, sa, x, y)
+        pb, sb, lb, nb = graphed(pb, sb, x, y)
+        la, lb = float(la), float(lb)
+        torch.cuda.synchronize()
+        assert abs(la - lb) <= 1e-6 * abs(la), (i, la, lb)
+        assert abs(float(na) - float(nb)) <= 1e-5 * float(na), (i, float(na), float(nb))
+        for (name, a), b in zip(named_leaves({"p": pa, "m": sa["m"], "v": sa["v"]}),
+                                leaves({"p": pb, "m": sb["m"], "v": sb["v"]})):
+            d = float((a.float() - b.float()).abs().max())
+            assert d <= 1e-6, (i, name, d)
+    assert graphed.graph is not None and sb["step"] == 6
