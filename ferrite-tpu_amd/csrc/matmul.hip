@@ -495,7 +495,9 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
 // the f32 partials would outweigh the work.
 int splitk_slices(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = cdiv(M, (int64_t)Gemm2::BM) * cdiv(N, (int64_t)Gemm2::BN);
-  if (tiles >= 64) return 1;
+  // Up to half the CUs busy and a long K (the 8192 x 768 outputs of a 768-wide model): two
+  // slices fill 3/4 of the CUs, and the two f32 partial slabs stay in the Infinity Cache.
+  if (tiles >= 64) return (tiles <= 128 && K >= 2048) ? 2 : 1;
   int64_t s = std::min<int64_t>({cdiv(256, tiles), K / 512, (int64_t)16});
   if (s < 2) return 1;
   const int64_t kslice = cdiv(cdiv(K, s), (int64_t)Gemm2::BK) * Gemm2::BK;

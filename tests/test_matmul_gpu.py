@@ -169,6 +169,7 @@ def _mm_ex(xs, ys, m, n, k, x_t, y_t, out_dtype, workspace=True):
     (768, 768, 4096),    # 9 tiles, K split 8 ways (512 deep)
     (520, 264, 1024),    # ragged tile edges, K split
     (1024, 2304, 768),   # 36 tiles but K too short to split
+    (8192, 768, 3072),   # 96 tiles, long K: split 2 ways
     (8192, 768, 512),    # enough tiles: no split
 ])
 @pytest.mark.parametrize("x_t,y_t", [(False, False), (True, False), (False, True), (True, True)])
