@@ -15,6 +15,9 @@ working set exceeds the 256 MB Infinity Cache) and the blocked matmul (bf16
 4096^3, f32 1000^3). Each carries its roofline fraction against MI355X peaks.
 "gpt_train_step" times the caller of these kernels: one forward+backward+AdamW
 step of the 12-layer GPT of BASELINE config 5 (bf16 parameters, batch 8 x 1024).
+"decode_attention" and "serving" time the serving side: the decode-attention
+kernel over a full 8192-key cache, and greedy generation at the reference's
+serving-benchmark config (TTFT, inter-token latency).
 
 cpu_baseline: the CPU oracle (numpy f32, the reference's materialised
 impl='xla' math) timed on this host's cores on a bounded sample of the same
@@ -271,6 +274,56 @@ def bench_gpt_train(steps, warmup, linear_routes=("pallas", "xla"), modes=("grap
     return out
 
 
+def bench_decode_attention(iters=20):
+    """Decode attention over a full static cache: B=8, H=32, max_len=8192, D=128 bf16, every
+    sequence at its last position. HBM-bound: each call reads all keys and values once
+    (8*32*8192*128*2*2 = 1.07 GB) and writes one row per head."""
+    import torch
+
+    from ferrite.kernels.decode_attention import decode_attention
+
+    dev = torch.device("cuda:0")
+    b, h, L, d = 8, 32, 8192, 128
+    g = torch.Generator(device=dev).manual_seed(21)
+    q, kn, vn = (torch.randn(b, h, d, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    kc = torch.randn(b, h, L, d, device=dev, generator=g).to(torch.bfloat16)
+    vc = torch.randn(b, h, L, d, device=dev, generator=g).to(torch.bfloat16)
+    pos = torch.full((b,), L - 1, dtype=torch.int32, device=dev)
+    t = _events_time(lambda: decode_attention(q, kn, vn, kc, vc, pos), iters, 3)
+    nbytes = 2 * b * h * L * d * 2 + 3 * b * h * d * 2 + 2 * b * h * d * 2
+    return {"shape": [b, h, L, d], "us": t * 1e6, "gbs": nbytes / t / 1e9, "bytes": nbytes,
+            "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS}
+
+
+def bench_serving(new_tokens=128, prompt_len=100, batches=(1, 8, 32)):
+    """The reference's serving benchmark (benchmarks/bench_serve.py): GPT seq 512, d_model 512,
+    4 layers, 4 heads, d_ff 2048, bf16, random init; prompts of 100 tokens, 128 new tokens,
+    greedy. Prefill and decode replay captured HIP graphs; decode attention runs on the HIP
+    kernel ("pallas") or on torch math ("xla", the reference's XLA decode)."""
+    import numpy as np
+    import torch
+
+    from ferrite.model.gpt import GPTConfig, init_params
+    from ferrite.serving.engine import Engine, ServeConfig
+
+    dev = torch.device("cuda:0")
+    cfg = GPTConfig(seq_len=512, d_model=512, n_head=4, n_layer=4, d_ff=2048)
+    params = init_params(0, cfg, device=dev)
+    rng = np.random.default_rng(0)
+    rows = []
+    for batch in batches:
+        for kernels in ("pallas", "xla"):
+            eng = Engine(params, cfg, ServeConfig(batch=batch, max_len=cfg.seq_len, buckets=(64, 128, 256),
+                                                  decode_kernels=kernels))
+            prompts = [list(rng.integers(1, 256, size=prompt_len)) for _ in range(batch)]
+            eng.generate(prompts, 4)
+            _, stats = eng.generate(prompts, new_tokens)
+            rows.append({"batch": batch, "decode_kernels": kernels, "prompt_len": prompt_len, "new_tokens": new_tokens,
+                         **{k: round(v, 4) if isinstance(v, float) else v for k, v in stats.items()}})
+            del eng
+    return rows
+
+
 def bench_copy(nbytes: int = 256 << 20, iters: int = 5):
     """A plain device-to-device copy of `nbytes`: reads and writes exactly nbytes, so FETCH_SIZE and
     WRITE_SIZE of its dispatch calibrate the byte counters; also a ceiling for streaming kernels."""
@@ -315,7 +368,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["attn", "rmsnorm", "matmul", "gpt", "all"], default="all")
+    ap.add_argument("--only", choices=["attn", "rmsnorm", "matmul", "gpt", "serve", "all"], default="all")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (the HBM byte-counter calibration for rocprofv3 --pmc)")
     a = ap.parse_args(argv)
@@ -341,6 +394,9 @@ def main(argv=None):
         kernels["matmul"] = bench_matmul(max(a.steps // 2, 3), 2)
     if a.only in ("gpt", "all"):
         kernels["gpt_train_step"] = bench_gpt_train(max(a.steps // 2, 3), 2)
+    if a.only in ("serve", "all"):
+        kernels["decode_attention"] = bench_decode_attention()
+        kernels["serving"] = bench_serving()
 
     att = kernels.get("attention")
     if att is not None:

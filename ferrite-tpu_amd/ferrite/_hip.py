@@ -43,6 +43,11 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _c_i64, _vp],
     ),
+    "ferrite_hip_decode_attention_workspace": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "ferrite_hip_decode_attention": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_f32, _vp, _c_i64, _vp],
+    ),
     "ferrite_hip_heads_split": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _vp]),
     "ferrite_hip_heads_merge": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _vp]),
     "ferrite_hip_cross_entropy_fwd": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _vp]),

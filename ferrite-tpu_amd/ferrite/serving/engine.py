@@ -1,0 +1,294 @@
+"""Greedy decoding with a static KV cache, replayed from captured HIP graphs.
+
+Reference: src/ferrite/serving/engine.py. Same split between prefill and decode,
+same cache layout, bucketing, API and statistics:
+
+* Prompts are right-padded to one of a few **buckets**. The reference compiles
+  each bucket's prefill ahead of time; here each bucket's prefill is captured
+  once into a HIP graph, and serving replays it, so no launch at serving time
+  depends on the Python model code.
+* The KV cache is a fixed ``[layers, batch, heads, max_len, head_dim]`` buffer
+  updated in place, and the decode step is one captured graph whatever the
+  position (positions live in device memory).
+* Prefill is compute-bound and runs the flash-attention kernel. Decode is
+  memory-bound: the reference leaves it to XLA and names a decode-attention
+  kernel as its next step; here ``decode_kernels="pallas"`` runs that kernel
+  (csrc/decode.hip), which writes the new key/value rows and attends over the
+  cache in one launch per layer.
+* ``jax.export`` (engine.py:206-228) has no counterpart: a captured graph is the
+  serialisation-free analogue, and it lives in the serving process.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+import time
+from typing import Any
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from ferrite.model.gpt import GPTConfig, _attention, _dot_f32, _linear, _merge_heads, _norm, _split_heads
+
+
+@dataclasses.dataclass(frozen=True)
+class ServeConfig:
+    """Serving settings (engine.py:35-40)."""
+
+    batch: int = 1
+    max_len: int = 512
+    buckets: tuple[int, ...] = (64, 128, 256)
+    prefill_kernels: str = "pallas"  # "pallas" | "xla": attention + norms in prefill
+    decode_kernels: str = "pallas"  # "pallas" (HIP decode attention + norms) | "xla" (torch math, as the reference)
+    graphs: bool = True  # replay prefill and decode from captured HIP graphs
+
+
+def bucket_for(length: int, buckets: tuple[int, ...]) -> int:
+    """The smallest bucket that holds ``length`` tokens (engine.py:43-47)."""
+    for b in buckets:
+        if length <= b:
+            return b
+    raise ValueError(f"prompt length {length} exceeds largest bucket {buckets[-1]}")
+
+
+# ---------------------------------------------------------------- model pieces
+
+
+def _block_prefill(layer, h, pending, cfg: GPTConfig):
+    """One transformer block over a full sequence, returning (h, pending, k, v) (engine.py:53-66)."""
+    if pending is None:
+        y = _norm(h, layer["ln1"], None, cfg)
+    else:
+        h, y = _norm(pending, layer["ln1"], h, cfg)
+    q, k, v = _split_heads(_linear(y, layer["wqkv"], cfg), cfg)  # [B, H, S, hd]
+    a = _linear(_merge_heads(_attention(q, k, v, cfg), cfg), layer["wo"], cfg)
+    h, y2 = _norm(a, layer["ln2"], h, cfg)
+    pending = _linear(F.gelu(_linear(y2, layer["w1"], cfg), approximate="tanh"), layer["w2"], cfg)
+    return h, pending, k, v
+
+
+@torch.no_grad()
+def prefill(params, tokens, lengths, cfg: GPTConfig, max_len: int, k_cache=None, v_cache=None):
+    """tokens [B, L] (right-padded), lengths [B] -> (next-token logits [B, V], k_cache, v_cache)
+    (engine.py:69-86). Caches are [layers, B, H, max_len, hd]; the prompt's keys and values
+    fill positions 0..L-1 (padding positions hold values decode never attends to and
+    overwrites in order). Given caches are written in place."""
+    b, s = tokens.shape
+    if k_cache is None:
+        shape = (cfg.n_layer, b, cfg.n_head, max_len, cfg.head_dim)
+        k_cache = torch.zeros(shape, dtype=cfg.dtype, device=tokens.device)
+        v_cache = torch.zeros(shape, dtype=cfg.dtype, device=tokens.device)
+    h = (params["tok_emb"][tokens] + params["pos_emb"][:s]).to(cfg.dtype)
+    pending = None
+    for i, layer in enumerate(params["layers"]):
+        h, pending, k, v = _block_prefill(layer, h, pending, cfg)
+        k_cache[i, :, :, :s].copy_(k)
+        v_cache[i, :, :, :s].copy_(v)
+    _, y = _norm(pending, params["ln_f"], h, cfg)
+    idx = (lengths.long() - 1).view(b, 1, 1).expand(b, 1, cfg.d_model)
+    last = torch.gather(y, 1, idx)[:, 0]  # [B, d]
+    logits = _dot_f32(last.contiguous(), params["tok_emb"].to(cfg.dtype).t())
+    return logits, k_cache, v_cache
+
+
+def _cache_attention(q, k_cache, v_cache, pos, scale):
+    """q [B, H, hd]; caches [B, H, max_len, hd]; pos [B]: f32 scores over keys <= pos
+    (engine.py:89-95)."""
+    s = torch.einsum("bhd,bhkd->bhk", q.float(), k_cache.float()) * scale
+    keys = torch.arange(k_cache.shape[2], device=q.device)[None, :]
+    s = torch.where((keys <= pos.long()[:, None])[:, None, :], s, torch.full_like(s, -1e30))
+    p = torch.softmax(s, dim=-1)
+    return torch.einsum("bhk,bhkd->bhd", p, v_cache.float()).to(q.dtype)
+
+
+def _write_cache(cache, new, pos):
+    """cache [B, H, max_len, hd] <- new [B, H, hd] at row pos[b] (engine.py:98-104), in place."""
+    idx = torch.arange(cache.shape[0], device=cache.device)
+    cache[idx, :, pos.long()] = new.to(cache.dtype)
+
+
+@torch.no_grad()
+def decode_step(params, token, pos, k_cache, v_cache, cfg: GPTConfig):
+    """One greedy decode step (engine.py:107-131): token [B] at position pos [B] -> logits
+    [B, V]; the caches are updated in place. ``cfg.attention == "pallas"`` runs the HIP
+    decode-attention kernel; otherwise the torch restatement of the reference's XLA math."""
+    b = token.shape[0]
+    h = (params["tok_emb"][token] + params["pos_emb"][pos.long()]).to(cfg.dtype)  # [B, d]
+    scale = 1.0 / math.sqrt(cfg.head_dim)
+    pending = None
+    for i, layer in enumerate(params["layers"]):
+        if pending is None:
+            y = _norm(h, layer["ln1"], None, cfg)
+        else:
+            h, y = _norm(pending, layer["ln1"], h, cfg)
+        qkv = _linear(y, layer["wqkv"], cfg).reshape(b, 3, cfg.n_head, cfg.head_dim)
+        q, k, v = (qkv[:, j].contiguous() for j in range(3))  # [B, H, hd]
+        if cfg.attention == "pallas":
+            from ferrite.kernels.decode_attention import decode_attention
+
+            a = decode_attention(q, k, v, k_cache[i], v_cache[i], pos, scale=scale)
+        else:
+            _write_cache(k_cache[i], k, pos)
+            _write_cache(v_cache[i], v, pos)
+            a = _cache_attention(q, k_cache[i], v_cache[i], pos, scale)
+        a = _linear(a.reshape(b, cfg.d_model), layer["wo"], cfg)
+        h, y2 = _norm(a, layer["ln2"], h, cfg)
+        pending = _linear(F.gelu(_linear(y2, layer["w1"], cfg), approximate="tanh"), layer["w2"], cfg)
+    _, y = _norm(pending, params["ln_f"], h, cfg)
+    return _dot_f32(y, params["tok_emb"].to(cfg.dtype).t())
+
+
+# ---------------------------------------------------------------- engine
+
+
+class _Captured:
+    """A function of fixed-address tensors, run eagerly once and then captured into a HIP graph."""
+
+    def __init__(self, fn, graphs: bool):
+        self.fn, self.graphs = fn, graphs
+        self.graph = None
+        self.out = None
+
+    def __call__(self):
+        if not self.graphs:
+            return self.fn()
+        if self.graph is None:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                self.fn()  # warm-up: library handles, allocator, kernel attributes
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                self.out = self.fn()
+        self.graph.replay()
+        return self.out
+
+
+class Engine:
+    """Prefill per bucket and one decode step, each captured as a HIP graph; greedy generation
+    (engine.py:137-203)."""
+
+    def __init__(self, params, model_cfg: GPTConfig, serve_cfg: ServeConfig, device=None):
+        if max(serve_cfg.buckets) > model_cfg.seq_len or serve_cfg.max_len > model_cfg.seq_len:
+            raise ValueError("buckets and max_len must fit within the model's trained seq_len (positional table)")
+        if max(serve_cfg.buckets) > serve_cfg.max_len:
+            raise ValueError("buckets must fit within max_len")
+        self.params = params
+        self.cfg = model_cfg
+        self.serve = serve_cfg
+        self.device = torch.device(device) if device is not None else params["tok_emb"].device
+        use_graphs = serve_cfg.graphs and self.device.type == "cuda"
+        if serve_cfg.prefill_kernels == "pallas":
+            self.prefill_cfg = model_cfg
+        else:
+            self.prefill_cfg = model_cfg.replace(attention="xla", norm="xla")
+        if serve_cfg.decode_kernels == "pallas":
+            self.decode_cfg = model_cfg
+        else:
+            self.decode_cfg = model_cfg.replace(attention="xla", norm="xla", linear="xla")
+        b, dev = serve_cfg.batch, self.device
+        shape = (model_cfg.n_layer, b, model_cfg.n_head, serve_cfg.max_len, model_cfg.head_dim)
+        self.k_cache = torch.zeros(shape, dtype=model_cfg.dtype, device=dev)
+        self.v_cache = torch.zeros(shape, dtype=model_cfg.dtype, device=dev)
+        self.lengths = torch.ones((b,), dtype=torch.int32, device=dev)
+        self.token = torch.zeros((b,), dtype=torch.long, device=dev)
+        self.pos = torch.zeros((b,), dtype=torch.int32, device=dev)
+        self.compile_seconds: dict[str, float] = {}
+        self._prefill: dict[int, Any] = {}
+        self._tokens: dict[int, torch.Tensor] = {}
+        for bucket in serve_cfg.buckets:
+            t0 = time.perf_counter()
+            toks = torch.zeros((b, bucket), dtype=torch.long, device=dev)
+            self._tokens[bucket] = toks
+
+            def run(toks=toks):
+                logits, _, _ = prefill(self.params, toks, self.lengths, self.prefill_cfg, serve_cfg.max_len,
+                                       self.k_cache, self.v_cache)
+                return logits
+
+            self._prefill[bucket] = _Captured(run, use_graphs)
+            self._prefill[bucket]()  # capture now, as the reference compiles ahead of time
+            self.compile_seconds[f"prefill_{bucket}"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        self._decode = _Captured(
+            lambda: decode_step(self.params, self.token, self.pos, self.k_cache, self.v_cache, self.decode_cfg),
+            use_graphs)
+        self._decode()
+        self.compile_seconds["decode"] = time.perf_counter() - t0
+        self.n_compiles = len(self.compile_seconds)
+        self.k_cache.zero_()
+        self.v_cache.zero_()
+
+    # -- public API ---------------------------------------------------------
+
+    def prefill(self, prompts: list[list[int]]):
+        """Returns (first token [B], pos [B], caches). Prompts are right-padded to a bucket."""
+        b = self.serve.batch
+        if len(prompts) != b:
+            raise ValueError(f"engine built for batch {b}, got {len(prompts)} prompts")
+        lengths = np.array([len(p) for p in prompts], np.int32)
+        if lengths.min() < 1:
+            raise ValueError("empty prompt")
+        bucket = bucket_for(int(lengths.max()), self.serve.buckets)
+        tokens = np.zeros((b, bucket), np.int64)
+        for i, p in enumerate(prompts):
+            tokens[i, : len(p)] = p
+        self._tokens[bucket].copy_(torch.from_numpy(tokens))
+        self.lengths.copy_(torch.from_numpy(lengths))
+        logits = self._prefill[bucket]()
+        return torch.argmax(logits, dim=-1), self.lengths.clone(), self.k_cache, self.v_cache
+
+    def decode(self, token, pos, kc=None, vc=None):
+        """One step from ``token`` at ``pos``; returns (next token, caches)."""
+        self.token.copy_(token)
+        self.pos.copy_(pos)
+        logits = self._decode()
+        return torch.argmax(logits, dim=-1), self.k_cache, self.v_cache
+
+    def generate(self, prompts: list[list[int]], max_new_tokens: int) -> tuple[np.ndarray, dict]:
+        """Greedy generation; returns generated tokens [B, max_new_tokens] and timing stats."""
+        if max(len(p) for p in prompts) + max_new_tokens > self.serve.max_len:
+            raise ValueError("prompt + new tokens exceed max_len")
+        sync = torch.cuda.synchronize if self.device.type == "cuda" else (lambda: None)
+        t0 = time.perf_counter()
+        token, pos, _, _ = self.prefill(prompts)
+        out = [token.cpu().numpy()]  # waits for the prefill
+        ttft = time.perf_counter() - t0
+        step_times = []
+        for _ in range(max_new_tokens - 1):
+            t = time.perf_counter()
+            token, _, _ = self.decode(token, pos)
+            out.append(token.cpu().numpy())
+            step_times.append(time.perf_counter() - t)
+            pos = pos + 1
+        sync()
+        total = time.perf_counter() - t0
+        stats = {
+            "ttft_ms": ttft * 1e3,
+            "itl_ms_median": float(np.median(step_times)) * 1e3 if step_times else float("nan"),
+            "itl_ms_p99": float(np.percentile(step_times, 99)) * 1e3 if step_times else float("nan"),
+            "tokens_per_second": len(prompts) * max_new_tokens / total,
+            "total_s": total,
+            "n_compiles": self.n_compiles,
+        }
+        return np.stack(out, axis=1), stats
+
+
+@torch.no_grad()
+def reference_greedy(params, cfg: GPTConfig, prompt: list[int], max_new_tokens: int) -> np.ndarray:
+    """Slow but obviously correct greedy decoding: the full model re-run each step (engine.py:231-242)."""
+    from ferrite.model.gpt import forward
+
+    dev = params["tok_emb"].device
+    toks = list(prompt)
+    out = []
+    for _ in range(max_new_tokens):
+        logits = forward(params, torch.tensor([toks], dtype=torch.long, device=dev), cfg)
+        nxt = int(torch.argmax(logits[0, -1]))
+        out.append(nxt)
+        toks.append(nxt)
+    return np.array(out)

@@ -29,6 +29,8 @@
  *   ferrite_hip_adamw         ../model/train.py:59-74    (adamw_update, XLA fusions in the reference)
  *   ferrite_hip_cross_entropy_fwd/_bwd ../model/gpt.py:147-152 (loss_fn and its autodiff, XLA in the reference)
  *   ferrite_hip_heads_split/_merge ../model/gpt.py:137-138 (the head transposes, XLA copies in the reference)
+ *   ferrite_hip_decode_attention ../serving/engine.py:89-104 (_cache_attention + _write_cache, XLA in the
+ *                                                          reference, whose README.md:283-285 names this kernel next)
  *
  * The one layout change against the reference: the softmax statistics
  * (logsumexp `lse` and `delta`) are compact f32 [B, H, S] arrays instead of the
@@ -116,6 +118,22 @@ int ferrite_hip_matmul(const void* x, const void* y, void* out, int64_t m, int64
 int64_t ferrite_hip_matmul_workspace(int64_t m, int64_t n, int64_t k, int in_dtype);
 int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k, int x_t, int y_t,
                           int in_dtype, int out_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Decode attention over a static KV cache (../serving/engine.py:89-104).
+ * q, k_new, v_new: [B, H, D]; k_cache, v_cache: [B, H, max_len, D], all of
+ * `dtype`; pos: device int32 [B]. Writes k_new/v_new into the caches at row
+ * pos[b], then out[b, h] = softmax_j(scale * q . k_j) . v_j over j = 0..pos[b]
+ * (f32 statistics). A pos outside [0, max_len) writes nothing and gives NaN.
+ * D in {64, 128, 256}; all pointers 16-byte aligned. With max_len > 256 the
+ * keys are split over workgroups and `workspace` (device memory of
+ * ferrite_hip_decode_attention_workspace(b, h, max_len, d) bytes) holds the
+ * f32 partials.
+ */
+int64_t ferrite_hip_decode_attention_workspace(int64_t b, int64_t h, int64_t max_len, int64_t d);
+int ferrite_hip_decode_attention(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                                 const int32_t* pos, void* out, int64_t b, int64_t h, int64_t max_len, int64_t d,
+                                 int dtype, float scale, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Head layout changes. heads_split: tokens [B, S, groups, H, D] -> groups
