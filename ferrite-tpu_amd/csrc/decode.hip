@@ -177,25 +177,52 @@ __global__ __launch_bounds__(kDecThreads) void decode_attn_kernel(const T* __res
 }
 
 // One block per head: merge the chunks that hold keys (0..pos) and normalise.
+// Loads go out eight chunks at a time, so a thread waits on a few batches of
+// independent loads rather than on one chain of dependent ones. An empty chunk
+// (m = -inf, l = acc = 0) gets weight exp2(-inf) = 0.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void decode_combine_kernel(const float* __restrict__ part, const int32_t* __restrict__ pos,
                                                              T* __restrict__ out, int nchunks, int max_len) {
+  constexpr int G = 8;
+  constexpr int S = D + 2;  // floats per chunk partial
   const int h = blockIdx.x, b = blockIdx.y, H = gridDim.x;
   const int64_t bh = (int64_t)b * H + h;
   const int p = pos[b];
   const bool valid = p >= 0 && p < max_len;
   const int used = valid ? min(nchunks, p / kChunk + 1) : 0;
-  const float* src = part + bh * nchunks * (D + 2);
+  const float* src = part + bh * nchunks * S;
   float mx = -INFINITY;
-  for (int s = 0; s < used; ++s) mx = fmaxf(mx, src[s * (D + 2) + D]);
+  int s0 = 0;
+  for (; s0 + G <= used; s0 += G) {
+    float m[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) m[j] = src[(s0 + j) * S + D];
+#pragma unroll
+    for (int j = 0; j < G; ++j) mx = fmaxf(mx, m[j]);
+  }
+  for (; s0 < used; ++s0) mx = fmaxf(mx, src[s0 * S + D]);
   for (int e = threadIdx.x; e < D; e += blockDim.x) {
     float l = 0.f, a = 0.f;
-    for (int s = 0; s < used; ++s) {
-      const float ms = src[s * (D + 2) + D];
-      if (ms == -INFINITY) continue;
-      const float w = exp2f(ms - mx);
-      l += src[s * (D + 2) + D + 1] * w;
-      a += src[s * (D + 2) + e] * w;
+    int s = 0;
+    for (; s + G <= used; s += G) {
+      float m[G], lv[G], av[G];
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        m[j] = src[(s + j) * S + D];
+        lv[j] = src[(s + j) * S + D + 1];
+        av[j] = src[(s + j) * S + e];
+      }
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        const float w = exp2f(m[j] - mx);
+        l += lv[j] * w;
+        a += av[j] * w;
+      }
+    }
+    for (; s < used; ++s) {
+      const float w = exp2f(src[s * S + D] - mx);
+      l += src[s * S + D + 1] * w;
+      a += src[s * S + e] * w;
     }
     out[bh * D + e] = Elem<T>::from_f32(valid ? a / l : NAN);
   }

@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import argparse
 import dataclasses
+import gc
 import json
 import math
 import os
@@ -233,6 +234,8 @@ class GraphedTrainStep:
         else:
             if self.graph is None:
                 torch.cuda.synchronize()
+                # No graph may be destroyed during a capture: collect unreachable ones first.
+                gc.collect()
                 self.graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(self.graph):
                     self.loss = self._body()

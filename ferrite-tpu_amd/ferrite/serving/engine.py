@@ -22,6 +22,7 @@ same cache layout, bucketing, API and statistics:
 from __future__ import annotations
 
 import dataclasses
+import gc
 import math
 import time
 from typing import Any
@@ -161,6 +162,9 @@ class _Captured:
                 self.fn()  # warm-up: library handles, allocator, kernel attributes
             torch.cuda.current_stream().wait_stream(side)
             torch.cuda.synchronize()
+            # A graph may not be destroyed while another is being captured: collect unreachable
+            # objects (a dropped engine's graphs among them) now rather than mid-capture.
+            gc.collect()
             self.graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(self.graph):
                 self.out = self.fn()
@@ -200,23 +204,24 @@ class Engine:
         self.compile_seconds: dict[str, float] = {}
         self._prefill: dict[int, Any] = {}
         self._tokens: dict[int, torch.Tensor] = {}
+        # The captured functions hold the tensors they use, not the engine: no reference cycle,
+        # so a dropped engine frees its graphs at once.
+        p_, kc, vc, lens, tok, pos = self.params, self.k_cache, self.v_cache, self.lengths, self.token, self.pos
+        pcfg, dcfg, max_len = self.prefill_cfg, self.decode_cfg, serve_cfg.max_len
         for bucket in serve_cfg.buckets:
             t0 = time.perf_counter()
             toks = torch.zeros((b, bucket), dtype=torch.long, device=dev)
             self._tokens[bucket] = toks
 
             def run(toks=toks):
-                logits, _, _ = prefill(self.params, toks, self.lengths, self.prefill_cfg, serve_cfg.max_len,
-                                       self.k_cache, self.v_cache)
+                logits, _, _ = prefill(p_, toks, lens, pcfg, max_len, kc, vc)
                 return logits
 
             self._prefill[bucket] = _Captured(run, use_graphs)
             self._prefill[bucket]()  # capture now, as the reference compiles ahead of time
             self.compile_seconds[f"prefill_{bucket}"] = time.perf_counter() - t0
         t0 = time.perf_counter()
-        self._decode = _Captured(
-            lambda: decode_step(self.params, self.token, self.pos, self.k_cache, self.v_cache, self.decode_cfg),
-            use_graphs)
+        self._decode = _Captured(lambda: decode_step(p_, tok, pos, kc, vc, dcfg), use_graphs)
         self._decode()
         self.compile_seconds["decode"] = time.perf_counter() - t0
         self.n_compiles = len(self.compile_seconds)

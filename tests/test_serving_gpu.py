@@ -123,3 +123,25 @@ def test_graph_replay_matches_eager_engine(dev):
     ga2, _ = a.generate([p[:3] for p in prompts], 5)  # the small bucket, after the large one
     gb2, _ = b.generate([p[:3] for p in prompts], 5)
     np.testing.assert_array_equal(ga2, gb2)
+
+
+def test_engines_built_after_dropped_ones(dev):
+    """Engines are built, used and dropped in a loop, as the serving benchmark does: a dropped
+    engine's graphs must be gone before the next engine captures (no graph may be destroyed
+    during a capture), so each new engine still matches the eager one."""
+    import gc
+    import weakref
+
+    cfg = CFG.replace(dtype=torch.bfloat16, n_head=4)
+    params = init_params(3, cfg, device=dev)
+    ref = Engine(params, cfg, ServeConfig(batch=2, max_len=128, buckets=(32,), graphs=False))
+    want, _ = ref.generate([[1, 2, 3], [4, 5]], 6)
+    for batch_kernels in ("pallas", "xla", "pallas"):
+        eng = Engine(params, cfg, ServeConfig(batch=2, max_len=128, buckets=(32,), decode_kernels=batch_kernels))
+        got, _ = eng.generate([[1, 2, 3], [4, 5]], 6)
+        if batch_kernels == "pallas":
+            np.testing.assert_array_equal(got, want)
+        alive = weakref.ref(eng._decode)
+        del eng
+        assert alive() is None  # freed without waiting for the cycle collector
+    gc.collect()
