@@ -32,9 +32,10 @@ struct Vec16 {
   static constexpr int N = 16 / sizeof(T);
 };
 
-template <typename T>
+// NT: a streaming load (the cache rows are read once per step).
+template <typename T, bool NT = false>
 __device__ __forceinline__ void load_vec(const T* p, float* out) {
-  const u32x4 raw = *reinterpret_cast<const u32x4*>(p);
+  const u32x4 raw = NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)) : *reinterpret_cast<const u32x4*>(p);
   if constexpr (sizeof(T) == 2) {
     const bf16x8 v = __builtin_bit_cast(bf16x8, raw);
 #pragma unroll
@@ -107,8 +108,8 @@ __global__ __launch_bounds__(kDecThreads) void decode_attn_kernel(const T* __res
     for (int u = 0; u < kUnroll; ++u) {
       const int r = r0 + rs + u * RPW + grp;
       if (r < last) {
-        load_vec(kb + (int64_t)r * D + sub * V, kv[u]);
-        load_vec(vb + (int64_t)r * D + sub * V, vv[u]);
+        load_vec<T, true>(kb + (int64_t)r * D + sub * V, kv[u]);
+        load_vec<T, true>(vb + (int64_t)r * D + sub * V, vv[u]);
       } else if (r == last) {
         load_vec(k_new + bh * D + sub * V, kv[u]);
         load_vec(v_new + bh * D + sub * V, vv[u]);
