@@ -1839,43 +1839,55 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
   store_acc_rows<bf16, D, true>(dva, dv + (int64_t)bh * Sk * d, kvrow, Sk, d, 1.0f);
 }
 
-template <int D>
+// W waves of 32 queries; SLOTS K/V tile slots in LDS (3: tiles t + 1 and t + 2
+// load while tile t is used; 2: only t + 1, which halves the LDS so that two
+// workgroups share a CU).
+template <int D, int W = 8, int SLOTS = 3>
 struct DqPp {
-  static constexpr int kWaves = 8, kThreads = 64 * kWaves;
+  static constexpr int kWaves = W, kThreads = 64 * kWaves;
   static constexpr int BQ = 32 * kWaves, BK = 64, KS = D / 16, DT = D / 32;
   typedef BwdTile<D> Tile;
-  static constexpr int kSlots = 3;
+  static constexpr int kSlots = SLOTS;
   static constexpr int kSlotBytes = 2 * Tile::kBytes;  // K then V
   static constexpr int kLds = kSlots * kSlotBytes;
   static constexpr int kDma = Tile::kBlocks / kWaves;  // per wave per tile, for K and for V
+  static_assert(SLOTS == 2 || SLOTS == 3, "two or three slots");
+  static_assert(Tile::kBlocks % kWaves == 0, "tile blocks split evenly over the waves");
 };
 
-// dQ for 256 queries (32 per wave, Q and dO fragments in registers),
-// sweeping 64-key tiles up to the diagonal. Waves w and w + 4 share a SIMD.
+// dQ for 32 W queries (32 per wave, Q and dO fragments in registers),
+// sweeping 64-key tiles up to the diagonal. With 8 waves, waves w and w + 4
+// share a SIMD. ZIG (a grid resident all at once, two workgroups per CU):
+// the second half of the grid takes the light query tiles in rising order,
+// so that block b and block b + grid / 2 pair a long and a short sweep.
 // Per 32-key half: S^T = K Q^T and dP^T = V dO^T from row reads of the K and
 // V tiles, dS^T = P^T (dP^T - delta) on the VALU (one query per lane, so lse
 // and delta are per-lane scalars), then dQ^T += K^T dS^T from transposed
 // reads of the K tile.
-template <int D>
-__global__ __launch_bounds__(512, 2) void attn_dq_pp_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
-                                                           const bf16* __restrict__ v, const bf16* __restrict__ dout,
-                                                           const float* __restrict__ lse,
-                                                           const float* __restrict__ delta, bf16* __restrict__ dq,
-                                                           int bh_count, int Sq, int Sk, int d, int causal,
-                                                           float scale, float scale_log2, int n_qtiles) {
-  typedef DqPp<D> F;
+template <int D, int W, int SLOTS, bool ZIG>
+__global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                                const bf16* __restrict__ v,
+                                                                const bf16* __restrict__ dout,
+                                                                const float* __restrict__ lse,
+                                                                const float* __restrict__ delta,
+                                                                bf16* __restrict__ dq, int bh_count, int Sq, int Sk,
+                                                                int d, int causal, float scale, float scale_log2,
+                                                                int n_qtiles) {
+  typedef DqPp<D, W, SLOTS> F;
   typedef typename F::Tile Tile;
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
   // Heaviest (last) query tiles first.
   const int bh = blockIdx.x % bh_count;
-  const int qt = n_qtiles - 1 - (int)(blockIdx.x / bh_count);
+  const int blk = (int)(blockIdx.x / bh_count);
+  const int half_q = n_qtiles / 2;
+  const int qt = !ZIG ? n_qtiles - 1 - blk : blk < n_qtiles - half_q ? n_qtiles - 1 - blk : blk - (n_qtiles - half_q);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
-  // SIMD w % 4 holds row blocks 2 (w % 4) and 2 (w % 4) + 1.
+  // 8 waves: SIMD w % 4 holds row blocks 2 (w % 4) and 2 (w % 4) + 1.
   const int q0 = qt * F::BQ;
-  const int q0w = q0 + 32 * (2 * (wave & 3) + (wave >> 2));
+  const int q0w = q0 + 32 * (W == 8 ? 2 * (wave & 3) + (wave >> 2) : wave);
   const int qrow = q0w + l32;
 
   const bf16* qb = q + (int64_t)bh * Sq * d;
@@ -1888,7 +1900,7 @@ __global__ __launch_bounds__(512, 2) void attn_dq_pp_kernel(const bf16* __restri
   const bool wave_active = q0w < Sq;
   const int n_w = !wave_active ? 0 : causal ? min(min(q0w + 31, Sq - 1), Sk - 1) / F::BK + 1 : n;
 
-  const PpDma<Tile, true, 8> dma(wave, d);
+  const PpDma<Tile, true, W> dma(wave, d);
   auto slot = [&](int t) { return smem + (t % F::kSlots) * F::kSlotBytes; };
   auto issue_tile = [&](int t) {
     char* sl = slot(t);
@@ -1903,8 +1915,10 @@ __global__ __launch_bounds__(512, 2) void attn_dq_pp_kernel(const bf16* __restri
   const float nlse2 = qok ? -lse[(int64_t)bh * Sq + qrow] * kLog2e : 0.f;
   const float dl = qok ? delta[(int64_t)bh * Sq + qrow] : 0.f;
 
+  // Tiles 0 .. SLOTS - 2 go out first; tile t + SLOTS - 1 is issued after
+  // tile t's barrier, into the slot tile t - 1 left.
   issue_tile(0);
-  if (n > 1) issue_tile(1);
+  if (SLOTS == 3 && n > 1) issue_tile(1);
 
   f32x16 acc[F::DT];
 #pragma unroll
@@ -1994,14 +2008,15 @@ __global__ __launch_bounds__(512, 2) void attn_dq_pp_kernel(const bf16* __restri
   bf16x8 dsf[2];
   auto nop = [] {};
   for (int t = 0; t < n; ++t) {
-    // Tile t complete for this wave (tile t + 1 may be in flight); after the
-    // barrier every wave has left tile t - 1's slot, which tile t + 2 takes.
-    if (t + 1 < n)
+    // Tile t complete for this wave (with three slots tile t + 1 may be in
+    // flight); after the barrier every wave has left tile t - 1's slot, which
+    // tile t + SLOTS - 1 takes.
+    if (SLOTS == 3 && t + 1 < n)
       wait_vmem<2 * F::kDma>();
     else
       wait_vmem<0>();
     lds_barrier();
-    if (t + 2 < n) issue_tile(t + 2);
+    if (t + SLOTS - 1 < n) issue_tile(t + SLOTS - 1);
     if (t >= n_w) continue;
     const char* sl = slot(t);
     const int kv0 = t * F::BK;
@@ -2145,20 +2160,36 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
   return check_launch("ferrite_flash_attention_fwd");
 }
 
-template <int D>
-int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
-                 void* dq, const Shape& s, int causal, float scale, hipStream_t stream) {
-  typedef DqPp<D> F;
+template <int D, int W, int SLOTS, bool ZIG>
+int dq_pp_launch_t(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
+                   void* dq, const Shape& s, int causal, float scale, hipStream_t stream) {
+  typedef DqPp<D, W, SLOTS> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq: grid too large");
-  auto kern = attn_dq_pp_kernel<D>;
+  auto kern = attn_dq_pp_kernel<D, W, SLOTS, ZIG>;
   set_lds(kern, F::kLds);
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
                      delta, static_cast<bf16*>(dq), (int)bh, (int)s.sq, (int)s.sk, (int)s.d, causal, scale,
                      scale * kLog2e, (int)nq);
   return check_launch("ferrite_flash_attention_bwd_dq");
+}
+
+template <int D>
+int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
+                 void* dq, const Shape& s, int causal, float scale, hipStream_t stream) {
+  if constexpr (D == 64) {
+    // 128-query workgroups of 4 waves with two LDS slots (67 KB): two share a
+    // CU. A grid resident all at once (the long-context case) pairs long and
+    // short causal sweeps on each CU.
+    typedef DqPp<64, 4, 2> F4;
+    const bool one_round = causal && cdiv(s.sq, F4::BQ) * s.b * s.h <= 2 * (int64_t)cu_count();
+    return one_round ? dq_pp_launch_t<D, 4, 2, true>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream)
+                     : dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream);
+  } else {
+    return dq_pp_launch_t<D, 8, 3, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream);
+  }
 }
 
 template <typename T, int D, bool AL>
