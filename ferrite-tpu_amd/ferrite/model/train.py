@@ -245,8 +245,10 @@ class GraphedTrainStep:
         return params, {"m": opt["m"], "v": opt["v"], "step": step}, loss, self.gnorm
 
 
-def train(model_cfg: GPTConfig, train_cfg: TrainConfig, *, verbose: bool = True, device=None) -> dict[str, Any]:
-    """Train for ``train_cfg.steps`` steps and return the results dictionary (train.py:102-177)."""
+def train(model_cfg: GPTConfig, train_cfg: TrainConfig, *, verbose: bool = True, device=None,
+          graph: bool = False) -> dict[str, Any]:
+    """Train for ``train_cfg.steps`` steps and return the results dictionary (train.py:102-177).
+    ``graph=True`` replays the step from a captured HIP graph (see :class:`GraphedTrainStep`)."""
     device = torch.device(device) if device is not None else default_device()
     corpus = data_lib.load(train_cfg.data)
     train_data, _ = data_lib.split(corpus)
@@ -256,7 +258,7 @@ def train(model_cfg: GPTConfig, train_cfg: TrainConfig, *, verbose: bool = True,
     n_params = param_count(params)
     n_nonembed = n_params - params["tok_emb"].numel() - params["pos_emb"].numel()
     opt = adamw_init(params)
-    step_fn = build_train_step(model_cfg, train_cfg)
+    step_fn = build_train_step(model_cfg, train_cfg, graph=graph)
 
     def batch():
         x, y = data_lib.get_batch(rng, train_data, train_cfg.batch, model_cfg.seq_len)
@@ -346,17 +348,24 @@ def main(argv=None):
     ap.add_argument("--attention", choices=["pallas", "xla"], default="pallas")
     ap.add_argument("--norm", choices=["pallas", "xla"], default="pallas")
     ap.add_argument("--linear", choices=["pallas", "xla"], default="xla")
+    ap.add_argument("--loss", choices=["pallas", "xla"], default="pallas",
+                    help="tied head + cross-entropy on the HIP loss kernels or torch's cross_entropy")
     ap.add_argument("--dtype", choices=["bfloat16", "float32"], default="bfloat16")
     ap.add_argument("--lr", type=float, default=6e-4)
     ap.add_argument("--data", choices=["tinyshakespeare", "synthetic"], default="tinyshakespeare")
     ap.add_argument("--out", default=None, help="results JSON path")
     ap.add_argument("--save-params", default=None, help=".npz checkpoint path")
+    ap.add_argument("--optimizer", choices=["fused", "foreach"], default=None,
+                    help="AdamW on the fused HIP kernel (default on a GPU) or torch multi-tensor ops (default on CPU)")
+    ap.add_argument("--graph", action="store_true", help="replay the step from a captured HIP graph")
     a = ap.parse_args(argv)
     dtype = {"bfloat16": torch.bfloat16, "float32": torch.float32}[a.dtype]
-    mcfg = GPTConfig(seq_len=a.seq, d_model=a.d_model, n_head=a.heads, n_layer=a.layers, d_ff=a.d_ff, attention=a.attention, norm=a.norm, linear=a.linear, dtype=dtype)
-    tcfg = TrainConfig(steps=a.steps, batch=a.batch, lr=a.lr, data=a.data, out=a.out, save_params=a.save_params)
+    mcfg = GPTConfig(seq_len=a.seq, d_model=a.d_model, n_head=a.heads, n_layer=a.layers, d_ff=a.d_ff, attention=a.attention, norm=a.norm, linear=a.linear, loss=a.loss, dtype=dtype)
+    optimizer = a.optimizer or ("fused" if platform.is_rocm() else "foreach")
+    tcfg = TrainConfig(steps=a.steps, batch=a.batch, lr=a.lr, data=a.data, out=a.out, save_params=a.save_params,
+                       optimizer=optimizer)
     with platform.interpret_mode():
-        res = train(mcfg, tcfg)
+        res = train(mcfg, tcfg, graph=a.graph)
     print(json.dumps({k: v for k, v in res.items() if k != "loss_curve"}, indent=2, default=str))
 
 

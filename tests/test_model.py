@@ -186,3 +186,17 @@ def test_short_training_run_reduces_loss_on_cpu(tmp_path):
     back = load_params(str(tmp_path / "p.npz"), cfg)
     assert [n for n, _ in named_leaves(back)] == [n for n, _ in named_leaves(init_params(0, cfg))]
     assert not torch.equal(back["tok_emb"], init_params(0, cfg)["tok_emb"])  # trained
+
+
+def test_cli_on_cpu(tmp_path):
+    """The command line (train.py:201-240 in the reference) runs the torch routes on the CPU and picks
+    the multi-tensor optimizer there by default."""
+    from ferrite.model.train import main
+
+    out = tmp_path / "cli.json"
+    main(["--steps", "2", "--batch", "2", "--seq", "32", "--layers", "1", "--d-model", "32", "--heads", "1",
+          "--d-ff", "64", "--data", "synthetic", "--dtype", "float32", "--attention", "xla", "--norm", "xla",
+          "--linear", "xla", "--loss", "xla", "--out", str(out)])
+    res = json.loads(out.read_text())
+    assert res["train"]["optimizer"] == "foreach" and res["model"]["loss"] == "xla"
+    assert np.isfinite(res["loss_last"])
