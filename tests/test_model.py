@@ -189,7 +189,7 @@ def test_short_training_run_reduces_loss_on_cpu(tmp_path):
 
 
 def test_cli_on_cpu(tmp_path):
-    """The command line (train.py:201-240 in the reference) runs the torch routes on the CPU and picks
+    """The command line (train.py:201-227 in the reference) runs the torch routes on the CPU and picks
     the multi-tensor optimizer there by default."""
     from ferrite.model.train import main
 
