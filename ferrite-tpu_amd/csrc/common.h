@@ -160,6 +160,8 @@ __device__ __forceinline__ float wave_sum(float x) {
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
+// Compute units of the current device (256 on an MI355X).
+int cu_count();
 
 inline bool valid_dtype(int dt) { return dt == FERRITE_F32 || dt == FERRITE_BF16; }
 inline const char* dtype_name(int dt) { return dt == FERRITE_F32 ? "f32" : dt == FERRITE_BF16 ? "bf16" : "?"; }

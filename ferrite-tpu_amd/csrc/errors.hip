@@ -1,4 +1,5 @@
 // Per-thread error reporting of the C ABI (ferrite_hip_last_error).
+#include <atomic>
 #include <string>
 
 #include "common.h"
@@ -19,6 +20,20 @@ int check_launch(const char* what) {
   if (e != hipSuccess) return fail(FERRITE_ERR_LAUNCH, std::string(what) + ": " + hipGetErrorString(e));
   g_last_error.clear();
   return FERRITE_OK;
+}
+
+// Compute units of the current device, looked up once per device. Racing
+// first calls store the same value.
+int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 }  // namespace ferrite

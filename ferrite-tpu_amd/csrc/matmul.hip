@@ -490,15 +490,18 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
     *reinterpret_cast<f32x4*>(out + i) = acc;
 }
 
-// K slices for a problem with few output tiles: enough slices to give every CU a
-// workgroup, each at least 512 deep; 1 when the tiles already fill most CUs or
-// the f32 partials would outweigh the work.
+// K slices for a problem with few output tiles: as many slices as keep every
+// workgroup in one round (one per CU), each at least 512 deep; 1 when the tiles
+// already fill most CUs or the f32 partials would outweigh the work. A round
+// that spills over by a few workgroups costs a whole second round: 36 tiles in
+// 8 slices (288 workgroups on 256 CUs) take longer than in 7.
 int splitk_slices(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = cdiv(M, (int64_t)Gemm2::BM) * cdiv(N, (int64_t)Gemm2::BN);
+  const int64_t cus = cu_count();
   // Up to half the CUs busy and a long K (the 8192 x 768 outputs of a 768-wide model): two
   // slices fill 3/4 of the CUs, and the two f32 partial slabs stay in the Infinity Cache.
-  if (tiles >= 64) return (tiles <= 128 && K >= 2048) ? 2 : 1;
-  int64_t s = std::min<int64_t>({cdiv(256, tiles), K / 512, (int64_t)16});
+  if (tiles >= cus / 4) return (2 * tiles <= cus && K >= 2048) ? 2 : 1;
+  int64_t s = std::min<int64_t>({cus / tiles, K / 512, (int64_t)16});
   if (s < 2) return 1;
   const int64_t kslice = cdiv(cdiv(K, s), (int64_t)Gemm2::BK) * Gemm2::BK;
   return (int)cdiv(K, kslice);

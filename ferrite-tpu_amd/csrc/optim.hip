@@ -27,7 +27,7 @@ namespace {
 constexpr int kAdamGroup = 32;                // tensors per launch (kernel-argument table)
 constexpr int kAdamThreads = 256;
 constexpr int kAdamTile = kAdamThreads * 8;   // elements per block iteration (8 per thread)
-constexpr int kAdamNormBlocks = 512;          // partial sums per group
+constexpr int kAdamNormBlocks = 2048;         // partial sums per group (enough loads in flight to stream g)
 
 struct AdamGroup {
   void* p[kAdamGroup];

@@ -52,7 +52,7 @@ def test_abi_argument_checks_return_codes():
     assert "null" in _hip.last_error()
     assert lib.ferrite_hip_rmsnorm_bwd(1, 1, 1, None, 1, 1, 1, 4, 8, _hip.F32, _hip.F32, _hip.BF16, 1e-6, None) == 1
     # AdamW: workspace query and argument checks (host arrays are inspected before any launch)
-    assert lib.ferrite_hip_adamw_workspace(75) == (3 * 512 + 4) * 4
+    assert lib.ferrite_hip_adamw_workspace(75) == (3 * 2048 + 4) * 4
     assert lib.ferrite_hip_adamw_workspace(-1) == -1
     args = [None] * 6 + [_hip.BF16, _hip.BF16, 1e-3, 0.9, 0.95, 1e-8, 0.1, 1.0]
     assert lib.ferrite_hip_adamw(1, *args, 1, None, None, 1, None) == 1

@@ -151,6 +151,6 @@ def test_graphed_step_matches_eager(dev, linear):
         assert abs(float(na) - float(nb)) <= 1e-5 * float(na), (i, float(na), float(nb))
         for (name, a), b in zip(named_leaves({"p": pa, "m": sa["m"], "v": sa["v"]}),
                                 leaves({"p": pb, "m": sb["m"], "v": sb["v"]})):
-            d = float((a.float() - b.float()).abs().max())
+            d = float((a.detach().float() - b.detach().float()).abs().max())
             assert d <= 1e-6, (i, name, d)
     assert graphed.graph is not None and sb["step"] == 6
