@@ -333,15 +333,21 @@ struct OperandTile {
 
 // out[M,N] (or, with a K split, the f32 partial slab of K slice blockIdx.x / tiles)
 // = x . y over this slice. XT: x is given transposed, stored [K,M]; YT: y is given
-// transposed, stored [N,K].
-template <typename TO, bool XT, bool YT>
+// transposed, stored [N,K]. BM = 256 or 128 output rows per workgroup (128 only
+// with a k-contiguous x, whose tile is then the first two 64-row subtiles).
+template <typename TO, bool XT, bool YT, int BM = 256, int SLOTS = 2>
 __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict__ x, const bf16* __restrict__ y,
                                                           TO* __restrict__ out, int M, int N, int K, int tiles_m,
                                                           int tiles_n, int kslice) {
   typedef Gemm2 G;
   typedef OperandTile<!XT> XTl;
   typedef OperandTile<YT> YTl;
-  constexpr int kStageBytes = XTl::kBytes + YTl::kBytes;
+  static_assert(BM == 256 || (BM == 128 && !XT), "128-row tiles need a k-contiguous x");
+  static_assert(SLOTS == 2 || (SLOTS == 3 && BM == 128), "three LDS stages fit 128-row tiles only");
+  constexpr int XF = BM / 64;                // x fragments (32 rows each) per wave and k-step
+  constexpr int kDmaX = BM / 64;             // x DMA instructions per wave and stage
+  constexpr int kXBytes = BM == 256 ? XTl::kBytes : 2 * GemmXTile::kSubBytes;
+  constexpr int kStageBytes = kXBytes + YTl::kBytes;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int lane = threadIdx.x & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -359,59 +365,67 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
   const int gsize = min(tiles_m - first_m, kGroup);
   const int tm = first_m + (v % (kGroup * tiles_n)) % gsize;
   const int tn = (v % (kGroup * tiles_n)) / gsize;
-  const int m0 = tm * G::BM, n0 = tn * G::BN;
-  const int wm0 = (wave >> 2) * 128, wn0 = (wave & 3) * 64;
+  const int m0 = tm * BM, n0 = tn * G::BN;
+  const int wm0 = (wave >> 2) * (BM / 2), wn0 = (wave & 3) * 64;
   const int kbeg = slice * kslice;
   const int nk = min(K - kbeg, kslice) / G::BK;
   out += (int64_t)slice * M * N;
 
   // Per-lane DMA offsets; free indices past M or N read as zeros.
-  uint32_t xoff[G::kDma], yoff[G::kDma];
+  uint32_t xoff[kDmaX], yoff[G::kDma];
 #pragma unroll
-  for (int i = 0; i < G::kDma; ++i) {
-    xoff[i] = XTl::dma_off(wave + 8 * i, lane, XT ? M : K, m0, M);
-    yoff[i] = YTl::dma_off(wave + 8 * i, lane, YT ? K : N, n0, N);
-  }
+  for (int i = 0; i < kDmaX; ++i) xoff[i] = XTl::dma_off(wave + 8 * i, lane, XT ? M : K, m0, M);
+#pragma unroll
+  for (int i = 0; i < G::kDma; ++i) yoff[i] = YTl::dma_off(wave + 8 * i, lane, YT ? K : N, n0, N);
   auto issue = [&](int kt) {
-    char* st = smem + (kt & 1) * kStageBytes;
+    char* st = smem + (kt % SLOTS) * kStageBytes;
     const int k0 = kbeg + kt * G::BK;
     const u32x4 rx = buffer_rsrc(XT ? x + (int64_t)k0 * M + m0 : x + (int64_t)m0 * K + k0, 0x7ffffff0u);
     const u32x4 ry = buffer_rsrc(YT ? y + (int64_t)n0 * K + k0 : y + (int64_t)k0 * N + n0, 0x7ffffff0u);
 #pragma unroll
     for (int i = 0; i < G::kDma; ++i) {
-      dma16(rx, st + XTl::block_off(wave + 8 * i), xoff[i]);
-      dma16(ry, st + XTl::kBytes + YTl::block_off(wave + 8 * i), yoff[i]);
+      if (i < kDmaX) dma16(rx, st + XTl::block_off(wave + 8 * i), xoff[i]);
+      dma16(ry, st + kXBytes + YTl::block_off(wave + 8 * i), yoff[i]);
     }
   };
 
-  f32x16 acc[2][4];
+  f32x16 acc[2][XF];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < XF; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
 
   const int xb = XTl::lane_base(lane);
   const int yb = YTl::lane_base(lane);
-  // LDS read instructions per k-step of 16: 2 y fragments (A operand) and 4 x fragments (B).
-  constexpr int kReads = 2 * YTl::kReads + 4 * XTl::kReads;
-  static_assert(kReads <= 16, "at most two reads per product");
+  // LDS read instructions per k-step of 16: 2 y fragments (A operand) and XF x fragments (B),
+  // for NM products.
+  constexpr int NM = 2 * XF;
+  constexpr int kReads = 2 * YTl::kReads + XF * XTl::kReads;
+  static_assert(kReads <= 2 * NM, "at most two reads per product");
 
+  // SLOTS stages in a ring: stage kt + SLOTS - 1 is loaded while stage kt is
+  // multiplied, into the slot that stage kt - 1 left at this step's barrier.
+  constexpr int kDmaWave = kDmaX + G::kDma;  // DMA instructions per wave and stage
   issue(0);
+  if (SLOTS == 3 && nk > 1) issue(1);
   for (int kt = 0; kt < nk; ++kt) {
-    wait_vmem<0>();
+    if (SLOTS == 3 && kt + 1 < nk)
+      wait_vmem<kDmaWave>();  // stage kt has landed; stage kt + 1 may be in flight
+    else
+      wait_vmem<0>();
     lds_barrier();
-    if (kt + 1 < nk) issue(kt + 1);
-    const char* xs = smem + (kt & 1) * kStageBytes + xb;
-    const char* ys = smem + (kt & 1) * kStageBytes + XTl::kBytes + yb;
-    // 4 k-steps x (2 y fragments, 4 x fragments, 8 products); the next
-    // k-step's six fragments are read while this one's products run.
-    bf16x8 fa[2][2], fb[2][4];
+    if (kt + SLOTS - 1 < nk) issue(kt + SLOTS - 1);
+    const char* xs = smem + (kt % SLOTS) * kStageBytes + xb;
+    const char* ys = smem + (kt % SLOTS) * kStageBytes + kXBytes + yb;
+    // 4 k-steps x (2 y fragments, XF x fragments, NM products); the next
+    // k-step's fragments are read while this one's products run.
+    bf16x8 fa[2][2], fb[2][XF];
 #pragma unroll
     for (int j = 0; j < 2; ++j) fa[0][j] = YTl::read(ys, 0, wn0 + 32 * j);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fb[0][i] = XTl::read(xs, 0, wm0 + 32 * i);
+    for (int i = 0; i < XF; ++i) fb[0][i] = XTl::read(xs, 0, wm0 + 32 * i);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int c = kk & 1;
@@ -419,30 +433,30 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
 #pragma unroll
         for (int j = 0; j < 2; ++j) fa[c ^ 1][j] = YTl::read(ys, kk + 1, wn0 + 32 * j);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fb[c ^ 1][i] = XTl::read(xs, kk + 1, wm0 + 32 * i);
+        for (int i = 0; i < XF; ++i) fb[c ^ 1][i] = XTl::read(xs, kk + 1, wm0 + 32 * i);
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mma32(fa[c][j], fb[c][i], acc[j][i]);
+        for (int i = 0; i < XF; ++i) mma32(fa[c][j], fb[c][i], acc[j][i]);
     }
     // First fragments, then per k-step: the next step's reads spread over this
-    // step's eight MFMAs, then the last step's products.
+    // step's NM MFMAs, then the last step's products.
     __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       if (kk + 1 < 4) {
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
+        for (int r = 0; r < NM; ++r) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          const int nr = kReads / 8 + (r < kReads % 8 ? 1 : 0);  // 0..2 (kReads <= 12)
+          const int nr = kReads / NM + (r < kReads % NM ? 1 : 0);  // 0..2
           if (nr == 2)
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
           else if (nr == 1)
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
       } else {
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
       }
     }
   }
@@ -452,7 +466,7 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < XF; ++i) {
       const int m = m0 + wm0 + 32 * i + l32;
       if (m >= M) continue;
 #pragma unroll
@@ -512,10 +526,39 @@ int64_t splitk_workspace(int64_t M, int64_t N, int64_t K) {
   return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
 }
 
+// Output rows per workgroup. 128-row tiles (k-contiguous x only) halve the work of a
+// tile, so a problem whose 256-row tiles spill into a mostly empty round, or fill
+// less than half the CUs, runs in fewer or shorter rounds: 8192 x 2304 takes 288
+// 256-row tiles (two rounds on 256 CUs) but 576 128-row ones (three rounds of half
+// the work), and 8192 x 768 one round of 192 tiles instead of 96 tiles or a K split.
+// A 128-row tile moves more bytes per product, costed at 0.55 of a 256-row one.
+// With fewer than a quarter of the CUs' worth of 256-row tiles the K split is used.
+int pick_bm(int64_t M, int64_t N, bool xt) {
+  if (xt) return 256;
+  const int64_t cus = cu_count();
+  const int64_t t256 = cdiv(M, (int64_t)256) * cdiv(N, (int64_t)Gemm2::BN);
+  const int64_t t128 = cdiv(M, (int64_t)128) * cdiv(N, (int64_t)Gemm2::BN);
+  if (t256 < cus / 4) return 256;
+  return 11 * cdiv(t128, cus) < 20 * cdiv(t256, cus) ? 128 : 256;
+}
+
 template <typename TO, bool XT, bool YT>
 int launch_gemm_dma_t(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, void* ws,
                       int64_t ws_bytes, hipStream_t stream) {
   typedef Gemm2 G;
+  if constexpr (!XT) {
+    if (pick_bm(M, N, XT) == 128) {
+      constexpr int kLds128 = 3 * (2 * GemmXTile::kSubBytes + OperandTile<YT>::kBytes);
+      static_assert(kLds128 <= 160 * 1024, "three stages of a 128-row tile fit the LDS");
+      const int64_t tiles_m = cdiv(M, (int64_t)128), tiles_n = cdiv(N, G::BN);
+      auto kern = gemm_dma_kernel<TO, false, YT, 128, 3>;
+      (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds128);
+      hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n)), dim3(G::kThreads), kLds128, stream,
+                         static_cast<const bf16*>(x), static_cast<const bf16*>(y), static_cast<TO*>(out), (int)M,
+                         (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)K);
+      return check_launch("ferrite_matmul");
+    }
+  }
   const int64_t tiles_m = cdiv(M, G::BM), tiles_n = cdiv(N, G::BN);
   int slices = splitk_slices(M, N, K);
   if (slices > 1 && (ws == nullptr || ws_bytes < splitk_workspace(M, N, K) || (M * N) % 4 != 0 ||
@@ -560,7 +603,7 @@ bool dma_ok(const void* x, const void* y, const void* out, int64_t m, int64_t n,
   auto fits = [](int64_t bytes) { return bytes < 0x7ffffff0; };
   return k % Gemm2::BK == 0 && n % 8 == 0 && (!xt || m % 8 == 0) && a16(x) && a16(y) && a16(out) &&
          m <= 0x7fffffff && n <= 0x7fffffff && k <= 0x7fffffff && fits(xt ? 64 * m * 2 : 256 * k * 2) &&
-         fits(yt ? 256 * k * 2 : 64 * n * 2) && cdiv(m, (int64_t)Gemm2::BM) * cdiv(n, (int64_t)Gemm2::BN) * 16 <= 0x7fffffff;
+         fits(yt ? 256 * k * 2 : 64 * n * 2) && cdiv(m, (int64_t)128) * cdiv(n, (int64_t)Gemm2::BN) * 16 <= 0x7fffffff;
 }
 
 }  // namespace

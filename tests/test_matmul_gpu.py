@@ -169,8 +169,10 @@ def _mm_ex(xs, ys, m, n, k, x_t, y_t, out_dtype, workspace=True):
     (768, 768, 4096),    # 9 tiles, K split 8 ways (512 deep)
     (520, 264, 1024),    # ragged tile edges, K split
     (1024, 2304, 768),   # 36 tiles but K too short to split
-    (8192, 768, 3072),   # 96 tiles, long K: split 2 ways
-    (8192, 768, 512),    # enough tiles: no split
+    (8192, 768, 3072),   # 96 tiles: 128-row tiles (k-contiguous x), else long K split 2 ways
+    (8192, 768, 512),    # 128-row tiles (k-contiguous x), else no split
+    (8192, 2304, 768),   # 288 256-row tiles: 576 128-row ones with a k-contiguous x
+    (2000, 2056, 320),   # 128-row tiles with ragged row and column edges
 ])
 @pytest.mark.parametrize("x_t,y_t", [(False, False), (True, False), (False, True), (True, True)])
 def test_transposed_operands_and_k_split(dev, m, n, k, x_t, y_t):
