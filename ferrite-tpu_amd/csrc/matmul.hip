@@ -377,16 +377,25 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
   for (int i = 0; i < kDmaX; ++i) xoff[i] = XTl::dma_off(wave + 8 * i, lane, XT ? M : K, m0, M);
 #pragma unroll
   for (int i = 0; i < G::kDma; ++i) yoff[i] = YTl::dma_off(wave + 8 * i, lane, YT ? K : N, n0, N);
-  auto issue = [&](int kt) {
+  // DMA instruction q (x instructions first, then y) of stage kt. A stage past
+  // the slice gets an empty buffer range: its instructions read nothing and
+  // write zeros into a slot that no later stage reads.
+  auto issue_one = [&](int kt, int q) {
     char* st = smem + (kt % SLOTS) * kStageBytes;
     const int k0 = kbeg + kt * G::BK;
-    const u32x4 rx = buffer_rsrc(XT ? x + (int64_t)k0 * M + m0 : x + (int64_t)m0 * K + k0, 0x7ffffff0u);
-    const u32x4 ry = buffer_rsrc(YT ? y + (int64_t)n0 * K + k0 : y + (int64_t)k0 * N + n0, 0x7ffffff0u);
-#pragma unroll
-    for (int i = 0; i < G::kDma; ++i) {
-      if (i < kDmaX) dma16(rx, st + XTl::block_off(wave + 8 * i), xoff[i]);
-      dma16(ry, st + kXBytes + YTl::block_off(wave + 8 * i), yoff[i]);
+    const uint32_t range = kt < nk ? 0x7ffffff0u : 0u;
+    if (q < kDmaX) {
+      const u32x4 rx = buffer_rsrc(XT ? x + (int64_t)k0 * M + m0 : x + (int64_t)m0 * K + k0, range);
+      dma16(rx, st + XTl::block_off(wave + 8 * q), xoff[q]);
+    } else {
+      const u32x4 ry = buffer_rsrc(YT ? y + (int64_t)n0 * K + k0 : y + (int64_t)k0 * N + n0, range);
+      dma16(ry, st + kXBytes + YTl::block_off(wave + 8 * (q - kDmaX)), yoff[q - kDmaX]);
     }
+  };
+  constexpr int kDmaWave = kDmaX + G::kDma;  // DMA instructions per wave and stage
+  auto issue = [&](int kt) {
+#pragma unroll
+    for (int q = 0; q < kDmaWave; ++q) issue_one(kt, q);
   };
 
   f32x16 acc[2][XF];
@@ -399,15 +408,23 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
 
   const int xb = XTl::lane_base(lane);
   const int yb = YTl::lane_base(lane);
-  // LDS read instructions per k-step of 16: 2 y fragments (A operand) and XF x fragments (B),
-  // for NM products.
+  // Per k-step of 16: NM products over 2 y fragments (A operand) and XF x
+  // fragments (B).
   constexpr int NM = 2 * XF;
-  constexpr int kReads = 2 * YTl::kReads + XF * XTl::kReads;
-  static_assert(kReads <= 2 * NM, "at most two reads per product");
+  constexpr int NFR = 2 + XF;
+  static_assert(NFR <= NM, "one fragment read per product slot at most");
+  constexpr int NSLOT = 4 * NM;  // product slots per 64-deep stage
 
   // SLOTS stages in a ring: stage kt + SLOTS - 1 is loaded while stage kt is
   // multiplied, into the slot that stage kt - 1 left at this step's barrier.
-  constexpr int kDmaWave = kDmaX + G::kDma;  // DMA instructions per wave and stage
+  // The program order is the schedule: product slot i holds one MFMA, at most
+  // one fragment read for the next k-step and at most one DMA instruction, and
+  // a scheduling fence closes it. The DMA instructions go out one at a time
+  // between products (issued together after the barrier, the eight waves
+  // queue in the CU's address path and stall their products): over the first
+  // half of the stage with two slots, so the last lands before the next
+  // barrier, and over the whole stage with three.
+  constexpr int kDmaSpan = SLOTS == 3 ? NSLOT : NSLOT / 2;
   issue(0);
   if (SLOTS == 3 && nk > 1) issue(1);
   for (int kt = 0; kt < nk; ++kt) {
@@ -416,50 +433,35 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
     else
       wait_vmem<0>();
     lds_barrier();
-    if (kt + SLOTS - 1 < nk) issue(kt + SLOTS - 1);
+    const int kload = kt + SLOTS - 1;
     const char* xs = smem + (kt % SLOTS) * kStageBytes + xb;
     const char* ys = smem + (kt % SLOTS) * kStageBytes + kXBytes + yb;
-    // 4 k-steps x (2 y fragments, XF x fragments, NM products); the next
-    // k-step's fragments are read while this one's products run.
     bf16x8 fa[2][2], fb[2][XF];
+    // Fragment f of k-step kk in the order of first use by the products
+    // (j, i) = (r / XF, r % XF): y 0, x 0 .. XF - 1, y 1.
+    auto read = [&](int kk, int f) {
+      if (f == 0)
+        fa[kk & 1][0] = YTl::read(ys, kk, wn0);
+      else if (f <= XF)
+        fb[kk & 1][f - 1] = XTl::read(xs, kk, wm0 + 32 * (f - 1));
+      else
+        fa[kk & 1][1] = YTl::read(ys, kk, wn0 + 32);
+    };
 #pragma unroll
-    for (int j = 0; j < 2; ++j) fa[0][j] = YTl::read(ys, 0, wn0 + 32 * j);
+    for (int f = 0; f < NFR; ++f) read(0, f);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < XF; ++i) fb[0][i] = XTl::read(xs, 0, wm0 + 32 * i);
+    for (int i = 0; i < NSLOT; ++i) {
+      const int kk = i / NM, r = i % NM, c = kk & 1;
+      if (kk + 1 < 4 && r < NFR) read(kk + 1, r);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int c = kk & 1;
-      if (kk + 1 < 4) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) fa[c ^ 1][j] = YTl::read(ys, kk + 1, wn0 + 32 * j);
-#pragma unroll
-        for (int i = 0; i < XF; ++i) fb[c ^ 1][i] = XTl::read(xs, kk + 1, wm0 + 32 * i);
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < XF; ++i) mma32(fa[c][j], fb[c][i], acc[j][i]);
-    }
-    // First fragments, then per k-step: the next step's reads spread over this
-    // step's NM MFMAs, then the last step's products.
-    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      if (kk + 1 < 4) {
-#pragma unroll
-        for (int r = 0; r < NM; ++r) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          const int nr = kReads / NM + (r < kReads % NM ? 1 : 0);  // 0..2
-          if (nr == 2)
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-          else if (nr == 1)
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-      } else {
-        __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
-      }
+      for (int q = 0; q < kDmaWave; ++q)
+        if (i == (2 * q + 1) * kDmaSpan / (2 * kDmaWave)) issue_one(kload, q);
+      mma32(fa[c][r / XF], fb[c][r % XF], acc[r / XF][r % XF]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
+  wait_vmem<0>();  // the empty loads past the slice have landed too
 
   // Epilogue: acc[j][i] is a C^T tile; register r of lane (l32, g) is
   // C[m0 + wm0 + 32 i + l32][n0 + wn0 + 32 j + (r / 4) * 8 + g * 4 + r % 4].
