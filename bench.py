@@ -125,7 +125,15 @@ def bench_attention(b, h, t, d, steps, warmup, seed=7):
     def dqk():
         _hip.check(lib.ferrite_hip_attn_bwd_dq(qp, kp, vp, dop, lp, dp, dqp, b, h, t, t, d, bf, 1, scale, st), "dq")
 
-    def bwd():
+    def dq_delta():
+        _hip.check(lib.ferrite_hip_attn_bwd_dq_delta(qp, kp, vp, op, dop, lp, dp, dqp, b, h, t, t, d, bf, 1, scale, st),
+                   "dq_delta")
+
+    def bwd():  # the backward flash_attention runs: dQ computing delta, then dK/dV reading it
+        dq_delta()
+        dkv()
+
+    def bwd_split():  # the reference's order: delta pass, dK/dV, dQ
         dlt()
         dkv()
         dqk()
@@ -135,13 +143,16 @@ def bench_attention(b, h, t, d, steps, warmup, seed=7):
     t_delta = _events_time(dlt, steps, warmup)
     t_dkv = _events_time(dkv, steps, warmup)
     t_dq = _events_time(dqk, steps, warmup)
+    t_dq_delta = _events_time(dq_delta, steps, warmup)
+    t_bwd_split = _events_time(bwd_split, steps, warmup)
     t_bwd = _events_time(bwd, steps, warmup)
     f_fwd = attention_flops(b, h, t, t, d, causal=True)
     f_bwd = attention_flops(b, h, t, t, d, causal=True, backward=True)
     return {
         "shape": [b, h, t, d],
         "fwd_us": t_fwd * 1e6, "fwd_tflops": f_fwd / t_fwd / 1e12,
-        "delta_us": t_delta * 1e6, "dkv_us": t_dkv * 1e6, "dq_us": t_dq * 1e6,
+        "delta_us": t_delta * 1e6, "dkv_us": t_dkv * 1e6, "dq_us": t_dq * 1e6, "dq_with_delta_us": t_dq_delta * 1e6,
+        "bwd_split_us": t_bwd_split * 1e6,
         "bwd_us": t_bwd * 1e6, "bwd_tflops": f_bwd / t_bwd / 1e12,
         "fwd_bwd_tflops": (f_fwd + f_bwd) / (t_fwd + t_bwd) / 1e12,
         "fwd_frac_bf16_peak": f_fwd / t_fwd / 1e12 / PEAK_BF16_TFLOPS,

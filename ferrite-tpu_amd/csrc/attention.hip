@@ -1864,15 +1864,18 @@ struct DqPp {
 // V tiles, dS^T = P^T (dP^T - delta) on the VALU (one query per lane, so lse
 // and delta are per-lane scalars), then dQ^T += K^T dS^T from transposed
 // reads of the K tile.
-template <int D, int W, int SLOTS, bool ZIG>
+// FUSED: delta is not read but computed here from O and dO (the rows' dO
+// fragments are loaded anyway) and written out for the dK/dV kernel, which
+// then runs after this one: the separate delta pass over O and dO goes away.
+template <int D, int W, int SLOTS, bool ZIG, bool FUSED = false>
 __global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                                 const bf16* __restrict__ v,
                                                                 const bf16* __restrict__ dout,
                                                                 const float* __restrict__ lse,
-                                                                const float* __restrict__ delta,
+                                                                float* __restrict__ delta,
                                                                 bf16* __restrict__ dq, int bh_count, int Sq, int Sk,
                                                                 int d, int causal, float scale, float scale_log2,
-                                                                int n_qtiles) {
+                                                                int n_qtiles, const bf16* __restrict__ o) {
   typedef DqPp<D, W, SLOTS> F;
   typedef typename F::Tile Tile;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -1913,7 +1916,22 @@ __global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __r
   load_row_frags<bf16, D, true, false>(dof, dob, q0w, Sq, d);
   const bool qok = qrow < Sq;
   const float nlse2 = qok ? -lse[(int64_t)bh * Sq + qrow] * kLog2e : 0.f;
-  const float dl = qok ? delta[(int64_t)bh * Sq + qrow] : 0.f;
+  float dl;
+  if constexpr (FUSED) {
+    // delta = sum_d f32(dO) f32(O) (flash_attention.py:328-329): this lane
+    // holds half of its row's elements, lane ^ 32 the other half.
+    bf16x8 of[F::KS];
+    load_row_frags<bf16, D, true, false>(of, o + (int64_t)bh * Sq * d, q0w, Sq, d);
+    float part = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < F::KS; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part = __builtin_fmaf((float)dof[kk][e], (float)of[kk][e], part);
+    dl = lane32_sum(part);
+    if (qok && g == 0) delta[(int64_t)bh * Sq + qrow] = dl;
+  } else {
+    dl = qok ? delta[(int64_t)bh * Sq + qrow] : 0.f;
+  }
 
   // Tiles 0 .. SLOTS - 2 go out first; tile t + SLOTS - 1 is issued after
   // tile t's barrier, into the slot tile t - 1 left.
@@ -2146,35 +2164,36 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
   return check_launch("ferrite_flash_attention_fwd");
 }
 
+// o == nullptr: read delta; otherwise compute it from o and dout and write it.
 template <int D, int W, int SLOTS, bool ZIG>
-int dq_pp_launch_t(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
-                   void* dq, const Shape& s, int causal, float scale, hipStream_t stream) {
+int dq_pp_launch_t(const void* q, const void* k, const void* v, const void* dout, const float* lse, float* delta,
+                   void* dq, const Shape& s, int causal, float scale, hipStream_t stream, const void* o) {
   typedef DqPp<D, W, SLOTS> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq: grid too large");
-  auto kern = attn_dq_pp_kernel<D, W, SLOTS, ZIG>;
+  auto kern = o ? attn_dq_pp_kernel<D, W, SLOTS, ZIG, true> : attn_dq_pp_kernel<D, W, SLOTS, ZIG, false>;
   set_lds(kern, F::kLds);
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
                      delta, static_cast<bf16*>(dq), (int)bh, (int)s.sq, (int)s.sk, (int)s.d, causal, scale,
-                     scale * kLog2e, (int)nq);
+                     scale * kLog2e, (int)nq, static_cast<const bf16*>(o));
   return check_launch("ferrite_flash_attention_bwd_dq");
 }
 
 template <int D>
-int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
-                 void* dq, const Shape& s, int causal, float scale, hipStream_t stream) {
+int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, float* delta,
+                 void* dq, const Shape& s, int causal, float scale, hipStream_t stream, const void* o = nullptr) {
   if constexpr (D == 64) {
     // 128-query workgroups of 4 waves with two LDS slots (67 KB): two share a
     // CU. A grid resident all at once (the long-context case) pairs long and
     // short causal sweeps on each CU.
     typedef DqPp<64, 4, 2> F4;
     const bool one_round = causal && cdiv(s.sq, F4::BQ) * s.b * s.h <= 2 * (int64_t)cu_count();
-    return one_round ? dq_pp_launch_t<D, 4, 2, true>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream)
-                     : dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream);
+    return one_round ? dq_pp_launch_t<D, 4, 2, true>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o)
+                     : dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o);
   } else {
-    return dq_pp_launch_t<D, 8, 3, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream);
+    return dq_pp_launch_t<D, 8, 3, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o);
   }
 }
 
@@ -2182,7 +2201,7 @@ template <typename T, int D, bool AL>
 int dq_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
               void* dq, const Shape& s, int causal, float scale, hipStream_t stream) {
   if constexpr (sizeof(T) == 2 && AL && D <= 128)
-    return dq_pp_launch<D>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream);
+    return dq_pp_launch<D>(q, k, v, dout, lse, const_cast<float*>(delta), dq, s, causal, scale, stream);
   typedef Dq<T, D, AL> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
@@ -2306,6 +2325,27 @@ extern "C" int ferrite_hip_attn_bwd_dkv(const void* q, const void* k, const void
   return fail(FERRITE_ERR_INVALID_ARGUMENT, "unreachable head_dim")
   FERRITE_DISPATCH(dkv_launch, s, dtype, al, q, k, v, dout, lse, delta, dk, dv, s, causal, scale, st);
 #undef FERRITE_DISPATCH_256
+}
+
+extern "C" int ferrite_hip_attn_bwd_dq_delta(const void* q, const void* k, const void* v, const void* o,
+                                             const void* dout, const float* lse, float* delta, void* dq, int64_t b,
+                                             int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype, int causal,
+                                             float scale, void* stream) {
+  const Shape s{b, h, sq, sk, d};
+  if (int rc = check_shape("ferrite_hip_attn_bwd_dq_delta", s, dtype, causal, true)) return rc;
+  if (!q || !k || !v || !o || !dout || !lse || !delta || !dq)
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq_delta: null pointer");
+  const bool al = d % (dtype == FERRITE_BF16 ? 8 : 4) == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
+                  aligned16(o) && aligned16(dout) && aligned16(dq);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int dp = pad_dim(d);
+  if (dtype == FERRITE_BF16 && al && dp <= 128) {
+    if (dp == 64) return dq_pp_launch<64>(q, k, v, dout, lse, delta, dq, s, causal, scale, st, o);
+    return dq_pp_launch<128>(q, k, v, dout, lse, delta, dq, s, causal, scale, st, o);
+  }
+  // Other dtypes and head dims: the delta kernel, then dQ reading it.
+  if (int rc = ferrite_hip_attn_bwd_delta(o, dout, delta, b, h, sq, d, dtype, stream)) return rc;
+  return ferrite_hip_attn_bwd_dq(q, k, v, dout, lse, delta, dq, b, h, sq, sk, d, dtype, causal, scale, stream);
 }
 
 extern "C" int ferrite_hip_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout,

@@ -87,6 +87,33 @@ def _flash_delta(out, do):
     return delta
 
 
+def _flash_backward_fused(q, k, v, out, do, lse, *, causal: bool, scale: float):
+    """dQ, dK, dV with delta (flash_attention.py:328-329) computed inside the dQ kernel from O
+    and dO and handed to dK/dV, which therefore runs second: no separate delta pass."""
+    _hip.require_gpu(q, k, v, out, do, lse)
+    q, k, v, out, do, lse = (t.contiguous() for t in (q, k, v, out, do, lse))
+    b, h, sq, d = q.shape
+    sk = k.shape[2]
+    dt = _hip.dtype_code(q.dtype)
+    stream = _hip.stream_of(q)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    delta = torch.empty((b, h, sq), dtype=torch.float32, device=q.device)
+    lib = _hip.lib()
+    rc = lib.ferrite_hip_attn_bwd_dq_delta(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), do.data_ptr(), lse.data_ptr(), delta.data_ptr(),
+        dq.data_ptr(), b, h, sq, sk, d, dt, int(causal), float(scale), stream,
+    )
+    _hip.check(rc, "ferrite_flash_attention_bwd_dq")
+    rc = lib.ferrite_hip_attn_bwd_dkv(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(), delta.data_ptr(),
+        dk.data_ptr(), dv.data_ptr(), b, h, sq, sk, d, dt, int(causal), float(scale), stream,
+    )
+    _hip.check(rc, "ferrite_flash_attention_bwd_dkv")
+    return dq, dk, dv
+
+
 def _flash_backward(q, k, v, do, lse, delta, *, causal: bool, scale: float, bs: BlockSizes | None = None):
     """dQ, dK, dV. Reference: _flash_backward, flash_attention.py:246-307 (two kernels, no atomics)."""
     _hip.require_gpu(q, k, v, do, lse, delta)
@@ -134,8 +161,7 @@ class _Flash(torch.autograd.Function):
     def backward(ctx, do):
         q, k, v, out, lse = ctx.saved_tensors
         do = do.to(out.dtype).contiguous()
-        delta = _flash_delta(out, do)
-        dq, dk, dv = _flash_backward(q, k, v, do, lse, delta, causal=ctx.causal, scale=ctx.scale, bs=ctx.bs)
+        dq, dk, dv = _flash_backward_fused(q, k, v, out, do, lse, causal=ctx.causal, scale=ctx.scale)
         return dq, dk, dv, None, None, None
 
 

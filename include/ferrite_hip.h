@@ -20,6 +20,8 @@
  *                                                          an XLA fusion in the reference)
  *   ferrite_hip_attn_bwd_dkv  flash_attention.py:197-221, :253-279 ("ferrite_flash_attention_bwd_dkv")
  *   ferrite_hip_attn_bwd_dq   flash_attention.py:224-243, :281-306 ("ferrite_flash_attention_bwd_dq")
+ *   ferrite_hip_attn_bwd_dq_delta  the same dQ with delta (flash_attention.py:328-329)
+ *                                  computed inside it and written out for dK/dV
  *   ferrite_hip_add_rmsnorm   rmsnorm.py:52-56, :77-110  ("ferrite_add_rmsnorm")
  *   ferrite_hip_rmsnorm       rmsnorm.py:46-49, :77-110  ("ferrite_rmsnorm")
  *   ferrite_hip_rmsnorm_bwd   rmsnorm.py:159-166, :128-131, :148-153 (the custom_vjp backward of
@@ -213,6 +215,18 @@ int ferrite_hip_attn_bwd_dkv(const void* q, const void* k, const void* v, const 
 int ferrite_hip_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout, const float* lse,
                             const float* delta, void* dq, int64_t b, int64_t h, int64_t sq, int64_t sk, int64_t d,
                             int dtype, int causal, float scale, void* stream);
+
+/*
+ * dQ of flash attention that also produces delta (flash_attention.py:224-243 with
+ * :328-329 folded in): delta[B, H, Sq] = sum_d f32(dO) * f32(O) is computed from o
+ * inside the dQ kernel, used there and written to `delta` (an output here), so the
+ * dK/dV call that reads it comes after this one and no separate delta pass runs.
+ * bf16 with head dims up to 128 run the fused kernel; other inputs run
+ * ferrite_hip_attn_bwd_delta and then ferrite_hip_attn_bwd_dq, with the same result.
+ */
+int ferrite_hip_attn_bwd_dq_delta(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                                  const float* lse, float* delta, void* dq, int64_t b, int64_t h, int64_t sq,
+                                  int64_t sk, int64_t d, int dtype, int causal, float scale, void* stream);
 
 #ifdef __cplusplus
 }

@@ -131,12 +131,14 @@ def test_gpt_attention_shape(dev):
     _abi_case(dev, 8, 12, 1024, 1024, 64, "bf16", True, seed=41, scale=0.125)
 
 
-def _abi_case(dev, b, h, sq, sk, d, dtype, causal, seed, scale):
+def _abi_case(dev, b, h, sq, sk, d, dtype, causal, seed, scale, fused=False):
     """Ragged lengths and odd head dims through the C ABI (the Python API requires
     block-multiple lengths, like the reference). bf16 gradients are held to 2e-2 or
     to 1.5x the error of the reference's own bf16 recipe (P and dS rounded to bf16
     before the products, oracle.attention.flash_backward), whichever is larger: at
-    a large scale the gradients reach ~10 and the recipe itself is ~4e-2 off."""
+    a large scale the gradients reach ~10 and the recipe itself is ~4e-2 off.
+    fused: dQ through ferrite_hip_attn_bwd_dq_delta, which computes delta itself;
+    that delta must match the delta kernel's to f32 rounding, and dK/dV read it."""
     q, k, v = _qkv(seed, (b, h, sq, d), dtype, kv_len=sk)
     do = normal(seed + 3, q.shape, dtype)
     qt, kt, vt, dot = (to_dev(a, dtype, dev) for a in (q, k, v, do))
@@ -145,16 +147,27 @@ def _abi_case(dev, b, h, sq, sk, d, dtype, causal, seed, scale):
     lib, st, dt = _hip.lib(), _hip.stream_of(qt), _hip.dtype_code(qt.dtype)
     _hip.check(lib.ferrite_hip_attn_fwd(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), o.data_ptr(), lse.data_ptr(),
                                         b, h, sq, sk, d, dt, int(causal), scale, st), "fwd")
-    delta = _flash_delta(o, dot)
     dq = torch.full_like(qt, float("nan"))
     dk = torch.full_like(kt, float("nan"))
     dv = torch.full_like(vt, float("nan"))
+    if fused:
+        delta = torch.full((b, h, sq), float("nan"), device=dev)
+        _hip.check(lib.ferrite_hip_attn_bwd_dq_delta(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), o.data_ptr(),
+                                                     dot.data_ptr(), lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
+                                                     b, h, sq, sk, d, dt, int(causal), scale, st), "dq_delta")
+        want = _flash_delta(o, dot)
+        torch.cuda.synchronize()
+        mag = (to_np(o).astype(np.float64) * to_np(dot).astype(np.float64)).__abs__().sum(-1)
+        assert np.all(np.abs(to_np(delta).astype(np.float64) - to_np(want)) <= 1e-6 * mag + 1e-30)
+    else:
+        delta = _flash_delta(o, dot)
     _hip.check(lib.ferrite_hip_attn_bwd_dkv(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), dot.data_ptr(), lse.data_ptr(),
                                             delta.data_ptr(), dk.data_ptr(), dv.data_ptr(), b, h, sq, sk, d, dt,
                                             int(causal), scale, st), "dkv")
-    _hip.check(lib.ferrite_hip_attn_bwd_dq(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), dot.data_ptr(), lse.data_ptr(),
-                                           delta.data_ptr(), dq.data_ptr(), b, h, sq, sk, d, dt, int(causal), scale,
-                                           st), "dq")
+    if not fused:
+        _hip.check(lib.ferrite_hip_attn_bwd_dq(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), dot.data_ptr(),
+                                               lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), b, h, sq, sk, d, dt,
+                                               int(causal), scale, st), "dq")
     torch.cuda.synchronize()
     o_ref, lse_ref = oatt.forward(q, k, v, causal=causal, scale=scale)
     grads_ref = oatt.backward(q, k, v, do, causal=causal, scale=scale)
@@ -183,9 +196,10 @@ def _abi_case(dev, b, h, sq, sk, d, dtype, causal, seed, scale):
     (1, 1, 1, 1, 64, "bf16", True),         # single token
 ])
 @pytest.mark.parametrize("scale", ["default", 0.37])
-def test_ragged_and_unaligned_via_abi(dev, b, h, sq, sk, d, dtype, causal, scale):
+@pytest.mark.parametrize("fused", [False, True], ids=["delta_pass", "delta_in_dq"])
+def test_ragged_and_unaligned_via_abi(dev, b, h, sq, sk, d, dtype, causal, scale, fused):
     scale = 1.0 / np.sqrt(d) if scale == "default" else scale
-    _abi_case(dev, b, h, sq, sk, d, dtype, causal, seed=31, scale=scale)
+    _abi_case(dev, b, h, sq, sk, d, dtype, causal, seed=31, scale=scale, fused=fused)
 
 
 @pytest.mark.parametrize("b,h,s,d", [
@@ -195,9 +209,10 @@ def test_ragged_and_unaligned_via_abi(dev, b, h, sq, sk, d, dtype, causal, scale
     (1, 1, 128, 64),
     (1, 2, 128, 80),    # d padded 80 -> 128 on the 64-row-tile path
 ])
-def test_causal_tile_edges_via_abi(dev, b, h, s, d):
+@pytest.mark.parametrize("fused", [False, True], ids=["delta_pass", "delta_in_dq"])
+def test_causal_tile_edges_via_abi(dev, b, h, s, d, fused):
     """Causal bf16 lengths that are multiples of 64 but not of the 256-row query tile."""
-    _abi_case(dev, b, h, s, s, d, "bf16", True, seed=37, scale=1.0 / np.sqrt(d))
+    _abi_case(dev, b, h, s, s, d, "bf16", True, seed=37, scale=1.0 / np.sqrt(d), fused=fused)
 
 
 @pytest.mark.parametrize("d", [64, 128])
