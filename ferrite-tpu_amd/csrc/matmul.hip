@@ -245,6 +245,66 @@ int launch_gemm(const void* x, const void* y, void* out, int64_t M, int64_t N, i
 }
 
 // ===========================================================================
+// GELU epilogues (the MLP of model/gpt.py:141: jax.nn.gelu(approximate=True))
+// ===========================================================================
+// gelu(u) = u/2 (1 + tanh(z)), z = b (u + c u^3), b = sqrt(2/pi), c = 0.044715,
+// written as u s with s = (1 + tanh z)/2 = 1 / (1 + 2^(-2 z log2 e)): one exp2
+// and one reciprocal instead of a libm tanh (the epilogue runs once per output
+// element, after the products, with nothing to hide it behind), and no
+// cancellation in 1 + tanh z at negative u. gelu'(u) = s + 2 u s (1 - s) b (1 + 3 c u^2).
+// Both in f32 from the bf16-rounded u, as an elementwise pass over the rounded
+// product computes them.
+constexpr int kEpiNone = 0, kEpiGelu = 1, kEpiGeluGrad = 2;
+constexpr float kGeluB = 0.7978845608028654f, kGeluC = 0.044715f;
+constexpr float kGeluE = -2.0f * kGeluB * 1.4426950408889634f;  // -2 b log2(e)
+
+__device__ __forceinline__ float gelu_gate(float u) {  // s = (1 + tanh z) / 2
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(kGeluE * (u + kGeluC * u * u * u)));
+}
+__device__ __forceinline__ float gelu_tanh(float u) { return u * gelu_gate(u); }
+__device__ __forceinline__ float gelu_tanh_grad(float u) {
+  const float s = gelu_gate(u);
+  return s + 2.f * u * s * (1.f - s) * kGeluB * (1.f + 3.f * kGeluC * u * u);
+}
+
+// Four consecutive outputs v = bf16(x . y) of one row. kEpiGelu: aux <- v (the
+// pre-activation), out <- bf16(gelu(v)). kEpiGeluGrad: u is the pre-activation
+// (read from aux); out <- bf16(v * gelu'(u)) (v is the incoming gradient).
+__device__ __forceinline__ void gelu_store(const bf16x4& v, bf16* out, bf16* aux) {
+  *reinterpret_cast<bf16x4*>(aux) = v;
+  bf16x4 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = (bf16)gelu_tanh((float)v[e]);
+  *reinterpret_cast<bf16x4*>(out) = r;
+}
+__device__ __forceinline__ void gelu_grad_store(const bf16x4& v, const bf16x4& u, bf16* out) {
+  bf16x4 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = (bf16)((float)v[e] * gelu_tanh_grad((float)u[e]));
+  *reinterpret_cast<bf16x4*>(out) = r;
+}
+template <int EPI>
+__device__ __forceinline__ void gelu_epilogue(const bf16x4& v, bf16* out, bf16* aux) {
+  if constexpr (EPI == kEpiGelu)
+    gelu_store(v, out, aux);
+  else
+    gelu_grad_store(v, *reinterpret_cast<const bf16x4*>(aux), out);
+}
+
+// The same epilogue as a pass of its own, for products the DMA kernel does not
+// take: kEpiGelu reads the pre-activation from aux, kEpiGeluGrad the gradient
+// from out (both written there by the plain product).
+template <int EPI>
+__global__ __launch_bounds__(256) void gelu_pass_kernel(bf16* __restrict__ out, bf16* __restrict__ aux, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  if constexpr (EPI == kEpiGelu)
+    out[i] = (bf16)gelu_tanh((float)aux[i]);
+  else
+    out[i] = (bf16)((float)out[i] * gelu_tanh_grad((float)aux[i]));
+}
+
+// ===========================================================================
 // bf16 GEMM on DMA-fed LDS tiles (K % 64 == 0, N % 8 == 0, 16-byte aligned)
 // ===========================================================================
 // 256 x 256 output tile per workgroup of 8 waves, 64 k per step through two
@@ -335,15 +395,16 @@ struct OperandTile {
 // = x . y over this slice. XT: x is given transposed, stored [K,M]; YT: y is given
 // transposed, stored [N,K]. BM = 256 or 128 output rows per workgroup (128 only
 // with a k-contiguous x, whose tile is then the first two 64-row subtiles).
-template <typename TO, bool XT, bool YT, int BM = 256, int SLOTS = 2>
+template <typename TO, bool XT, bool YT, int BM = 256, int SLOTS = 2, int EPI = kEpiNone>
 __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict__ x, const bf16* __restrict__ y,
                                                           TO* __restrict__ out, int M, int N, int K, int tiles_m,
-                                                          int tiles_n, int kslice) {
+                                                          int tiles_n, int kslice, bf16* __restrict__ aux) {
   typedef Gemm2 G;
   typedef OperandTile<!XT> XTl;
   typedef OperandTile<YT> YTl;
   static_assert(BM == 256 || (BM == 128 && !XT), "128-row tiles need a k-contiguous x");
   static_assert(SLOTS == 2 || (SLOTS == 3 && BM == 128), "three LDS stages fit 128-row tiles only");
+  static_assert(EPI == kEpiNone || sizeof(TO) == 2, "the GELU epilogues write bf16");
   constexpr int XF = BM / 64;                // x fragments (32 rows each) per wave and k-step
   constexpr int kDmaX = BM / 64;             // x DMA instructions per wave and stage
   constexpr int kXBytes = BM == 256 ? XTl::kBytes : 2 * GemmXTile::kSubBytes;
@@ -465,6 +526,21 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
 
   // Epilogue: acc[j][i] is a C^T tile; register r of lane (l32, g) is
   // C[m0 + wm0 + 32 i + l32][n0 + wn0 + 32 j + (r / 4) * 8 + g * 4 + r % 4].
+  // The gradient epilogue's pre-activations are all loaded first, so their
+  // latency is paid once rather than once per store.
+  constexpr int UJ = EPI == kEpiGeluGrad ? 2 : 1, UI = EPI == kEpiGeluGrad ? XF : 1;
+  bf16x4 ua[UJ][UI][4];
+  if constexpr (EPI == kEpiGeluGrad) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < XF; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int m = m0 + wm0 + 32 * i + l32, n = n0 + wn0 + 32 * j + 8 * q + 4 * g;
+          ua[j][i][q] = m < M && n < N ? *reinterpret_cast<const bf16x4*>(aux + (int64_t)m * N + n) : bf16x4{};
+        }
+  }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -476,7 +552,14 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
         const int n = n0 + wn0 + 32 * j + 8 * q + 4 * g;
         if (n >= N) continue;  // N % 8 == 0: a quad is either all in or all out
         TO* dst = out + (int64_t)m * N + n;
-        if constexpr (sizeof(TO) == 2) {
+        if constexpr (EPI != kEpiNone) {
+          const bf16x4 v = {(bf16)acc[j][i][4 * q], (bf16)acc[j][i][4 * q + 1], (bf16)acc[j][i][4 * q + 2],
+                            (bf16)acc[j][i][4 * q + 3]};
+          if constexpr (EPI == kEpiGelu)
+            gelu_store(v, reinterpret_cast<bf16*>(dst), aux + (int64_t)m * N + n);
+          else
+            gelu_grad_store(v, ua[j][i < UI ? i : 0][q], reinterpret_cast<bf16*>(dst));
+        } else if constexpr (sizeof(TO) == 2) {
           *reinterpret_cast<bf16x4*>(dst) = bf16x4{(bf16)acc[j][i][4 * q], (bf16)acc[j][i][4 * q + 1],
                                                    (bf16)acc[j][i][4 * q + 2], (bf16)acc[j][i][4 * q + 3]};
         } else {
@@ -490,9 +573,9 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
 
 // out = sum over the K slices of the f32 partial slabs, in slice order
 // (deterministic), cast to TO. MN % 4 == 0.
-template <typename TO>
+template <typename TO, int EPI = kEpiNone>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, TO* __restrict__ out,
-                                                                int64_t mn, int slices) {
+                                                                int64_t mn, int slices, bf16* __restrict__ aux) {
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i >= mn) return;
   f32x4 acc = *reinterpret_cast<const f32x4*>(part + i);
@@ -500,7 +583,10 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
     const f32x4 v = *reinterpret_cast<const f32x4*>(part + (int64_t)s * mn + i);
     acc += v;
   }
-  if constexpr (sizeof(TO) == 2)
+  if constexpr (EPI != kEpiNone)
+    gelu_epilogue<EPI>(bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]}, reinterpret_cast<bf16*>(out + i),
+                       aux + i);
+  else if constexpr (sizeof(TO) == 2)
     *reinterpret_cast<bf16x4*>(out + i) = bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
   else
     *reinterpret_cast<f32x4*>(out + i) = acc;
@@ -544,20 +630,21 @@ int pick_bm(int64_t M, int64_t N, bool xt) {
   return 11 * cdiv(t128, cus) < 20 * cdiv(t256, cus) ? 128 : 256;
 }
 
-template <typename TO, bool XT, bool YT>
+template <typename TO, bool XT, bool YT, int EPI = kEpiNone>
 int launch_gemm_dma_t(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, void* ws,
-                      int64_t ws_bytes, hipStream_t stream) {
+                      int64_t ws_bytes, hipStream_t stream, void* aux = nullptr) {
   typedef Gemm2 G;
+  bf16* const ax = static_cast<bf16*>(aux);
   if constexpr (!XT) {
     if (pick_bm(M, N, XT) == 128) {
       constexpr int kLds128 = 3 * (2 * GemmXTile::kSubBytes + OperandTile<YT>::kBytes);
       static_assert(kLds128 <= 160 * 1024, "three stages of a 128-row tile fit the LDS");
       const int64_t tiles_m = cdiv(M, (int64_t)128), tiles_n = cdiv(N, G::BN);
-      auto kern = gemm_dma_kernel<TO, false, YT, 128, 3>;
+      auto kern = gemm_dma_kernel<TO, false, YT, 128, 3, EPI>;
       (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds128);
       hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n)), dim3(G::kThreads), kLds128, stream,
                          static_cast<const bf16*>(x), static_cast<const bf16*>(y), static_cast<TO*>(out), (int)M,
-                         (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)K);
+                         (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)K, ax);
       return check_launch("ferrite_matmul");
     }
   }
@@ -570,31 +657,31 @@ int launch_gemm_dma_t(const void* x, const void* y, void* out, int64_t M, int64_
   constexpr int kLds = 2 * (OperandTile<!XT>::kBytes + OperandTile<YT>::kBytes);
   const dim3 grid((unsigned)(tiles_m * tiles_n * slices));
   if (slices == 1) {
-    auto kern = gemm_dma_kernel<TO, XT, YT>;
+    auto kern = gemm_dma_kernel<TO, XT, YT, 256, 2, EPI>;
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
     hipLaunchKernelGGL(kern, grid, dim3(G::kThreads), kLds, stream, static_cast<const bf16*>(x),
                        static_cast<const bf16*>(y), static_cast<TO*>(out), (int)M, (int)N, (int)K, (int)tiles_m,
-                       (int)tiles_n, kslice);
+                       (int)tiles_n, kslice, ax);
   } else {
     auto kern = gemm_dma_kernel<float, XT, YT>;
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
     hipLaunchKernelGGL(kern, grid, dim3(G::kThreads), kLds, stream, static_cast<const bf16*>(x),
                        static_cast<const bf16*>(y), static_cast<float*>(ws), (int)M, (int)N, (int)K, (int)tiles_m,
-                       (int)tiles_n, kslice);
+                       (int)tiles_n, kslice, nullptr);
     const int64_t mn = M * N;
-    hipLaunchKernelGGL((gemm_splitk_reduce_kernel<TO>), dim3((unsigned)cdiv(mn / 4, 256)), dim3(256), 0, stream,
-                       static_cast<const float*>(ws), static_cast<TO*>(out), mn, slices);
+    hipLaunchKernelGGL((gemm_splitk_reduce_kernel<TO, EPI>), dim3((unsigned)cdiv(mn / 4, 256)), dim3(256), 0, stream,
+                       static_cast<const float*>(ws), static_cast<TO*>(out), mn, slices, ax);
   }
   return check_launch("ferrite_matmul");
 }
 
-template <typename TO>
+template <typename TO, int EPI = kEpiNone>
 int launch_gemm_dma(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, bool xt, bool yt,
-                    void* ws, int64_t ws_bytes, hipStream_t stream) {
-  if (xt && yt) return launch_gemm_dma_t<TO, true, true>(x, y, out, M, N, K, ws, ws_bytes, stream);
-  if (xt) return launch_gemm_dma_t<TO, true, false>(x, y, out, M, N, K, ws, ws_bytes, stream);
-  if (yt) return launch_gemm_dma_t<TO, false, true>(x, y, out, M, N, K, ws, ws_bytes, stream);
-  return launch_gemm_dma_t<TO, false, false>(x, y, out, M, N, K, ws, ws_bytes, stream);
+                    void* ws, int64_t ws_bytes, hipStream_t stream, void* aux = nullptr) {
+  if (xt && yt) return launch_gemm_dma_t<TO, true, true, EPI>(x, y, out, M, N, K, ws, ws_bytes, stream, aux);
+  if (xt) return launch_gemm_dma_t<TO, true, false, EPI>(x, y, out, M, N, K, ws, ws_bytes, stream, aux);
+  if (yt) return launch_gemm_dma_t<TO, false, true, EPI>(x, y, out, M, N, K, ws, ws_bytes, stream, aux);
+  return launch_gemm_dma_t<TO, false, false, EPI>(x, y, out, M, N, K, ws, ws_bytes, stream, aux);
 }
 
 // Whether the DMA-fed kernel takes this problem: whole 64-deep k steps, N % 8 == 0 (and
@@ -647,6 +734,41 @@ extern "C" int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, in
   }
   if (out_dtype == FERRITE_BF16) return launch_gemm<float, bf16, 128, 128, 32, 2, 2>(x, y, out, m, n, k, s);
   return launch_gemm<float, float, 128, 128, 32, 2, 2>(x, y, out, m, n, k, s);
+}
+
+extern "C" int ferrite_hip_matmul_gelu(const void* x, const void* y, void* out, void* aux, int64_t m, int64_t n,
+                                       int64_t k, int x_t, int y_t, int mode, void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
+  using namespace ferrite;
+  const char* name = "ferrite_hip_matmul_gelu";
+  if (mode != FERRITE_GELU && mode != FERRITE_GELU_GRAD)
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": mode must be FERRITE_GELU or FERRITE_GELU_GRAD");
+  if (m < 1 || n < 1 || k < 1) return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": need M, N, K >= 1");
+  if (!x || !y || !out || !aux) return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": null pointer");
+  if (aux == out) return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": aux and out must differ");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool xt = x_t != 0, yt = y_t != 0;
+  auto a8 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; };
+  if (dma_ok(x, y, out, m, n, k, xt, yt) && a8(aux)) {
+    if (mode == FERRITE_GELU)
+      return launch_gemm_dma<bf16, kEpiGelu>(x, y, out, m, n, k, xt, yt, workspace, workspace_bytes, s, aux);
+    return launch_gemm_dma<bf16, kEpiGeluGrad>(x, y, out, m, n, k, xt, yt, workspace, workspace_bytes, s, aux);
+  }
+  // Other shapes: the plain product (into aux for the forward, into out for the
+  // gradient), then the GELU as a pass of its own.
+  void* prod = mode == FERRITE_GELU ? aux : out;
+  if (int rc = ferrite_hip_matmul_ex(x, y, prod, m, n, k, x_t, y_t, FERRITE_BF16, FERRITE_BF16, workspace,
+                                     workspace_bytes, stream))
+    return rc;
+  const int64_t mn = m * n;
+  if (cdiv(mn, 256) > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": output too large");
+  if (mode == FERRITE_GELU)
+    hipLaunchKernelGGL(gelu_pass_kernel<kEpiGelu>, dim3((unsigned)cdiv(mn, 256)), dim3(256), 0, s,
+                       static_cast<bf16*>(out), static_cast<bf16*>(aux), mn);
+  else
+    hipLaunchKernelGGL(gelu_pass_kernel<kEpiGeluGrad>, dim3((unsigned)cdiv(mn, 256)), dim3(256), 0, s,
+                       static_cast<bf16*>(out), static_cast<bf16*>(aux), mn);
+  return check_launch(name);
 }
 
 extern "C" int ferrite_hip_matmul(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k,

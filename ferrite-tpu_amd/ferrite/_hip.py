@@ -19,6 +19,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libferrite_
 
 F32 = 0
 BF16 = 1
+GELU = 1
+GELU_GRAD = 2
 OK = 0
 
 _c_i64 = ctypes.c_int64
@@ -70,6 +72,10 @@ SIGNATURES: dict[str, tuple] = {
     "ferrite_hip_attn_bwd_dq": (
         _c_int,
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f32, _vp],
+    ),
+    "ferrite_hip_matmul_gelu": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp, _c_i64, _vp],
     ),
     "ferrite_hip_attn_bwd_dq_delta": (
         _c_int,

@@ -106,6 +106,71 @@ def matmul(x, y, *, block_m: int | None = None, block_n: int | None = None, bloc
     return _MatmulFn.apply(x, y, cfg)
 
 
+def _mm_gelu(xs, ys, aux, m: int, n: int, k: int, x_t: bool, y_t: bool, mode: int):
+    """bf16 [m, n] product of op(xs) @ op(ys) with a GELU epilogue (ferrite_hip_matmul_gelu):
+    mode GELU writes the pre-activation into aux and returns gelu of it; mode GELU_GRAD
+    returns the product times gelu'(aux)."""
+    xs, ys = xs.contiguous(), ys.contiguous()
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=xs.device)
+    if (x_t or y_t) and not _transposed_ok(torch.bfloat16, m, n, k, x_t, (xs, ys, out)):
+        if x_t:
+            xs, x_t = xs.t().contiguous(), False
+        if y_t:
+            ys, y_t = ys.t().contiguous(), False
+    lib = _hip.lib()
+    ws_bytes = lib.ferrite_hip_matmul_workspace(m, n, k, _hip.BF16)
+    ws = torch.empty(((ws_bytes + 3) // 4,), dtype=torch.float32, device=xs.device) if ws_bytes > 0 else None
+    rc = lib.ferrite_hip_matmul_gelu(xs.data_ptr(), ys.data_ptr(), out.data_ptr(), aux.data_ptr(), m, n, k, int(x_t),
+                                     int(y_t), mode, _hip.ptr(ws), max(ws_bytes, 0), _hip.stream_of(xs))
+    _hip.check(rc, "ferrite_matmul_gelu")
+    return out
+
+
+class _GeluMlpFn(torch.autograd.Function):
+    """gelu(x @ w1) @ w2 with the GELU in the matmul epilogues. Forward: the up-projection
+    stores u = x @ w1 and a = gelu(u) in one pass. Backward: the product g @ w2^T is scaled by
+    gelu'(u) as it is stored, so neither direction runs an elementwise GELU pass. The other
+    products are the matmul VJP's (transposed operands read in place)."""
+
+    @staticmethod
+    def forward(ctx, x, w1, w2):
+        t, d = x.shape
+        f, e = w1.shape[1], w2.shape[1]
+        u = torch.empty((t, f), dtype=torch.bfloat16, device=x.device)
+        a = _mm_gelu(x, w1, u, t, f, d, False, False, _hip.GELU)
+        out = _mm(a, w2, t, e, f, False, False, torch.bfloat16)
+        ctx.save_for_backward(x, w1, w2, u, a)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w1, w2, u, a = ctx.saved_tensors
+        t, d = x.shape
+        f, e = w1.shape[1], w2.shape[1]
+        g = g.to(torch.bfloat16).contiguous()
+        du = _mm_gelu(g, w2, u, t, f, e, False, True, _hip.GELU_GRAD)  # (g @ w2^T) * gelu'(u)
+        dw2 = _mm(a, g, f, e, t, True, False, torch.bfloat16)  # a^T @ g
+        dx = _mm(du, w1, t, d, f, False, True, torch.bfloat16)  # du @ w1^T
+        dw1 = _mm(x, du, d, f, t, True, False, torch.bfloat16)  # x^T @ du
+        return dx, dw1, dw2
+
+
+def mlp_gelu(x, w1, w2):
+    """``gelu(x @ w1) @ w2`` (the tanh GELU, jax.nn.gelu(approximate=True)) for bf16
+    ``x: [..., d]``, ``w1: [d, f]``, ``w2: [f, e]``, differentiable. The transformer MLP of
+    model/gpt.py:141, with the GELU and its derivative applied inside the matmul kernels."""
+    if x.dtype != torch.bfloat16 or w1.dtype != torch.bfloat16 or w2.dtype != torch.bfloat16:
+        raise ValueError("mlp_gelu takes bf16 x, w1, w2")
+    if w1.ndim != 2 or w2.ndim != 2 or x.shape[-1] != w1.shape[0] or w1.shape[1] != w2.shape[0]:
+        raise ValueError(f"expected [..., d] @ [d, f] @ [f, e]; got {tuple(x.shape)}, {tuple(w1.shape)}, {tuple(w2.shape)}")
+    _hip.require_gpu(x, w1, w2)
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.shape[0] == 0:
+        return x.new_zeros((*lead, w2.shape[1]))
+    return _GeluMlpFn.apply(x2, w1, w2).reshape(*lead, w2.shape[1])
+
+
 def matmul_reference(x, y, *, out_dtype=None):
     """Torch baseline with the same numerics contract (f32 accumulation), matmul.py:129-131."""
     out = torch.matmul(x.float(), y.float())

@@ -31,7 +31,7 @@ import torch.nn.functional as F
 from ferrite import platform
 from ferrite.kernels.flash_attention import BlockSizes, flash_attention, flash_attention_reference
 from ferrite.kernels.heads import merge_heads, split_heads
-from ferrite.kernels.matmul import matmul
+from ferrite.kernels.matmul import matmul, mlp_gelu
 from ferrite.kernels.rmsnorm import rmsnorm, rmsnorm_reference
 
 ROUTES = ("pallas", "xla")
@@ -172,6 +172,14 @@ def _linear(x, w, cfg: GPTConfig):
     return y.reshape(*lead, w.shape[1])
 
 
+def _mlp(y, layer, cfg: GPTConfig):
+    """gelu(y @ w1) @ w2 (gpt.py:141). The bf16 kernel route fuses the GELU and its derivative
+    into the matmul kernels (mlp_gelu); otherwise two linears around torch's tanh GELU."""
+    if cfg.linear == "pallas" and cfg.dtype == torch.bfloat16:
+        return mlp_gelu(y.to(cfg.dtype), layer["w1"].to(cfg.dtype), layer["w2"].to(cfg.dtype))
+    return _linear(F.gelu(_linear(y, layer["w1"], cfg), approximate="tanh"), layer["w2"], cfg)
+
+
 def _norm(x, w, residual, cfg: GPTConfig):
     """RMSNorm, or fused add+RMSNorm returning (h, y) when ``residual`` is given (gpt.py:107-110)."""
     if cfg.norm == "pallas":
@@ -286,7 +294,7 @@ def _trunk(params, tokens, cfg: GPTConfig):
         a = _merge_heads(_attention(q, k, v, cfg), cfg)  # [B, S, d]
         a = _linear(a, layer["wo"], cfg)
         h, y2 = _norm(a, layer["ln2"], h, cfg)
-        pending = _linear(F.gelu(_linear(y2, layer["w1"], cfg), approximate="tanh"), layer["w2"], cfg)
+        pending = _mlp(y2, layer, cfg)
     _, y = _norm(pending, params["ln_f"], h, cfg)
     return y.reshape(-1, cfg.d_model)
 

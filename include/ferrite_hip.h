@@ -28,6 +28,8 @@
  *                                                          _norm/_add_norm, XLA fusions in the reference)
  *   ferrite_hip_matmul        matmul.py:27-38, :52-86    ("ferrite_matmul")
  *   ferrite_hip_matmul_ex     matmul.py:99-104 (the VJP's products, transposed operands read in place)
+ *   ferrite_hip_matmul_gelu   model/gpt.py:141 (the MLP's matmul and jax.nn.gelu, an XLA fusion
+ *                                               after the matmul custom call in the reference)
  *   ferrite_hip_adamw         ../model/train.py:59-74    (adamw_update, XLA fusions in the reference)
  *   ferrite_hip_cross_entropy_fwd/_bwd ../model/gpt.py:147-152 (loss_fn and its autodiff, XLA in the reference)
  *   ferrite_hip_heads_split/_merge ../model/gpt.py:137-138 (the head transposes, XLA copies in the reference)
@@ -50,6 +52,10 @@ extern "C" {
 /* Element types. */
 #define FERRITE_F32 0
 #define FERRITE_BF16 1
+
+/* Epilogue modes of ferrite_hip_matmul_gelu. */
+#define FERRITE_GELU 1      /* out = gelu(x @ y), aux <- x @ y */
+#define FERRITE_GELU_GRAD 2 /* out = (x @ y) * gelu'(aux) */
 
 /* Return codes. */
 #define FERRITE_OK 0
@@ -120,6 +126,23 @@ int ferrite_hip_matmul(const void* x, const void* y, void* out, int64_t m, int64
 int64_t ferrite_hip_matmul_workspace(int64_t m, int64_t n, int64_t k, int in_dtype);
 int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k, int x_t, int y_t,
                           int in_dtype, int out_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * The MLP's up-projection and its GELU in one pass (model/gpt.py:141:
+ * jax.nn.gelu(x @ w1, approximate=True), the tanh form), and the matching
+ * gradient pass. bf16 operands and outputs; x_t / y_t, the workspace and the K
+ * split as in ferrite_hip_matmul_ex. aux and out are distinct [M, N] bf16 buffers.
+ *   mode FERRITE_GELU:      aux <- bf16(op(x) @ op(y))  (the pre-activation u)
+ *                           out <- bf16(gelu(aux))
+ *   mode FERRITE_GELU_GRAD: aux holds u;
+ *                           out <- bf16(bf16(op(x) @ op(y)) * gelu'(u))
+ * gelu and gelu' are taken in f32 from the bf16-rounded values, as an elementwise
+ * pass after the product computes them. Shapes the DMA-fed kernel takes apply
+ * them in its store (or in the K split's reduction); others run the product and
+ * then an elementwise pass.
+ */
+int ferrite_hip_matmul_gelu(const void* x, const void* y, void* out, void* aux, int64_t m, int64_t n, int64_t k,
+                            int x_t, int y_t, int mode, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Decode attention over a static KV cache (../serving/engine.py:89-104).
