@@ -29,9 +29,8 @@ from typing import Any
 
 import numpy as np
 import torch
-import torch.nn.functional as F
 
-from ferrite.model.gpt import GPTConfig, _attention, _dot_f32, _linear, _merge_heads, _norm, _split_heads
+from ferrite.model.gpt import GPTConfig, _attention, _dot_f32, _linear, _merge_heads, _mlp, _norm, _split_heads
 
 
 @dataclasses.dataclass(frozen=True)
@@ -66,7 +65,7 @@ def _block_prefill(layer, h, pending, cfg: GPTConfig):
     q, k, v = _split_heads(_linear(y, layer["wqkv"], cfg), cfg)  # [B, H, S, hd]
     a = _linear(_merge_heads(_attention(q, k, v, cfg), cfg), layer["wo"], cfg)
     h, y2 = _norm(a, layer["ln2"], h, cfg)
-    pending = _linear(F.gelu(_linear(y2, layer["w1"], cfg), approximate="tanh"), layer["w2"], cfg)
+    pending = _mlp(y2, layer, cfg)
     return h, pending, k, v
 
 
@@ -136,7 +135,7 @@ def decode_step(params, token, pos, k_cache, v_cache, cfg: GPTConfig):
             a = _cache_attention(q, k_cache[i], v_cache[i], pos, scale)
         a = _linear(a.reshape(b, cfg.d_model), layer["wo"], cfg)
         h, y2 = _norm(a, layer["ln2"], h, cfg)
-        pending = _linear(F.gelu(_linear(y2, layer["w1"], cfg), approximate="tanh"), layer["w2"], cfg)
+        pending = _mlp(y2, layer, cfg)
     _, y = _norm(pending, params["ln_f"], h, cfg)
     return _dot_f32(y, params["tok_emb"].to(cfg.dtype).t())
 
