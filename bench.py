@@ -226,15 +226,19 @@ def bench_matmul(steps, warmup):
         bm = (torch.rand(n, n, device=dev, generator=g) * 2 - 1).to(dt)
         c = torch.empty(n, n, device=dev, dtype=dt)
         lib, st = _hip.lib(), _hip.stream_of(a)
+        # what ferrite.kernels.matmul runs: the workspace from the size query, allocated once
+        ws_bytes = lib.ferrite_hip_matmul_workspace(n, n, n, code)
+        ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=dev)
 
         def mm():
-            _hip.check(lib.ferrite_hip_matmul(a.data_ptr(), bm.data_ptr(), c.data_ptr(), n, n, n, code, code, st), "mm")
+            _hip.check(lib.ferrite_hip_matmul_ex(a.data_ptr(), bm.data_ptr(), c.data_ptr(), n, n, n, 0, 0, code, code,
+                                                 ws.data_ptr(), ws_bytes, st), "mm")
 
         t = _events_time(mm, steps, warmup)
         t_torch = _events_time(lambda: torch.matmul(a, bm), steps, warmup)
         peak = PEAK_BF16_TFLOPS if dt == torch.bfloat16 else PEAK_FP32_TFLOPS
         out[name] = {"us": t * 1e6, "tflops": 2 * n**3 / t / 1e12, "frac_peak": 2 * n**3 / t / 1e12 / peak,
-                     "torch_matmul_us": t_torch * 1e6}
+                     "torch_matmul_us": t_torch * 1e6, "workspace_bytes": ws_bytes}
     return out
 
 

@@ -155,10 +155,12 @@ struct Gemm {
   }
 };
 
+// blockIdx.y is the K slice: k from kslice * blockIdx.y, at most kslice deep (a
+// multiple of BK), into the f32 partial slab blockIdx.y of `out` when split.
 template <typename T, typename TO, int BM, int BN, int BK, int WM, int WN, bool ALIGNED>
 __global__ __launch_bounds__((WM * WN * 64), 1) void gemm_kernel(const T* __restrict__ x, const T* __restrict__ y,
                                                               TO* __restrict__ out, int64_t M, int64_t N, int64_t K,
-                                                              int tiles_n) {
+                                                              int tiles_n, int64_t kslice) {
   typedef Gemm<T, TO, BM, BN, BK, WM, WN, ALIGNED> G;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tile = blockIdx.x;
@@ -175,14 +177,16 @@ __global__ __launch_bounds__((WM * WN * 64), 1) void gemm_kernel(const T* __rest
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
 
-  const int nk = (int)((K + BK - 1) / BK);
+  const int64_t kbeg = kslice * blockIdx.y;
+  out += (int64_t)blockIdx.y * M * N;
+  const int nk = (int)((std::min(K - kbeg, kslice) + BK - 1) / BK);
   typename G::Stage st;
-  G::load(st, x, y, m0, n0, 0, M, N, K);
+  G::load(st, x, y, m0, n0, kbeg, M, N, K);
   G::store(st, smem);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     char* cur = smem + (kt & 1) * G::kStageBytes;
-    if (kt + 1 < nk) G::load(st, x, y, m0, n0, (int64_t)(kt + 1) * BK, M, N, K);
+    if (kt + 1 < nk) G::load(st, x, y, m0, n0, kbeg + (int64_t)(kt + 1) * BK, M, N, K);
     G::compute(cur, acc, wm0, wn0);
     if (kt + 1 < nk) G::store(st, smem + ((kt + 1) & 1) * G::kStageBytes);
     __syncthreads();
@@ -219,29 +223,6 @@ __global__ __launch_bounds__((WM * WN * 64), 1) void gemm_kernel(const T* __rest
       }
     }
   }
-}
-
-template <typename T, typename TO, int BM, int BN, int BK, int WM, int WN>
-int launch_gemm(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
-  typedef Gemm<T, TO, BM, BN, BK, WM, WN, true> G;
-  const int64_t tiles_m = cdiv(M, BM), tiles_n = cdiv(N, BN);
-  if (tiles_m * tiles_n > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "matmul: output too large");
-  const size_t lds = 2 * (size_t)G::kStageBytes;
-  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  const bool aligned = K % Elem<T>::kVec == 0 && N % Elem<T>::kVec == 0 && N % 4 == 0 && a16(x) && a16(y) && a16(out);
-  dim3 grid((unsigned)(tiles_m * tiles_n)), block(WM * WN * 64);
-  if (aligned) {
-    auto k = gemm_kernel<T, TO, BM, BN, BK, WM, WN, true>;
-    (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL(k, grid, block, lds, stream, static_cast<const T*>(x), static_cast<const T*>(y),
-                       static_cast<TO*>(out), M, N, K, (int)tiles_n);
-  } else {
-    auto k = gemm_kernel<T, TO, BM, BN, BK, WM, WN, false>;
-    (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL(k, grid, block, lds, stream, static_cast<const T*>(x), static_cast<const T*>(y),
-                       static_cast<TO*>(out), M, N, K, (int)tiles_n);
-  }
-  return check_launch("ferrite_matmul");
 }
 
 // ===========================================================================
@@ -592,6 +573,48 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
     *reinterpret_cast<f32x4*>(out + i) = acc;
 }
 
+template <typename T, typename TO, int BM, int BN, int BK, int WM, int WN, bool AL>
+void launch_gemm_kernel(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, int64_t tiles,
+                        int64_t tiles_n, int slices, int64_t kslice, size_t lds, hipStream_t stream) {
+  auto k = gemm_kernel<T, TO, BM, BN, BK, WM, WN, AL>;
+  (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipLaunchKernelGGL(k, dim3((unsigned)tiles, (unsigned)slices), dim3(WM * WN * 64), lds, stream,
+                     static_cast<const T*>(x), static_cast<const T*>(y), static_cast<TO*>(out), M, N, K, (int)tiles_n,
+                     kslice);
+}
+
+template <typename T, typename TO, int BM, int BN, int BK, int WM, int WN>
+int launch_gemm(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, hipStream_t stream,
+                int slices = 1, void* ws = nullptr) {
+  typedef Gemm<T, TO, BM, BN, BK, WM, WN, true> G;
+  const int64_t tiles_m = cdiv(M, BM), tiles_n = cdiv(N, BN);
+  if (tiles_m * tiles_n > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "matmul: output too large");
+  const size_t lds = 2 * (size_t)G::kStageBytes;
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const bool aligned = K % Elem<T>::kVec == 0 && N % Elem<T>::kVec == 0 && N % 4 == 0 && a16(x) && a16(y) &&
+                       a16(slices > 1 ? ws : out);
+  const int64_t kslice = slices > 1 ? cdiv(cdiv(K, slices), (int64_t)BK) * BK : K;
+  if (slices > 1) slices = (int)cdiv(K, kslice);
+  if (slices > 1) {
+    if (aligned)
+      launch_gemm_kernel<T, float, BM, BN, BK, WM, WN, true>(x, y, ws, M, N, K, tiles_m * tiles_n, tiles_n, slices,
+                                                             kslice, lds, stream);
+    else
+      launch_gemm_kernel<T, float, BM, BN, BK, WM, WN, false>(x, y, ws, M, N, K, tiles_m * tiles_n, tiles_n, slices,
+                                                              kslice, lds, stream);
+    const int64_t mn = M * N;
+    hipLaunchKernelGGL((gemm_splitk_reduce_kernel<TO>), dim3((unsigned)cdiv(mn / 4, 256)), dim3(256), 0, stream,
+                       static_cast<const float*>(ws), static_cast<TO*>(out), mn, slices, nullptr);
+  } else if (aligned) {
+    launch_gemm_kernel<T, TO, BM, BN, BK, WM, WN, true>(x, y, out, M, N, K, tiles_m * tiles_n, tiles_n, 1, K, lds,
+                                                        stream);
+  } else {
+    launch_gemm_kernel<T, TO, BM, BN, BK, WM, WN, false>(x, y, out, M, N, K, tiles_m * tiles_n, tiles_n, 1, K, lds,
+                                                         stream);
+  }
+  return check_launch("ferrite_matmul");
+}
+
 // K slices for a problem with few output tiles: as many slices as keep every
 // workgroup in one round (one per CU), each at least 512 deep; 1 when the tiles
 // already fill most CUs or the f32 partials would outweigh the work. A round
@@ -611,6 +634,22 @@ int splitk_slices(int64_t M, int64_t N, int64_t K) {
 
 int64_t splitk_workspace(int64_t M, int64_t N, int64_t K) {
   const int s = splitk_slices(M, N, K);
+  return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
+}
+
+// f32 products too small for 128 x 128 tiles on every CU run 64 x 64 tiles of two
+// waves; with fewer than two waves per SIMD they also split K, each slice at least
+// 128 deep (1000^3: 256 tiles, 512 waves for 1024 SIMDs, so 4 slices).
+bool f32_small(int64_t M, int64_t N) { return cdiv(M, (int64_t)128) * cdiv(N, (int64_t)128) < cu_count(); }
+int f32_slices(int64_t M, int64_t N, int64_t K) {
+  if (!f32_small(M, N) || (M * N) % 4 != 0) return 1;
+  const int64_t waves = 2 * cdiv(M, (int64_t)64) * cdiv(N, (int64_t)64);
+  const int64_t s = std::min<int64_t>({cdiv(8 * (int64_t)cu_count(), waves), K / 128, (int64_t)8});
+  if (s < 2) return 1;
+  return (int)cdiv(K, cdiv(cdiv(K, s), (int64_t)32) * 32);
+}
+int64_t f32_workspace(int64_t M, int64_t N, int64_t K) {
+  const int s = f32_slices(M, N, K);
   return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
 }
 
@@ -700,7 +739,7 @@ bool dma_ok(const void* x, const void* y, const void* out, int64_t m, int64_t n,
 
 extern "C" int64_t ferrite_hip_matmul_workspace(int64_t m, int64_t n, int64_t k, int in_dtype) {
   if (m < 1 || n < 1 || k < 1) return -1;
-  return in_dtype == FERRITE_BF16 ? ferrite::splitk_workspace(m, n, k) : 0;
+  return in_dtype == FERRITE_BF16 ? ferrite::splitk_workspace(m, n, k) : ferrite::f32_workspace(m, n, k);
 }
 
 extern "C" int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k,
@@ -727,10 +766,13 @@ extern "C" int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, in
   }
   // f32: 128 x 128 tiles of four waves reach ~80% of the fp32 MFMA peak at 4096^3; a
   // problem with fewer such tiles than CUs (1000^3 has 64) runs 64 x 64 tiles of two
-  // waves instead, four times the workgroups (1000^3: 81 -> 50 us on MI355X).
-  if (cdiv(m, (int64_t)128) * cdiv(n, (int64_t)128) < 256) {
-    if (out_dtype == FERRITE_BF16) return launch_gemm<float, bf16, 64, 64, 32, 1, 2>(x, y, out, m, n, k, s);
-    return launch_gemm<float, float, 64, 64, 32, 1, 2>(x, y, out, m, n, k, s);
+  // waves instead, four times the workgroups (1000^3: 81 -> 50 us on MI355X), and splits
+  // K when that still leaves SIMDs idle and the caller gives a workspace.
+  if (f32_small(m, n)) {
+    int sl = f32_slices(m, n, k);
+    if (sl > 1 && (!workspace || workspace_bytes < f32_workspace(m, n, k))) sl = 1;
+    if (out_dtype == FERRITE_BF16) return launch_gemm<float, bf16, 64, 64, 32, 1, 2>(x, y, out, m, n, k, s, sl, workspace);
+    return launch_gemm<float, float, 64, 64, 32, 1, 2>(x, y, out, m, n, k, s, sl, workspace);
   }
   if (out_dtype == FERRITE_BF16) return launch_gemm<float, bf16, 128, 128, 32, 2, 2>(x, y, out, m, n, k, s);
   return launch_gemm<float, float, 128, 128, 32, 2, 2>(x, y, out, m, n, k, s);
