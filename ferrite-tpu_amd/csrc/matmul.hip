@@ -376,8 +376,8 @@ struct OperandTile {
 // = x . y over this slice. XT: x is given transposed, stored [K,M]; YT: y is given
 // transposed, stored [N,K]. BM = 256 or 128 output rows per workgroup (128 only
 // with a k-contiguous x, whose tile is then the first two 64-row subtiles).
-template <typename TO, bool XT, bool YT, int BM = 256, int SLOTS = 2, int EPI = kEpiNone>
-__global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict__ x, const bf16* __restrict__ y,
+template <typename TO, bool XT, bool YT, int BM = 256, int SLOTS = 2, int EPI = kEpiNone, int W = 8>
+__global__ __launch_bounds__(64 * W, W == 8 ? 2 : 1) void gemm_dma_kernel(const bf16* __restrict__ x, const bf16* __restrict__ y,
                                                           TO* __restrict__ out, int M, int N, int K, int tiles_m,
                                                           int tiles_n, int kslice, bf16* __restrict__ aux) {
   typedef Gemm2 G;
@@ -386,8 +386,13 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
   static_assert(BM == 256 || (BM == 128 && !XT), "128-row tiles need a k-contiguous x");
   static_assert(SLOTS == 2 || (SLOTS == 3 && BM == 128), "three LDS stages fit 128-row tiles only");
   static_assert(EPI == kEpiNone || sizeof(TO) == 2, "the GELU epilogues write bf16");
-  constexpr int XF = BM / 64;                // x fragments (32 rows each) per wave and k-step
-  constexpr int kDmaX = BM / 64;             // x DMA instructions per wave and stage
+  static_assert(W == 8 || (W == 4 && BM == 256), "four waves own 128 x 128 each of a 256-row tile");
+  // W = 8: wave w owns rows (w / 4) BM/2 .., columns (w % 4) 64 ..; W = 4: wave w owns
+  // rows (w / 2) 128 .., columns (w % 2) 128 .. (one wave per SIMD, accumulators in AGPRs).
+  constexpr int YF = W == 8 ? 2 : 4;         // y fragments (32 columns each) per wave and k-step
+  constexpr int XF = W == 8 ? BM / 64 : 4;   // x fragments (32 rows each) per wave and k-step
+  constexpr int kDmaX = BM / 8 / W;          // x DMA instructions per wave and stage
+  constexpr int kDmaY = 32 / W;              // y DMA instructions per wave and stage
   constexpr int kXBytes = BM == 256 ? XTl::kBytes : 2 * GemmXTile::kSubBytes;
   constexpr int kStageBytes = kXBytes + YTl::kBytes;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -408,17 +413,18 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
   const int tm = first_m + (v % (kGroup * tiles_n)) % gsize;
   const int tn = (v % (kGroup * tiles_n)) / gsize;
   const int m0 = tm * BM, n0 = tn * G::BN;
-  const int wm0 = (wave >> 2) * (BM / 2), wn0 = (wave & 3) * 64;
+  const int wm0 = W == 8 ? (wave >> 2) * (BM / 2) : (wave >> 1) * 128;
+  const int wn0 = W == 8 ? (wave & 3) * 64 : (wave & 1) * 128;
   const int kbeg = slice * kslice;
   const int nk = min(K - kbeg, kslice) / G::BK;
   out += (int64_t)slice * M * N;
 
   // Per-lane DMA offsets; free indices past M or N read as zeros.
-  uint32_t xoff[kDmaX], yoff[G::kDma];
+  uint32_t xoff[kDmaX], yoff[kDmaY];
 #pragma unroll
-  for (int i = 0; i < kDmaX; ++i) xoff[i] = XTl::dma_off(wave + 8 * i, lane, XT ? M : K, m0, M);
+  for (int i = 0; i < kDmaX; ++i) xoff[i] = XTl::dma_off(wave + W * i, lane, XT ? M : K, m0, M);
 #pragma unroll
-  for (int i = 0; i < G::kDma; ++i) yoff[i] = YTl::dma_off(wave + 8 * i, lane, YT ? K : N, n0, N);
+  for (int i = 0; i < kDmaY; ++i) yoff[i] = YTl::dma_off(wave + W * i, lane, YT ? K : N, n0, N);
   // DMA instruction q (x instructions first, then y) of stage kt. A stage past
   // the slice gets an empty buffer range: its instructions read nothing and
   // write zeros into a slot that no later stage reads.
@@ -428,21 +434,21 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
     const uint32_t range = kt < nk ? 0x7ffffff0u : 0u;
     if (q < kDmaX) {
       const u32x4 rx = buffer_rsrc(XT ? x + (int64_t)k0 * M + m0 : x + (int64_t)m0 * K + k0, range);
-      dma16(rx, st + XTl::block_off(wave + 8 * q), xoff[q]);
+      dma16(rx, st + XTl::block_off(wave + W * q), xoff[q]);
     } else {
       const u32x4 ry = buffer_rsrc(YT ? y + (int64_t)n0 * K + k0 : y + (int64_t)k0 * N + n0, range);
-      dma16(ry, st + kXBytes + YTl::block_off(wave + 8 * (q - kDmaX)), yoff[q - kDmaX]);
+      dma16(ry, st + kXBytes + YTl::block_off(wave + W * (q - kDmaX)), yoff[q - kDmaX]);
     }
   };
-  constexpr int kDmaWave = kDmaX + G::kDma;  // DMA instructions per wave and stage
+  constexpr int kDmaWave = kDmaX + kDmaY;  // DMA instructions per wave and stage
   auto issue = [&](int kt) {
 #pragma unroll
     for (int q = 0; q < kDmaWave; ++q) issue_one(kt, q);
   };
 
-  f32x16 acc[2][XF];
+  f32x16 acc[YF][XF];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < YF; ++j)
 #pragma unroll
     for (int i = 0; i < XF; ++i)
 #pragma unroll
@@ -450,10 +456,10 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
 
   const int xb = XTl::lane_base(lane);
   const int yb = YTl::lane_base(lane);
-  // Per k-step of 16: NM products over 2 y fragments (A operand) and XF x
+  // Per k-step of 16: NM products over YF y fragments (A operand) and XF x
   // fragments (B).
-  constexpr int NM = 2 * XF;
-  constexpr int NFR = 2 + XF;
+  constexpr int NM = YF * XF;
+  constexpr int NFR = YF + XF;
   static_assert(NFR <= NM, "one fragment read per product slot at most");
   constexpr int NSLOT = 4 * NM;  // product slots per 64-deep stage
 
@@ -478,21 +484,21 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
     const int kload = kt + SLOTS - 1;
     const char* xs = smem + (kt % SLOTS) * kStageBytes + xb;
     const char* ys = smem + (kt % SLOTS) * kStageBytes + kXBytes + yb;
-    bf16x8 fa[2][2], fb[2][XF];
+    bf16x8 fa[2][YF], fb[2][XF];
     // Fragment f of k-step kk in the order of first use by the products
-    // (j, i) = (r / XF, r % XF): y 0, x 0 .. XF - 1, y 1.
+    // (j, i) = (r / XF, r % XF): y 0, x 0 .. XF - 1, then y 1 .. YF - 1.
     auto read = [&](int kk, int f) {
       if (f == 0)
         fa[kk & 1][0] = YTl::read(ys, kk, wn0);
       else if (f <= XF)
         fb[kk & 1][f - 1] = XTl::read(xs, kk, wm0 + 32 * (f - 1));
       else
-        fa[kk & 1][1] = YTl::read(ys, kk, wn0 + 32);
+        fa[kk & 1][f - XF] = YTl::read(ys, kk, wn0 + 32 * (f - XF));
     };
 #pragma unroll
     for (int f = 0; f < NFR; ++f) read(0, f);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
+#pragma clang loop unroll(full)
     for (int i = 0; i < NSLOT; ++i) {
       const int kk = i / NM, r = i % NM, c = kk & 1;
       if (kk + 1 < 4 && r < NFR) read(kk + 1, r);
@@ -509,11 +515,11 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
   // C[m0 + wm0 + 32 i + l32][n0 + wn0 + 32 j + (r / 4) * 8 + g * 4 + r % 4].
   // The gradient epilogue's pre-activations are all loaded first, so their
   // latency is paid once rather than once per store.
-  constexpr int UJ = EPI == kEpiGeluGrad ? 2 : 1, UI = EPI == kEpiGeluGrad ? XF : 1;
+  constexpr int UJ = EPI == kEpiGeluGrad ? YF : 1, UI = EPI == kEpiGeluGrad ? XF : 1;
   bf16x4 ua[UJ][UI][4];
   if constexpr (EPI == kEpiGeluGrad) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < YF; ++j)
 #pragma unroll
       for (int i = 0; i < XF; ++i)
 #pragma unroll
@@ -523,7 +529,7 @@ __global__ __launch_bounds__(512, 2) void gemm_dma_kernel(const bf16* __restrict
         }
   }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < YF; ++j) {
 #pragma unroll
     for (int i = 0; i < XF; ++i) {
       const int m = m0 + wm0 + 32 * i + l32;
@@ -669,6 +675,16 @@ int pick_bm(int64_t M, int64_t N, bool xt) {
   return 11 * cdiv(t128, cus) < 20 * cdiv(t256, cus) ? 128 : 256;
 }
 
+// Four waves of 128 x 128 outputs per 256 x 256 tile (one per SIMD, accumulators in
+// AGPRs) read a third fewer LDS bytes per product than eight waves of 128 x 64, but
+// have no second wave to cover a workgroup's start and end. They pay from four
+// rounds of workgroups on: 8192^3 1244 -> 1372 TFLOP/s, 8192 x 4096 x 4096 level,
+// 4096^3 (one round) 2-5% slower. Both give bitwise the same output.
+bool use_four_waves(int64_t M, int64_t N, int64_t K) {
+  (void)K;
+  return cdiv(M, (int64_t)256) * cdiv(N, (int64_t)256) >= 4 * (int64_t)cu_count();
+}
+
 template <typename TO, bool XT, bool YT, int EPI = kEpiNone>
 int launch_gemm_dma_t(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, void* ws,
                       int64_t ws_bytes, hipStream_t stream, void* aux = nullptr) {
@@ -696,9 +712,10 @@ int launch_gemm_dma_t(const void* x, const void* y, void* out, int64_t M, int64_
   constexpr int kLds = 2 * (OperandTile<!XT>::kBytes + OperandTile<YT>::kBytes);
   const dim3 grid((unsigned)(tiles_m * tiles_n * slices));
   if (slices == 1) {
-    auto kern = gemm_dma_kernel<TO, XT, YT, 256, 2, EPI>;
+    const bool w4 = use_four_waves(M, N, K);
+    auto kern = w4 ? gemm_dma_kernel<TO, XT, YT, 256, 2, EPI, 4> : gemm_dma_kernel<TO, XT, YT, 256, 2, EPI, 8>;
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-    hipLaunchKernelGGL(kern, grid, dim3(G::kThreads), kLds, stream, static_cast<const bf16*>(x),
+    hipLaunchKernelGGL(kern, grid, dim3(w4 ? 256 : G::kThreads), kLds, stream, static_cast<const bf16*>(x),
                        static_cast<const bf16*>(y), static_cast<TO*>(out), (int)M, (int)N, (int)K, (int)tiles_m,
                        (int)tiles_n, kslice, ax);
   } else {

@@ -245,3 +245,39 @@ def test_deterministic(dev):
     runs = [_grads(q, k, v, do, dev, "bf16", True) for _ in range(2)]
     for a, b in zip(*runs):
         np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_kernels_are_race_free(dev, dtype):
+    """tests/test_flash_attention.py:79-85 runs forward+backward at 1x1x256x128 under Pallas's
+    interpret-mode race detector, which has no MI355X counterpart. The checks here: every output
+    of the forward and of each backward kernel (NaN-prefilled) is written, and three runs on the
+    same inputs are bitwise equal; a read racing with a write in another workgroup or wave would
+    show up as a NaN or as run-to-run differences."""
+    b, h, s, d = 1, 1, 256, 128
+    q, k, v = _qkv(11, (b, h, s, d), dtype)
+    do = normal(14, q.shape, dtype)
+    qt, kt, vt, dot = (to_dev(a, dtype, dev) for a in (q, k, v, do))
+    lib, st, dt = _hip.lib(), _hip.stream_of(qt), _hip.dtype_code(qt.dtype)
+    scale = d ** -0.5
+    runs = []
+    for _ in range(3):
+        o = torch.full_like(qt, float("nan"))
+        lse = torch.full((b, h, s), float("nan"), device=dev)
+        delta = torch.full((b, h, s), float("nan"), device=dev)
+        dq, dk, dv = (torch.full_like(qt, float("nan")) for _ in range(3))
+        _hip.check(lib.ferrite_hip_attn_fwd(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                            b, h, s, s, d, dt, 1, scale, st), "fwd")
+        _hip.check(lib.ferrite_hip_attn_bwd_dq_delta(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), o.data_ptr(),
+                                                     dot.data_ptr(), lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
+                                                     b, h, s, s, d, dt, 1, scale, st), "dq_delta")
+        _hip.check(lib.ferrite_hip_attn_bwd_dkv(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), dot.data_ptr(),
+                                                lse.data_ptr(), delta.data_ptr(), dk.data_ptr(), dv.data_ptr(), b, h, s,
+                                                s, d, dt, 1, scale, st), "dkv")
+        torch.cuda.synchronize()
+        outs = [o, lse, delta, dq, dk, dv]
+        assert not any(torch.isnan(t.float()).any() for t in outs)
+        runs.append([t.clone() for t in outs])
+    for later in runs[1:]:
+        for a, c in zip(runs[0], later):
+            assert torch.equal(a, c)
