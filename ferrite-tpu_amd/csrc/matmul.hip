@@ -528,10 +528,13 @@ __global__ __launch_bounds__(64 * W, W == 8 ? 2 : 1) void gemm_dma_kernel(const 
           ua[j][i][q] = m < M && n < N ? *reinterpret_cast<const bf16x4*>(aux + (int64_t)m * N + n) : bf16x4{};
         }
   }
+  // Row group i outermost: a row's YF * 32 columns (whole 128-byte lines) go out in
+  // consecutive stores; with the column tiles outermost the halves of each line were
+  // written 16 stores apart and half-written lines reached HBM twice (1.5x the bytes).
 #pragma unroll
-  for (int j = 0; j < YF; ++j) {
+  for (int i = 0; i < XF; ++i) {
 #pragma unroll
-    for (int i = 0; i < XF; ++i) {
+    for (int j = 0; j < YF; ++j) {
       const int m = m0 + wm0 + 32 * i + l32;
       if (m >= M) continue;
 #pragma unroll
