@@ -206,24 +206,27 @@ struct Stager {
 // Q / dO fragments of one wave's 32 rows held in registers as the B operand:
 // lane (l32, g) holds row r0 + l32, elements kk*16 + g*8 .. +8. With NEG the
 // fragments are negated (used for a negative softmax scale).
+// ld: element stride between rows (d for a dense [rows, d] tensor; larger for a head
+// of a token-major [rows, heads, d] one).
 template <typename T, int D, bool ALIGNED, bool NEG = false>
 __device__ __forceinline__ void load_row_frags(typename Elem<T>::frag (&f)[D / 16], const T* __restrict__ base,
-                                               int r0, int nrows, int d) {
+                                               int r0, int nrows, int d, int ld = 0) {
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
   const int row = r0 + l32;
+  if (ld == 0) ld = d;
   if constexpr (ALIGNED) {
     const __amdgpu_buffer_rsrc_t rsrc =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), (short)0, nrows * d * (int)sizeof(T), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), (short)0, nrows * ld * (int)sizeof(T), 0x00020000);
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
       const int c0 = kk * 16 + g * 8;
       if constexpr (sizeof(T) == 2) {
-        const int off = c0 < d ? (row * d + c0) * 2 : 0x7ffffff0;
+        const int off = c0 < d ? (row * ld + c0) * 2 : 0x7ffffff0;
         f[kk] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
       } else {
-        const int off0 = c0 < d ? (row * d + c0) * 4 : 0x7ffffff0;
-        const int off1 = c0 + 4 < d ? (row * d + c0 + 4) * 4 : 0x7ffffff0;
+        const int off0 = c0 < d ? (row * ld + c0) * 4 : 0x7ffffff0;
+        const int off1 = c0 + 4 < d ? (row * ld + c0 + 4) * 4 : 0x7ffffff0;
         const f32x4 a = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off0, 0, 0));
         const f32x4 b = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off1, 0, 0));
 #pragma unroll
@@ -239,7 +242,7 @@ __device__ __forceinline__ void load_row_frags(typename Elem<T>::frag (&f)[D / 1
     for (int kk = 0; kk < D / 16; ++kk) {
       const int c0 = kk * 16 + g * 8;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f[kk][e] = (rok && c0 + e < d) ? base[row * d + c0 + e] : (T)0.f;
+      for (int e = 0; e < 8; ++e) f[kk][e] = (rok && c0 + e < d) ? base[row * ld + c0 + e] : (T)0.f;
     }
   }
   if constexpr (NEG) {
@@ -255,16 +258,17 @@ __device__ __forceinline__ void load_row_frags(typename Elem<T>::frag (&f)[D / 1
 // out[row0 + l32][d] = acc * mul.
 template <typename T, int D, bool ALIGNED>
 __device__ __forceinline__ void store_acc_rows(const f32x16 (&acc)[D / 32], T* __restrict__ out, int64_t row,
-                                               int64_t nrows, int d, float mul) {
+                                               int64_t nrows, int d, float mul, int64_t ld = 0) {
   const int lane = threadIdx.x & 63;
   const int g = lane >> 5;
   if (row >= nrows) return;
+  if (ld == 0) ld = d;
 #pragma unroll
   for (int u = 0; u < D / 32; ++u) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int c = u * 32 + q * 8 + g * 4;
-      T* dst = out + row * d + c;
+      T* dst = out + row * ld + c;
       const float a0 = acc[u][q * 4 + 0] * mul, a1 = acc[u][q * 4 + 1] * mul;
       const float a2 = acc[u][q * 4 + 2] * mul, a3 = acc[u][q * 4 + 3] * mul;
       if (ALIGNED && c + 3 < d) {
@@ -282,6 +286,18 @@ __device__ __forceinline__ void store_acc_rows(const f32x16 (&acc)[D / 32], T* _
     }
   }
 }
+
+// Element strides of one tensor seen as [B, H, rows, d] with contiguous columns:
+// between batches, heads and rows. A dense [B, H, S, d] tensor has (H S d, S d, d);
+// the q part of a token-major [B, S, 3, H, d] projection has (3 S H d, d, 3 H d).
+struct View {
+  int64_t b, h, r;
+  __host__ __device__ int64_t at(int bh, int heads) const { return (int64_t)(bh / heads) * b + (int64_t)(bh % heads) * h; }
+};
+struct AttnViews {
+  View q, k, v, o, dout, dq, dk, dv;
+  int heads;
+};
 
 // N products acc(i) += A(i) * B(i) whose A operands come from LDS: the reads
 // run kAhead products ahead of the MFMAs and the scheduler is asked to
@@ -885,7 +901,7 @@ struct FwdW {
 template <int D, int RB, int W, bool ZIG>
 __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void attn_fwd_sw_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, bf16* __restrict__ o,
-    float* __restrict__ lse, int bh_count, int S, int d, float scale_log2, int neg_q, int n_qtiles) {
+    float* __restrict__ lse, int bh_count, int S, int d, float scale_log2, int neg_q, int n_qtiles, AttnViews vw) {
   typedef FwdW<D, RB, W> F;
   typedef typename F::KT KT;
   typedef typename F::VT VT;
@@ -912,23 +928,25 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
   const int n = (min(q0 + F::BQ, S) - 1) / F::BK + 1;
   const int n_w = q0w < S ? (q0w + 32 * RB - 1) / F::BK + 1 : 0;
 
-  const bf16* qb = q + (int64_t)bh * S * d;
-  const bf16* kb = k + (int64_t)bh * S * d;
-  const bf16* vb = v + (int64_t)bh * S * d;
+  // Row pitches (elements): d for dense [B, H, S, d] tensors.
+  const int ldq = (int)vw.q.r, ldk = (int)vw.k.r, ldv = (int)vw.v.r;
+  const bf16* qb = q + vw.q.at(bh, vw.heads);
+  const bf16* kb = k + vw.k.at(bh, vw.heads);
+  const bf16* vb = v + vw.v.at(bh, vw.heads);
 
   // K_0 and K_1 go out first; stage j then loads K_{j+3} and V_{j+1}.
-  const PpDma<KT, true, F::kWaves> kdma(wave, d);
-  const PpDma<VT, false, F::kWaves> vdma(wave, d);
-  kdma.issue(kb, 0, S, d, kring);
-  kdma.issue(kb, F::BK, S, d, kring + KT::kBytes);
+  const PpDma<KT, true, F::kWaves> kdma(wave, ldk);
+  const PpDma<VT, false, F::kWaves> vdma(wave, ldv);
+  kdma.issue(kb, 0, S, ldk, kring);
+  kdma.issue(kb, F::BK, S, ldk, kring + KT::kBytes);
 
   bf16x8 qf[RB][KS];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     if (neg_q)
-      load_row_frags<bf16, D, true, true>(qf[rb], qb, q0w + 32 * rb, S, d);
+      load_row_frags<bf16, D, true, true>(qf[rb], qb, q0w + 32 * rb, S, d, ldq);
     else
-      load_row_frags<bf16, D, true, false>(qf[rb], qb, q0w + 32 * rb, S, d);
+      load_row_frags<bf16, D, true, false>(qf[rb], qb, q0w + 32 * rb, S, d, ldq);
   }
 
   const int kbase = KT::off(l32, g * 16);
@@ -967,9 +985,9 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
   // nothing and write zeros into a slot nobody reads again.
   auto dma_part = [&](int j, int qd) {
     if (qd < F::kDma)
-      kdma.issue_one(kb, (j + 3) * F::BK, S, d, kring + ((j + 3) % F::kSlots) * KT::kBytes, qd);
+      kdma.issue_one(kb, (j + 3) * F::BK, S, ldk, kring + ((j + 3) % F::kSlots) * KT::kBytes, qd);
     else
-      vdma.issue_one(vb, (j + 1) * F::BK, S, d, vring + ((j + 1) % F::kSlots) * VT::kBytes, qd - F::kDma);
+      vdma.issue_one(vb, (j + 1) * F::BK, S, ldv, vring + ((j + 1) % F::kSlots) * VT::kBytes, qd - F::kDma);
   };
   auto dma = [&](int j) {
 #pragma unroll
@@ -1176,7 +1194,7 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
   for (int rb = 0; rb < RB; ++rb) {
     const int row = q0w + 32 * rb + l32;
     const float l = lane32_sum(lsum[rb]);
-    store_acc_rows<bf16, D, true>(acc[rb], o + (int64_t)bh * S * d, row, S, d, 1.0f / l);
+    store_acc_rows<bf16, D, true>(acc[rb], o + vw.o.at(bh, vw.heads), row, S, d, 1.0f / l, vw.o.r);
     if (g == 0 && row < S) lse[(int64_t)bh * S + row] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
   }
 }
@@ -1579,13 +1597,14 @@ __device__ __forceinline__ void stat_dma(const float* base, int r0, int nrows, c
 // workgroup barrier per 64-query tile (at odd half-steps); the DMA of tile
 // t + 3 goes out during the two half-steps after the barrier that frees its
 // slot.
-template <int D>
+// SAMEP: Q and dO share a row pitch (dense tensors), so one DMA descriptor serves both.
+template <int D, bool SAMEP = true>
 __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                             const bf16* __restrict__ v, const bf16* __restrict__ dout,
                                                             const float* __restrict__ lse,
                                                             const float* __restrict__ delta, bf16* __restrict__ dk,
                                                             bf16* __restrict__ dv, int bh_count, int Sq, int Sk, int d,
-                                                            int causal, float scale, float scale_log2) {
+                                                            int causal, float scale, float scale_log2, AttnViews vw) {
   typedef DkvPp<D> F;
   typedef typename F::Tile Tile;
   constexpr int KS = F::KS, DT = F::DT;
@@ -1605,10 +1624,12 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
   const int k0w = k0 + 32 * wave;
   const int kvrow = k0w + l32;
 
-  const bf16* qb = q + (int64_t)bh * Sq * d;
-  const bf16* dob = dout + (int64_t)bh * Sq * d;
-  const bf16* kb = k + (int64_t)bh * Sk * d;
-  const bf16* vb = v + (int64_t)bh * Sk * d;
+  // Row pitches (elements; d for dense tensors).
+  const int ldq = (int)vw.q.r, lddo = (int)vw.dout.r;
+  const bf16* qb = q + vw.q.at(bh, vw.heads);
+  const bf16* dob = dout + vw.dout.at(bh, vw.heads);
+  const bf16* kb = k + vw.k.at(bh, vw.heads);
+  const bf16* vb = v + vw.v.at(bh, vw.heads);
   const float* lseb = lse + (int64_t)bh * Sq;
   const float* db = delta + (int64_t)bh * Sq;
 
@@ -1619,10 +1640,11 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
   const int nh = 2 * nt;
 
   bf16x8 kf[KS], vf[KS];
-  load_row_frags<bf16, D, true, false>(kf, kb, k0w, Sk, d);
-  load_row_frags<bf16, D, true, false>(vf, vb, k0w, Sk, d);
+  load_row_frags<bf16, D, true, false>(kf, kb, k0w, Sk, d, (int)vw.k.r);
+  load_row_frags<bf16, D, true, false>(vf, vb, k0w, Sk, d, (int)vw.v.r);
 
-  const PpDma<Tile, true> dma(wave, d);
+  const PpDma<Tile, true> dma(wave, ldq);
+  const PpDma<Tile, true> dma_do(wave, SAMEP ? ldq : lddo);
   auto slot = [&](int t) { return smem + (t % F::kSlots) * F::kSlotBytes; };
   // DMA instruction qd of tile t. Tiles past the end have an empty buffer
   // range: they read nothing and write zeros into a slot nobody reads again.
@@ -1630,9 +1652,9 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
     char* sl = slot(t);
     const int r0 = (first + t) * F::BQ;
     if (qd < F::kDma)
-      dma.issue_one(qb, r0, Sq, d, sl, qd);
+      dma.issue_one(qb, r0, Sq, ldq, sl, qd);
     else if (qd < 2 * F::kDma)
-      dma.issue_one(dob, r0, Sq, d, sl + Tile::kBytes, qd - F::kDma);
+      (SAMEP ? dma : dma_do).issue_one(dob, r0, Sq, SAMEP ? ldq : lddo, sl + Tile::kBytes, qd - F::kDma);
     else if (qd == 2 * F::kDma)
       stat_dma(lseb, r0, Sq, sl + 2 * Tile::kBytes);
     else
@@ -1835,8 +1857,8 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
   wait_vmem<0>();
 
   if (k0w >= Sk) return;
-  store_acc_rows<bf16, D, true>(dka, dk + (int64_t)bh * Sk * d, kvrow, Sk, d, scale);
-  store_acc_rows<bf16, D, true>(dva, dv + (int64_t)bh * Sk * d, kvrow, Sk, d, 1.0f);
+  store_acc_rows<bf16, D, true>(dka, dk + vw.dk.at(bh, vw.heads), kvrow, Sk, d, scale, vw.dk.r);
+  store_acc_rows<bf16, D, true>(dva, dv + vw.dv.at(bh, vw.heads), kvrow, Sk, d, 1.0f, vw.dv.r);
 }
 
 // W waves of 32 queries; SLOTS K/V tile slots in LDS (3: tiles t + 1 and t + 2
@@ -1875,7 +1897,8 @@ __global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __r
                                                                 float* __restrict__ delta,
                                                                 bf16* __restrict__ dq, int bh_count, int Sq, int Sk,
                                                                 int d, int causal, float scale, float scale_log2,
-                                                                int n_qtiles, const bf16* __restrict__ o) {
+                                                                int n_qtiles, const bf16* __restrict__ o,
+                                                                AttnViews vw) {
   typedef DqPp<D, W, SLOTS> F;
   typedef typename F::Tile Tile;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -1893,27 +1916,29 @@ __global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __r
   const int q0w = q0 + 32 * (W == 8 ? 2 * (wave & 3) + (wave >> 2) : wave);
   const int qrow = q0w + l32;
 
-  const bf16* qb = q + (int64_t)bh * Sq * d;
-  const bf16* dob = dout + (int64_t)bh * Sq * d;
-  const bf16* kb = k + (int64_t)bh * Sk * d;
-  const bf16* vb = v + (int64_t)bh * Sk * d;
+  // Row pitches (elements; d for dense tensors). K and V share one (the host checks).
+  const int ldk = (int)vw.k.r;
+  const bf16* qb = q + vw.q.at(bh, vw.heads);
+  const bf16* dob = dout + vw.dout.at(bh, vw.heads);
+  const bf16* kb = k + vw.k.at(bh, vw.heads);
+  const bf16* vb = v + vw.v.at(bh, vw.heads);
 
   const int q_last = min(q0 + F::BQ, Sq) - 1;
   const int n = causal ? min(q_last, Sk - 1) / F::BK + 1 : (Sk + F::BK - 1) / F::BK;
   const bool wave_active = q0w < Sq;
   const int n_w = !wave_active ? 0 : causal ? min(min(q0w + 31, Sq - 1), Sk - 1) / F::BK + 1 : n;
 
-  const PpDma<Tile, true, W> dma(wave, d);
+  const PpDma<Tile, true, W> dma(wave, ldk);
   auto slot = [&](int t) { return smem + (t % F::kSlots) * F::kSlotBytes; };
   auto issue_tile = [&](int t) {
     char* sl = slot(t);
-    dma.issue(kb, t * F::BK, Sk, d, sl);
-    dma.issue(vb, t * F::BK, Sk, d, sl + Tile::kBytes);
+    dma.issue(kb, t * F::BK, Sk, ldk, sl);
+    dma.issue(vb, t * F::BK, Sk, ldk, sl + Tile::kBytes);
   };
 
   bf16x8 qf[F::KS], dof[F::KS];
-  load_row_frags<bf16, D, true, false>(qf, qb, q0w, Sq, d);
-  load_row_frags<bf16, D, true, false>(dof, dob, q0w, Sq, d);
+  load_row_frags<bf16, D, true, false>(qf, qb, q0w, Sq, d, (int)vw.q.r);
+  load_row_frags<bf16, D, true, false>(dof, dob, q0w, Sq, d, (int)vw.dout.r);
   const bool qok = qrow < Sq;
   const float nlse2 = qok ? -lse[(int64_t)bh * Sq + qrow] * kLog2e : 0.f;
   float dl;
@@ -1921,7 +1946,7 @@ __global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __r
     // delta = sum_d f32(dO) f32(O) (flash_attention.py:328-329): this lane
     // holds half of its row's elements, lane ^ 32 the other half.
     bf16x8 of[F::KS];
-    load_row_frags<bf16, D, true, false>(of, o + (int64_t)bh * Sq * d, q0w, Sq, d);
+    load_row_frags<bf16, D, true, false>(of, o + vw.o.at(bh, vw.heads), q0w, Sq, d, (int)vw.o.r);
     float part = 0.f;
 #pragma unroll
     for (int kk = 0; kk < F::KS; ++kk)
@@ -2054,7 +2079,7 @@ __global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __r
   }
 
   if (!wave_active) return;
-  store_acc_rows<bf16, D, true>(acc, dq + (int64_t)bh * Sq * d, qrow, Sq, d, scale);
+  store_acc_rows<bf16, D, true>(acc, dq + vw.dq.at(bh, vw.heads), qrow, Sq, d, scale, vw.dq.r);
 }
 
 // ===========================================================================
@@ -2095,9 +2120,15 @@ int check_shape(const char* name, const Shape& s, int dtype, int causal, bool bw
 
 int pad_dim(int64_t d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
 
+// Strides of dense [B, H, Sq, d] (q, o, dO, dQ) and [B, H, Sk, d] (k, v, dK, dV) tensors.
+AttnViews dense_views(const Shape& s) {
+  const View vq{s.h * s.sq * s.d, s.sq * s.d, s.d}, vk{s.h * s.sk * s.d, s.sk * s.d, s.d};
+  return AttnViews{vq, vk, vk, vq, vq, vq, vk, vk, (int)s.h};
+}
+
 template <int D, int RB = 1, int W = 8, bool ZIG = false>
 int fwd_sw_launch(const void* q, const void* k, const void* v, void* o, float* lse, const Shape& s, float c, int neg_q,
-                  hipStream_t stream) {
+                  hipStream_t stream, const AttnViews* views = nullptr) {
   typedef FwdW<D, RB, W> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
@@ -2106,7 +2137,7 @@ int fwd_sw_launch(const void* q, const void* k, const void* v, void* o, float* l
   set_lds(kern, F::kLds);
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<bf16*>(o), lse, (int)bh,
-                     (int)s.sq, (int)s.d, c, neg_q, (int)nq);
+                     (int)s.sq, (int)s.d, c, neg_q, (int)nq, views ? *views : dense_views(s));
   return check_launch("ferrite_flash_attention_fwd");
 }
 
@@ -2167,7 +2198,8 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
 // o == nullptr: read delta; otherwise compute it from o and dout and write it.
 template <int D, int W, int SLOTS, bool ZIG>
 int dq_pp_launch_t(const void* q, const void* k, const void* v, const void* dout, const float* lse, float* delta,
-                   void* dq, const Shape& s, int causal, float scale, hipStream_t stream, const void* o) {
+                   void* dq, const Shape& s, int causal, float scale, hipStream_t stream, const void* o,
+                   const AttnViews& vw) {
   typedef DqPp<D, W, SLOTS> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
@@ -2177,23 +2209,25 @@ int dq_pp_launch_t(const void* q, const void* k, const void* v, const void* dout
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
                      delta, static_cast<bf16*>(dq), (int)bh, (int)s.sq, (int)s.sk, (int)s.d, causal, scale,
-                     scale * kLog2e, (int)nq, static_cast<const bf16*>(o));
+                     scale * kLog2e, (int)nq, static_cast<const bf16*>(o), vw);
   return check_launch("ferrite_flash_attention_bwd_dq");
 }
 
 template <int D>
 int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, float* delta,
-                 void* dq, const Shape& s, int causal, float scale, hipStream_t stream, const void* o = nullptr) {
+                 void* dq, const Shape& s, int causal, float scale, hipStream_t stream, const void* o = nullptr,
+                 const AttnViews* views = nullptr) {
+  const AttnViews vw = views ? *views : dense_views(s);
   if constexpr (D == 64) {
     // 128-query workgroups of 4 waves with two LDS slots (67 KB): two share a
     // CU. A grid resident all at once (the long-context case) pairs long and
     // short causal sweeps on each CU.
     typedef DqPp<64, 4, 2> F4;
     const bool one_round = causal && cdiv(s.sq, F4::BQ) * s.b * s.h <= 2 * (int64_t)cu_count();
-    return one_round ? dq_pp_launch_t<D, 4, 2, true>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o)
-                     : dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o);
+    return one_round ? dq_pp_launch_t<D, 4, 2, true>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw)
+                     : dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
   } else {
-    return dq_pp_launch_t<D, 8, 3, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o);
+    return dq_pp_launch_t<D, 8, 3, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
   }
 }
 
@@ -2216,17 +2250,19 @@ int dq_launch(const void* q, const void* k, const void* v, const void* dout, con
 
 template <int D>
 int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
-                  void* dk, void* dv, const Shape& s, int causal, float scale, hipStream_t stream) {
+                  void* dk, void* dv, const Shape& s, int causal, float scale, hipStream_t stream,
+                  const AttnViews* views = nullptr) {
   typedef DkvPp<D> F;
   const int64_t nk = cdiv(s.sk, F::BKV);
   const int64_t bh = s.b * s.h;
   if (nk * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dkv: grid too large");
-  auto kern = attn_dkv_sw_kernel<D>;
+  const AttnViews vw = views ? *views : dense_views(s);
+  auto kern = vw.q.r == vw.dout.r ? attn_dkv_sw_kernel<D, true> : attn_dkv_sw_kernel<D, false>;
   set_lds(kern, F::kLds);
   hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
                      delta, static_cast<bf16*>(dk), static_cast<bf16*>(dv), (int)bh, (int)s.sq, (int)s.sk, (int)s.d,
-                     causal, scale, scale * kLog2e);
+                     causal, scale, scale * kLog2e, vw);
   return check_launch("ferrite_flash_attention_bwd_dkv");
 }
 
@@ -2325,6 +2361,76 @@ extern "C" int ferrite_hip_attn_bwd_dkv(const void* q, const void* k, const void
   return fail(FERRITE_ERR_INVALID_ARGUMENT, "unreachable head_dim")
   FERRITE_DISPATCH(dkv_launch, s, dtype, al, q, k, v, dout, lse, delta, dk, dv, s, causal, scale, st);
 #undef FERRITE_DISPATCH_256
+}
+
+namespace ferrite {
+namespace {
+
+// q, k, v heads inside a token-major [B, S, 3, H, d] projection, and O / dO as
+// token-major [B, S, H, d] (the layouts either side of model/gpt.py:137-138).
+AttnViews packed_views(int64_t b, int64_t s, int64_t h, int64_t d) {
+  const View vqkv{s * 3 * h * d, d, 3 * h * d}, vo{s * h * d, d, h * d};
+  return AttnViews{vqkv, vqkv, vqkv, vo, vo, vqkv, vqkv, vqkv, (int)h};
+}
+
+int check_packed(const char* name, int64_t b, int64_t s, int64_t h, int64_t d) {
+  if (b < 1 || s < 1 || h < 1 || (d != 64 && d != 128))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": need b, s, h >= 1 and head_dim 64 or 128");
+  if (s % 64 != 0) return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": need seq % 64 == 0");
+  if (s * 3 * h * d * 2 >= 0x7fffffff || b * h > 0x7fffffff)
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": a sequence spans over 2 GiB");
+  return FERRITE_OK;
+}
+
+}  // namespace
+}  // namespace ferrite
+
+extern "C" int ferrite_hip_attn_fwd_qkv(const void* qkv, void* o, float* lse, int64_t b, int64_t s, int64_t h,
+                                        int64_t d, float scale, void* stream) {
+  const char* name = "ferrite_hip_attn_fwd_qkv";
+  if (int rc = check_packed(name, b, s, h, d)) return rc;
+  if (!qkv || !o || !lse) return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": null pointer");
+  if (!aligned16(qkv) || !aligned16(o))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": qkv and o must be 16-byte aligned");
+  const Shape sh{b, h, s, s, d};
+  const AttnViews vw = packed_views(b, s, h, d);
+  const bf16* base = static_cast<const bf16*>(qkv);
+  const bf16 *q = base, *k = base + h * d, *v = base + 2 * h * d;
+  float c = scale * kLog2e;
+  const int neg_q = c < 0.f;
+  c = fmaxf(fabsf(c), 1e-30f);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d == 64) {
+    typedef FwdW<64, 1, 4> F4;
+    const bool one_round = cdiv(s, F4::BQ) * b * h <= 2 * (int64_t)cu_count();
+    return one_round ? fwd_sw_launch<64, 1, 4, true>(q, k, v, o, lse, sh, c, neg_q, st, &vw)
+                     : fwd_sw_launch<64, 1, 4, false>(q, k, v, o, lse, sh, c, neg_q, st, &vw);
+  }
+  return fwd_sw_launch<128>(q, k, v, o, lse, sh, c, neg_q, st, &vw);
+}
+
+extern "C" int ferrite_hip_attn_bwd_qkv(const void* qkv, const void* o, const void* dout, const float* lse,
+                                        float* delta, void* dqkv, int64_t b, int64_t s, int64_t h, int64_t d,
+                                        float scale, void* stream) {
+  const char* name = "ferrite_hip_attn_bwd_qkv";
+  if (int rc = check_packed(name, b, s, h, d)) return rc;
+  if (!qkv || !o || !dout || !lse || !delta || !dqkv)
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": null pointer");
+  if (!aligned16(qkv) || !aligned16(o) || !aligned16(dout) || !aligned16(dqkv))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": tensors must be 16-byte aligned");
+  const Shape sh{b, h, s, s, d};
+  const AttnViews vw = packed_views(b, s, h, d);
+  const bf16* base = static_cast<const bf16*>(qkv);
+  const bf16 *q = base, *k = base + h * d, *v = base + 2 * h * d;
+  bf16* gbase = static_cast<bf16*>(dqkv);
+  bf16 *dq = gbase, *dk = gbase + h * d, *dv = gbase + 2 * h * d;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // dQ computes delta from O and dO and writes it; dK/dV then reads it.
+  int rc = d == 64 ? dq_pp_launch<64>(q, k, v, dout, lse, delta, dq, sh, 1, scale, st, o, &vw)
+                   : dq_pp_launch<128>(q, k, v, dout, lse, delta, dq, sh, 1, scale, st, o, &vw);
+  if (rc) return rc;
+  return d == 64 ? dkv_pp_launch<64>(q, k, v, dout, lse, delta, dk, dv, sh, 1, scale, st, &vw)
+                 : dkv_pp_launch<128>(q, k, v, dout, lse, delta, dk, dv, sh, 1, scale, st, &vw);
 }
 
 extern "C" int ferrite_hip_attn_bwd_dq_delta(const void* q, const void* k, const void* v, const void* o,

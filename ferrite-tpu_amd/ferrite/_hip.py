@@ -77,6 +77,11 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp, _c_i64, _vp],
     ),
+    "ferrite_hip_attn_fwd_qkv": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _vp]),
+    "ferrite_hip_attn_bwd_qkv": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _vp],
+    ),
     "ferrite_hip_attn_bwd_dq_delta": (
         _c_int,
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f32, _vp],

@@ -200,6 +200,62 @@ def flash_attention(q, k, v, *, causal: bool = True, scale: float | None = None,
     return _Flash.apply(q, k, v, bool(causal), float(scale), bs)
 
 
+class _FlashQKV(torch.autograd.Function):
+    """Causal attention on the token-major projection [B, S, 3, H, D] -> [B, S, H, D], the
+    head transposes of model/gpt.py:137-138 folded into the kernels' addressing."""
+
+    @staticmethod
+    def forward(ctx, qkv, heads, scale):
+        b, s, three, h, d = qkv.shape
+        o = torch.empty((b, s, h, d), dtype=qkv.dtype, device=qkv.device)
+        lse = torch.empty((b, h, s), dtype=torch.float32, device=qkv.device)
+        rc = _hip.lib().ferrite_hip_attn_fwd_qkv(qkv.data_ptr(), o.data_ptr(), lse.data_ptr(), b, s, h, d,
+                                                 float(scale), _hip.stream_of(qkv))
+        _hip.check(rc, "ferrite_flash_attention_fwd")
+        ctx.save_for_backward(qkv, o, lse)
+        ctx.scale = scale
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        qkv, o, lse = ctx.saved_tensors
+        b, s, _, h, d = qkv.shape
+        do = do.to(o.dtype).contiguous()
+        dqkv = torch.empty_like(qkv)
+        delta = torch.empty((b, h, s), dtype=torch.float32, device=qkv.device)
+        rc = _hip.lib().ferrite_hip_attn_bwd_qkv(qkv.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(),
+                                                 delta.data_ptr(), dqkv.data_ptr(), b, s, h, d, float(ctx.scale),
+                                                 _hip.stream_of(qkv))
+        _hip.check(rc, "ferrite_flash_attention_bwd")
+        return dqkv, None, None
+
+
+def flash_attention_qkv_supported(qkv, heads: int) -> bool:
+    """Whether flash_attention_qkv takes this projection: bf16 on the GPU, head_dim 64 or 128,
+    sequence length a multiple of 64."""
+    if qkv.ndim != 3 or qkv.shape[-1] % (3 * heads):
+        return False
+    d = qkv.shape[-1] // (3 * heads)
+    return qkv.dtype == torch.bfloat16 and qkv.is_cuda and d in (64, 128) and qkv.shape[1] % 64 == 0
+
+
+def flash_attention_qkv(qkv, heads: int, *, scale: float | None = None):
+    """Causal ``softmax(q k^T * scale) v`` for the fused projection ``qkv: [B, S, 3 * H * D]``
+    (columns ordered (q|k|v, head, dim), as model/gpt.py:136-137 splits them), returning
+    ``[B, S, H * D]`` in the token-major order the output projection reads (gpt.py:138).
+    Differentiable; the same kernels and numbers as flash_attention on transposed copies,
+    without the copies. bf16, head_dim 64 or 128, sequence length a multiple of 64."""
+    if not flash_attention_qkv_supported(qkv, heads):
+        raise ValueError(f"flash_attention_qkv needs bf16 [B, S, 3*H*D] on the GPU with D in (64, 128) and S % 64 == 0; "
+                         f"got {tuple(qkv.shape)} {qkv.dtype} for {heads} heads")
+    b, s, c = qkv.shape
+    d = c // (3 * heads)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    o = _FlashQKV.apply(qkv.contiguous().view(b, s, 3, heads, d), heads, float(scale))
+    return o.view(b, s, heads * d)
+
+
 def flash_attention_reference(q, k, v, *, causal: bool = True, scale: float | None = None):
     """Materialised-scores attention in f32 with torch ops (the reference's XLA route,
     flash_attention.py:370-380). Not used by the HIP path."""

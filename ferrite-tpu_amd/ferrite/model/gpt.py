@@ -29,7 +29,8 @@ import torch
 import torch.nn.functional as F
 
 from ferrite import platform
-from ferrite.kernels.flash_attention import BlockSizes, flash_attention, flash_attention_reference
+from ferrite.kernels.flash_attention import (BlockSizes, flash_attention, flash_attention_qkv,
+                                            flash_attention_qkv_supported, flash_attention_reference)
 from ferrite.kernels.heads import merge_heads, split_heads
 from ferrite.kernels.matmul import matmul, mlp_gelu
 from ferrite.kernels.rmsnorm import rmsnorm, rmsnorm_reference
@@ -196,6 +197,17 @@ def _attention(q, k, v, cfg: GPTConfig):
     return flash_attention_reference(q, k, v, causal=True)
 
 
+def _attention_block(qkv, cfg: GPTConfig):
+    """[B, S, 3d] projection -> [B, S, d] attention output (gpt.py:136-138). The kernel route
+    reads the heads where the projection left them and writes the output token-major
+    (flash_attention_qkv) when the shape allows; otherwise heads are split, attended and merged."""
+    if (cfg.attention == "pallas" and cfg.attention_blocks(qkv.shape[1]) is not None
+            and flash_attention_qkv_supported(qkv, cfg.n_head)):
+        return flash_attention_qkv(qkv, cfg.n_head)
+    q, k, v = _split_heads(qkv, cfg)  # [B, H, S, hd] each
+    return _merge_heads(_attention(q, k, v, cfg), cfg)
+
+
 def _split_heads(qkv, cfg: GPTConfig):
     """[B, S, 3d] -> q, k, v as dense [B, H, S, hd] (gpt.py:137). The kernel route moves them
     with the HIP layout kernel; the torch route permutes."""
@@ -290,9 +302,7 @@ def _trunk(params, tokens, cfg: GPTConfig):
         else:
             h, y = _norm(pending, layer["ln1"], h, cfg)
         qkv = _linear(y, layer["wqkv"], cfg)  # [B, S, 3 * d]: rows (q|k|v, head, hd)
-        q, k, v = _split_heads(qkv, cfg)  # [B, H, S, hd] each
-        a = _merge_heads(_attention(q, k, v, cfg), cfg)  # [B, S, d]
-        a = _linear(a, layer["wo"], cfg)
+        a = _linear(_attention_block(qkv, cfg), layer["wo"], cfg)  # [B, S, d] in, [B, S, d] out
         h, y2 = _norm(a, layer["ln2"], h, cfg)
         pending = _mlp(y2, layer, cfg)
     _, y = _norm(pending, params["ln_f"], h, cfg)

@@ -22,6 +22,9 @@
  *   ferrite_hip_attn_bwd_dq   flash_attention.py:224-243, :281-306 ("ferrite_flash_attention_bwd_dq")
  *   ferrite_hip_attn_bwd_dq_delta  the same dQ with delta (flash_attention.py:328-329)
  *                                  computed inside it and written out for dK/dV
+ *   ferrite_hip_attn_fwd_qkv / _bwd_qkv  the causal forward and backward read and
+ *                                  written in the model's token-major layouts, with the
+ *                                  head transposes of model/gpt.py:137-138 folded in
  *   ferrite_hip_add_rmsnorm   rmsnorm.py:52-56, :77-110  ("ferrite_add_rmsnorm")
  *   ferrite_hip_rmsnorm       rmsnorm.py:46-49, :77-110  ("ferrite_rmsnorm")
  *   ferrite_hip_rmsnorm_bwd   rmsnorm.py:159-166, :128-131, :148-153 (the custom_vjp backward of
@@ -250,6 +253,26 @@ int ferrite_hip_attn_bwd_dq(const void* q, const void* k, const void* v, const v
 int ferrite_hip_attn_bwd_dq_delta(const void* q, const void* k, const void* v, const void* o, const void* dout,
                                   const float* lse, float* delta, void* dq, int64_t b, int64_t h, int64_t sq,
                                   int64_t sk, int64_t d, int dtype, int causal, float scale, void* stream);
+
+/*
+ * Causal flash attention on the model's token-major layouts (model/gpt.py:136-138:
+ * the fused projection reshaped to [B, S, 3, H, D], heads transposed in and out
+ * around flash_attention). qkv: bf16 [B, S, 3, H, D] (q, k, v of head h at
+ * [.., 0, h, :], [.., 1, h, :], [.., 2, h, :]); o: bf16 [B, S, H, D]; lse: f32
+ * [B, H, S]. The kernels read the heads and write O in place, so no transposed
+ * copies exist. Needs D of 64 or 128, S % 64 == 0 and 16-byte aligned tensors;
+ * the numbers are bitwise those of ferrite_hip_attn_fwd on transposed copies.
+ */
+int ferrite_hip_attn_fwd_qkv(const void* qkv, void* o, float* lse, int64_t b, int64_t s, int64_t h, int64_t d,
+                             float scale, void* stream);
+
+/*
+ * Its backward: dout bf16 [B, S, H, D]; delta f32 [B, H, S] is an output (computed
+ * inside dQ, then read by dK/dV); dqkv bf16 [B, S, 3, H, D] receives dQ, dK, dV in
+ * the projection's layout. Bitwise ferrite_hip_attn_bwd_dq_delta + _dkv on copies.
+ */
+int ferrite_hip_attn_bwd_qkv(const void* qkv, const void* o, const void* dout, const float* lse, float* delta,
+                             void* dqkv, int64_t b, int64_t s, int64_t h, int64_t d, float scale, void* stream);
 
 #ifdef __cplusplus
 }

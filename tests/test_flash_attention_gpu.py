@@ -281,3 +281,42 @@ def test_kernels_are_race_free(dev, dtype):
     for later in runs[1:]:
         for a, c in zip(runs[0], later):
             assert torch.equal(a, c)
+
+
+@pytest.mark.parametrize("b,s,h,d", [
+    (8, 1024, 12, 64),    # the GPT train step's attention
+    (2, 256, 4, 64),      # a grid resident at once (paired long/short sweeps)
+    (1, 384, 2, 128),     # D = 128, a partial 256-row query tile
+])
+def test_packed_qkv_matches_split_heads(dev, b, s, h, d):
+    """flash_attention_qkv reads q, k, v inside the fused projection [B, S, 3, H, D] and writes
+    O as [B, S, H, D] (model/gpt.py:136-138 without the transposed copies). Same kernels, same
+    arithmetic: output and the projection's gradient are bitwise those of splitting the heads,
+    flash_attention, and merging them back."""
+    from ferrite.kernels.flash_attention import flash_attention_qkv
+    from ferrite.kernels.heads import merge_heads, split_heads
+
+    qkv0 = to_dev(normal(120 + s, (b, s, 3 * h * d), "bf16"), "bf16", dev)
+    g = to_dev(normal(121 + s, (b, s, h * d), "bf16"), "bf16", dev)
+    a = qkv0.clone().requires_grad_()
+    out_a = flash_attention_qkv(a, h)
+    out_a.backward(g)
+    bq = qkv0.clone().requires_grad_()
+    q, k, v = split_heads(bq, 3, h)
+    out_b = merge_heads(flash_attention(q, k, v, causal=True))
+    out_b.backward(g)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b)
+    assert torch.equal(a.grad, bq.grad)
+
+
+def test_packed_qkv_argument_errors(dev):
+    lib = _hip.lib()
+    x = torch.zeros(1, 64, 3, 2, 96, device=dev, dtype=torch.bfloat16)
+    o = torch.zeros(1, 64, 2, 96, device=dev, dtype=torch.bfloat16)
+    lse = torch.zeros(1, 2, 64, device=dev)
+    st = _hip.stream_of(x)
+    assert lib.ferrite_hip_attn_fwd_qkv(x.data_ptr(), o.data_ptr(), lse.data_ptr(), 1, 64, 2, 96, 0.1, st) == 1
+    assert "head_dim" in _hip.last_error()
+    assert lib.ferrite_hip_attn_fwd_qkv(x.data_ptr(), o.data_ptr(), lse.data_ptr(), 1, 60, 2, 64, 0.1, st) == 1
+    assert "seq" in _hip.last_error()
