@@ -1,0 +1,39 @@
+"""The bench.py contract that needs no GPU: more than one GPU is refused with a message and exit
+code 2 (this build measures one GPU), and the committed traffic table that feeds the roofline's
+`traffic` field parses into plausible byte counts."""
+
+import json
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_world_size_above_one_is_refused():
+    env = dict(os.environ, WORLD_SIZE="4")
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py")], capture_output=True, text=True, env=env,
+                       timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_traffic_table_feeds_the_roofline():
+    sys.path.insert(0, ROOT)
+    import bench
+
+    for kernel in ("attn_fwd", "add_rmsnorm"):
+        t = bench._traffic(kernel)
+        assert t is not None and t > 0
+    # the forward's algorithmic bytes: q, k, v read and O written (4 B H S D 2) plus lse (4 B H S)
+    alg = 4 * 4 * 16 * 2048 * 128 * 2 + 4 * 16 * 2048 * 4
+    assert 1.0 <= bench._traffic("attn_fwd") / alg < 2.0
+    roof = bench._roofline("mfma", 900.0, bench.PEAK_BF16_TFLOPS, "TFLOP/s", bench._traffic("attn_fwd"))
+    assert roof["bound"] == "mfma" and abs(roof["frac"] - 900.0 / 2516.6) < 1e-3
+    json.dumps(roof)
