@@ -224,17 +224,21 @@ def test_vjp_reads_transposes_in_place(dev, m, k, n):
         assert np.all(np.abs(g64 - ex) <= bf16_ulp(ex) + 2.0**-20 * absb + 1e-30)
 
 
-def test_four_wave_tiles_match_eight_wave_tiles(dev):
+@pytest.mark.parametrize("x_t,y_t", [(False, False), (True, False), (False, True)])
+def test_four_wave_tiles_match_eight_wave_tiles(dev, x_t, y_t):
     """An 8192 x 8192 output has four rounds of 256 x 256 tiles and runs on four waves per tile; a
     2048 x 8192 one (one round) on eight. Both accumulate every output over the same 64-deep k
-    steps in the same order, so the first 2048 rows agree bitwise; the whole product is also held
-    to the bf16 bar on sampled rows against the f64 product of the same values."""
+    steps in the same order, so the first 2048 rows agree bitwise, with either operand read
+    transposed in place; the whole product is also held to the bf16 bar on sampled rows against
+    the f64 product of the same values."""
     k = 256
     a = normal(95, (8192, k), "bf16")
     b = normal(96, (k, 8192), "bf16")
-    xs, ys = to_dev(a, "bf16", dev), to_dev(b, "bf16", dev)
-    big, _ = _mm_ex(xs, ys, 8192, 8192, k, False, False, torch.bfloat16)
-    top, _ = _mm_ex(xs[:2048].contiguous(), ys, 2048, 8192, k, False, False, torch.bfloat16)
+    xs = to_dev(a.T.copy() if x_t else a, "bf16", dev)
+    ys = to_dev(b.T.copy() if y_t else b, "bf16", dev)
+    big, _ = _mm_ex(xs, ys, 8192, 8192, k, x_t, y_t, torch.bfloat16)
+    x_top = xs[:, :2048].contiguous() if x_t else xs[:2048].contiguous()
+    top, _ = _mm_ex(x_top, ys, 2048, 8192, k, x_t, y_t, torch.bfloat16)
     assert torch.equal(big[:2048], top)
     rows = np.arange(0, 8192, 97)
     exact = a[rows].astype(np.float64) @ b.astype(np.float64)
