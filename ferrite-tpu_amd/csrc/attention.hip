@@ -1635,8 +1635,16 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
 
   // Query tiles first .. first + nt - 1 (tile t in ring slot t % kSlots),
   // halves 0 .. nh - 1 (half x: tile x / 2, queries 32 (x % 2) .. of it).
+  // At D = 128 a sweep of fewer than three tiles is run as three: the tiles
+  // past the end of the queries arrive as zeros (Q, dO, lse and delta all 0),
+  // so their p = exp2(0) = 1 meets dO = 0 in dV and dS = p (0 - 0) = 0 in dK,
+  // and they add exact zeros. One code path for every length keeps the
+  // register allocation of the pipeline from splitting over the short cases,
+  // which cost 38 spilled registers there. D = 64 has registers to spare and
+  // keeps separate short paths (the padded form measured 2-3% slower).
+  constexpr bool kShortPaths = D != 128;
   const int first = causal ? k0 / F::BQ : 0;
-  const int nt = (Sq + F::BQ - 1) / F::BQ - first;
+  const int nt = max((Sq + F::BQ - 1) / F::BQ - first, kShortPaths ? 1 : 3);
   const int nh = 2 * nt;
 
   bf16x8 kf[KS], vf[KS];
@@ -1822,29 +1830,28 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
     lds_barrier();
   };
   // Half-step h: SDP for h + 1 < nh, SG for 0 <= h < nh, GRAD for 1 <= h <= nh
-  // (nh is even and >= 2). The causal mask can only touch halves 0 .. 3 of
+  // (nh is even, >= 2, and >= 6 without the short paths). The causal mask can only touch halves 0 .. 3 of
   // the sweep (the diagonal block): the first half-steps apply it on every
   // wave, where it is a no-op for halves below the wave's keys.
   sync_tile();
   stage(P1(), T_(), F_(), F_(), F_(), -1);
   stage(P0(), T_(), T_(), T_(), F_(), 0);
   sync_tile();
-  if (nh == 2) {
+  if (kShortPaths && nh == 2) {
     stage(P1(), F_(), T_(), T_(), T_(), 1);
     stage(P0(), F_(), F_(), F_(), T_(), 2);
   } else {
     stage(P1(), T_(), T_(), T_(), T_(), 1);
     stage(P0(), T_(), T_(), T_(), T_(), 2);
     sync_tile();
-    if (nh == 4) {
+    if (kShortPaths && nh == 4) {
       stage(P1(), F_(), T_(), T_(), T_(), 3);
       stage(P0(), F_(), F_(), F_(), T_(), 4);
     } else {
       stage(P1(), T_(), T_(), T_(), T_(), 3);
       stage(P0(), T_(), T_(), F_(), T_(), 4);
       // Full, unmasked half-steps in pairs, then the last two.
-      int h = 5;
-      for (; h + 1 <= nh - 2; h += 2) {
+      for (int h = 5; h + 1 <= nh - 2; h += 2) {
         sync_tile();
         stage(P1(), T_(), T_(), F_(), T_(), h);
         stage(P0(), T_(), T_(), F_(), T_(), h + 1);
