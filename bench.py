@@ -90,9 +90,13 @@ def _traffic(kernel: str):
     return None
 
 
-def _roofline(bound: str, achieved: float, peak: float, unit: str, traffic):
-    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": traffic}
+def _roofline(name: str, flops: float, nbytes: float, seconds: float, precision: str = "bf16", traffic=None) -> dict:
+    """The bench line's roofline object for one launch (ferrite.profiling.roofline at MI355X peaks)."""
+    from ferrite import platform
+    from ferrite.profiling.roofline import analyze
+
+    return analyze(name, flops, nbytes, seconds, peaks=platform.MI355X, precision=precision,
+                   traffic=traffic).bench_fields()
 
 
 def bench_attention(b, h, t, d, steps, warmup, seed=7):
@@ -157,7 +161,7 @@ def bench_attention(b, h, t, d, steps, warmup, seed=7):
         "fwd_bwd_tflops": (f_fwd + f_bwd) / (t_fwd + t_bwd) / 1e12,
         "fwd_frac_bf16_peak": f_fwd / t_fwd / 1e12 / PEAK_BF16_TFLOPS,
         "bwd_frac_bf16_peak": f_bwd / t_bwd / 1e12 / PEAK_BF16_TFLOPS,
-        "flops_fwd": f_fwd, "flops_bwd": f_bwd,
+        "flops_fwd": f_fwd, "flops_bwd": f_bwd, "bytes_fwd": 4 * b * h * t * d * 2 + 4 * b * h * t,
     }
 
 
@@ -283,6 +287,8 @@ def bench_gpt_train(steps, warmup, linear_routes=("pallas", "xla"), modes=("grap
                 "params": param_count(params), "params_nonembed": n_nonembed,
                 "loss_first": float(losses[0]), "loss_last": float(losses[-1]),
             }
+            if hasattr(step, "close"):
+                step.close()
             del params, opt, step, losses
             torch.cuda.synchronize()
             torch.cuda.empty_cache()
@@ -335,6 +341,7 @@ def bench_serving(new_tokens=128, prompt_len=100, batches=(1, 8, 32)):
             _, stats = eng.generate(prompts, new_tokens)
             rows.append({"batch": batch, "decode_kernels": kernels, "prompt_len": prompt_len, "new_tokens": new_tokens,
                          **{k: round(v, 4) if isinstance(v, float) else v for k, v in stats.items()}})
+            eng.close()
             del eng
     return rows
 
@@ -350,31 +357,81 @@ def bench_copy(nbytes: int = 256 << 20, iters: int = 5):
     return {"bytes_each_way": nbytes, "us": t * 1e6, "gbs_read_plus_write": 2 * nbytes / t / 1e9}
 
 
+def _blas_threads() -> int:
+    try:
+        import threadpoolctl
+
+        info = [d for d in threadpoolctl.threadpool_info() if d.get("user_api") == "blas"]
+        if info:
+            return int(info[0]["num_threads"])
+    except Exception:  # threadpoolctl missing or unreadable: fall back to the affinity mask
+        pass
+    return len(os.sched_getaffinity(0))
+
+
+def _time_until(fn, budget_s: float, unit: int = 1) -> tuple[int, float]:
+    """Call fn() after one untimed call until budget_s has passed and the count is a multiple of
+    `unit`; returns (calls, seconds)."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and n % unit == 0:
+            return n, el
+
+
 def cpu_baseline(budget_s: float = 12.0):
-    """The oracle's materialised f32 attention forward (numpy; BLAS threads on this host's cores) on a
-    bounded sample of the headline workload's (b, h) heads, reported in the same unit."""
+    """The oracle's restatement of the reference's impl='xla' path (numpy f32 on this host's cores)
+    on bounded samples of each BASELINE workload, reported in each kernel's own unit.
+
+    Headline: the materialised f32 causal attention forward (oracle.attention.forward) over whole
+    passes of the 64 (b, h) heads of 4x16x2048x128, TFLOP/s. Legs: add+RMSNorm at [4096, 1024]
+    (oracle.rmsnorm.add_rmsnorm, f32 statistics, outputs rounded to bf16; GB/s of the bf16 bytes
+    the kernel moves), and the matmul reference (f32 accumulation) at 4096^3 on bf16 values and
+    at 1000^3 f32, TFLOP/s."""
     import numpy as np
 
     from oracle import attention as oatt
+    from oracle import matmul as omm
+    from oracle import rmsnorm as orms
+    from oracle.bf16 import round_bf16
 
+    blas = _blas_threads()
     b, h, t, d = 4, 16, 2048, 128
     rng = np.random.default_rng(7)
     q, k, v = (rng.standard_normal((1, 1, t, d)).astype(np.float32) for _ in range(3))
-    oatt.forward(q, k, v, causal=True, dtype=np.float32)  # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:  # whole passes over the 64 heads until the time budget is spent
-        oatt.forward(q, k, v, causal=True, dtype=np.float32)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s and n % (b * h) == 0:
-            break
-    per_head = el / n
+    n, el = _time_until(lambda: oatt.forward(q, k, v, causal=True, dtype=np.float32), budget_s, unit=b * h)
     flops_head = 4 * t * t * d * 0.5
-    cores = len(os.sched_getaffinity(0))
-    return {"value": round(flops_head / per_head / 1e12, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"{n // (b * h)} full passes over the {b * h} (b,h) heads of the 4x16x2048x128 causal forward "
-                      f"({n} heads), oracle.attention.forward in numpy float32, {el:.1f} s",
-            "threads_env": os.environ.get("OMP_NUM_THREADS")}
+    out = {"value": round(flops_head * n / el / 1e12, 5), "unit": "TFLOP/s", "cores": blas, "kind": "port",
+           "sample": f"{n // (b * h)} full passes over the {b * h} (b,h) heads of the 4x16x2048x128 causal forward "
+                     f"({n} heads), oracle.attention.forward in numpy float32 (BLAS on {blas} threads), {el:.1f} s",
+           "threads_env": os.environ.get("OMP_NUM_THREADS")}
+
+    legs = {}
+    rows, dim = 4096, 1024
+    x = round_bf16(rng.standard_normal((rows, dim)).astype(np.float32))
+    r = round_bf16(rng.standard_normal((rows, dim)).astype(np.float32))
+    w = round_bf16((1 + 0.1 * rng.standard_normal(dim)).astype(np.float32))
+    n, el = _time_until(lambda: orms.add_rmsnorm(x, w, r, out_bf16=True), budget_s / 3)
+    nbytes = 4 * rows * dim * 2 + dim * 2
+    legs["add_rmsnorm"] = {"value": round(nbytes * n / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                           "sample": f"{n} calls of oracle.rmsnorm.add_rmsnorm on [4096, 1024] (numpy elementwise, "
+                                     f"one thread), {el:.1f} s; bytes counted as the bf16 kernel's 33,556,480"}
+    for name, size, bf in (("matmul_bf16_4096", 4096, True), ("matmul_f32_1000", 1000, False)):
+        a_ = rng.uniform(-1, 1, (size, size)).astype(np.float32)
+        b_ = rng.uniform(-1, 1, (size, size)).astype(np.float32)
+        if bf:
+            a_, b_ = round_bf16(a_), round_bf16(b_)
+        n, el = _time_until(lambda: omm.reference(a_, b_, out_bf16=bf, acc=np.float32), budget_s / 4)
+        legs[name] = {"value": round(2 * size**3 * n / el / 1e12, 5), "unit": "TFLOP/s", "cores": blas,
+                      "kind": "port",
+                      "sample": f"{n} products of oracle.matmul.reference {size}^3 in numpy float32 "
+                                f"({'bf16-valued inputs, output rounded to bf16' if bf else 'f32'}; BLAS on {blas} "
+                                f"threads), {el:.1f} s"}
+    out["legs"] = legs
+    return out
 
 
 def main(argv=None):
@@ -417,7 +474,8 @@ def main(argv=None):
     if att is not None:
         value = att["fwd_tflops"]
         ms = att["fwd_us"] / 1e3
-        roof = _roofline("mfma", value, PEAK_BF16_TFLOPS, "TFLOP/s", _traffic("attn_fwd"))
+        roof = _roofline("attn_fwd", att["flops_fwd"], att["bytes_fwd"], att["fwd_us"] * 1e-6,
+                         traffic=_traffic("attn_fwd"))
     else:  # partial runs report the first kernel measured
         first = next(iter(kernels.values()))
         value, ms, roof = first.get("gbs", first.get("tflops", 0.0)), first.get("us", 0.0) / 1e3, None
@@ -444,7 +502,8 @@ def main(argv=None):
     }
     if "add_rmsnorm" in kernels:
         r = kernels["add_rmsnorm"]
-        line["add_rmsnorm_roofline"] = _roofline("hbm", r["gbs"], PEAK_HBM_GBS, "GB/s", _traffic("add_rmsnorm"))
+        line["add_rmsnorm_roofline"] = _roofline("add_rmsnorm", 5 * r["shape"][0] * r["shape"][1], r["bytes"],
+                                                 r["us"] * 1e-6, traffic=_traffic("add_rmsnorm"))
     print(json.dumps(line), flush=True)
 
 

@@ -1654,8 +1654,12 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
   const PpDma<Tile, true> dma(wave, ldq);
   const PpDma<Tile, true> dma_do(wave, SAMEP ? ldq : lddo);
   auto slot = [&](int t) { return smem + (t % F::kSlots) * F::kSlotBytes; };
-  // DMA instruction qd of tile t. Tiles past the end have an empty buffer
-  // range: they read nothing and write zeros into a slot nobody reads again.
+  // DMA instruction qd of tile t. Tiles (and rows) past the end of the queries
+  // have an empty buffer range: the range check makes buffer_load ... lds write
+  // zeros into their LDS bytes instead of reading memory. The padded sweeps of
+  // D = 128 above read those slots, and their exactness rests on that zero
+  // fill: Q, dO, lse and delta of every padded row (statistics lanes 16-63 of
+  // stat_dma included) are 0 in LDS, never stale data of an earlier tile.
   auto dma_part = [&](int t, int qd) {
     char* sl = slot(t);
     const int r0 = (first + t) * F::BQ;

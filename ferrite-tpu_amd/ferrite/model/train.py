@@ -21,7 +21,6 @@ from __future__ import annotations
 
 import argparse
 import dataclasses
-import gc
 import json
 import math
 import os
@@ -32,6 +31,7 @@ import numpy as np
 import torch
 
 from ferrite import platform
+from ferrite.graphs import capture_window
 from ferrite.model import data as data_lib
 from ferrite.model.gpt import GPTConfig, flops_per_token, init_params, leaves, loss_fn, named_leaves, param_count, unflatten
 
@@ -234,15 +234,29 @@ class GraphedTrainStep:
         else:
             if self.graph is None:
                 torch.cuda.synchronize()
-                # No graph may be destroyed during a capture: collect unreachable ones first.
-                gc.collect()
                 self.graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(self.graph):
+                with capture_window(), torch.cuda.graph(self.graph):
                     self.loss = self._body()
             self.graph.replay()
             loss = self.loss
         self.calls += 1
         return params, {"m": opt["m"], "v": opt["v"], "step": step}, loss, self.gnorm
+
+    def close(self) -> None:
+        """Destroy the captured graph once the device has finished with it. A later call starts
+        over (warm-up, capture). Also called on leaving a ``with`` block."""
+        if self.graph is not None:
+            torch.cuda.synchronize()
+            self.graph.reset()
+            self.graph = None
+            self.loss = None
+        self.calls = 0
+
+    def __enter__(self) -> "GraphedTrainStep":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
 
 
 def train(model_cfg: GPTConfig, train_cfg: TrainConfig, *, verbose: bool = True, device=None,

@@ -22,7 +22,6 @@ same cache layout, bucketing, API and statistics:
 from __future__ import annotations
 
 import dataclasses
-import gc
 import math
 import time
 from typing import Any
@@ -30,6 +29,7 @@ from typing import Any
 import numpy as np
 import torch
 
+from ferrite.graphs import capture_window
 from ferrite.model.gpt import GPTConfig, _attention, _dot_f32, _linear, _merge_heads, _mlp, _norm, _split_heads
 
 
@@ -161,14 +161,19 @@ class _Captured:
                 self.fn()  # warm-up: library handles, allocator, kernel attributes
             torch.cuda.current_stream().wait_stream(side)
             torch.cuda.synchronize()
-            # A graph may not be destroyed while another is being captured: collect unreachable
-            # objects (a dropped engine's graphs among them) now rather than mid-capture.
-            gc.collect()
             self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph):
+            with capture_window(), torch.cuda.graph(self.graph):
                 self.out = self.fn()
         self.graph.replay()
         return self.out
+
+    def close(self) -> None:
+        """Destroy the graph (after the device has finished any replay of it) and its output."""
+        if self.graph is not None:
+            torch.cuda.synchronize()
+            self.graph.reset()
+            self.graph = None
+        self.out = None
 
 
 class Engine:
@@ -226,6 +231,22 @@ class Engine:
         self.n_compiles = len(self.compile_seconds)
         self.k_cache.zero_()
         self.v_cache.zero_()
+
+    # -- lifetime -----------------------------------------------------------
+
+    def close(self) -> None:
+        """Release every captured graph now (prefill buckets and decode). The engine cannot
+        serve afterwards. Also called on leaving a ``with Engine(...) as eng:`` block."""
+        for cap in self._prefill.values():
+            cap.close()
+        self._decode.close()
+        self._prefill.clear()
+
+    def __enter__(self) -> "Engine":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
 
     # -- public API ---------------------------------------------------------
 

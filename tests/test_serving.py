@@ -42,3 +42,29 @@ def test_engine_validation():
         eng.generate([[1] * 30], max_new_tokens=40)
     with pytest.raises(ValueError):
         eng.prefill([[1], [2]])
+
+
+def test_capture_window_holds_off_the_cycle_collector():
+    """ferrite.graphs.capture_window: no cyclic collection inside a capture, the collector's
+    previous state restored afterwards (also when the capture raises)."""
+    import gc
+
+    from ferrite.graphs import capture_window
+
+    assert gc.isenabled()
+    with capture_window():
+        assert not gc.isenabled()
+    assert gc.isenabled()
+    try:
+        with capture_window():
+            raise RuntimeError("capture failed")
+    except RuntimeError:
+        pass
+    assert gc.isenabled()
+    gc.disable()
+    try:
+        with capture_window():
+            assert not gc.isenabled()
+        assert not gc.isenabled()
+    finally:
+        gc.enable()

@@ -145,3 +145,18 @@ def test_engines_built_after_dropped_ones(dev):
         del eng
         assert alive() is None  # freed without waiting for the cycle collector
     gc.collect()
+
+
+def test_engine_close_releases_graphs(dev):
+    """Explicit lifetime: leaving a ``with Engine(...)`` block destroys every captured graph, and
+    an engine built after that captures and serves as before."""
+    cfg = CFG.replace(dtype=torch.bfloat16, n_head=4)
+    params = init_params(3, cfg, device=dev)
+    with Engine(params, cfg, ServeConfig(batch=2, max_len=128, buckets=(32,))) as eng:
+        want, _ = eng.generate([[1, 2, 3], [4, 5]], 6)
+        decode = eng._decode
+        assert decode.graph is not None
+    assert decode.graph is None and not eng._prefill
+    with Engine(params, cfg, ServeConfig(batch=2, max_len=128, buckets=(32,))) as eng2:
+        got, _ = eng2.generate([[1, 2, 3], [4, 5]], 6)
+    np.testing.assert_array_equal(got, want)
