@@ -14,6 +14,8 @@
 //   inv = rsqrt(sum(h*h) * (1/dim) + eps)
 //   y   = (h * inv) * f32(w)                (from the unrounded f32 h)
 #include <algorithm>
+#include <mutex>
+#include <string>
 
 #include "common.h"
 
@@ -464,9 +466,32 @@ __global__ __launch_bounds__(kDwCols* kDwGroups) void rmsnorm_bwd_dw_kernel(cons
   }
 }
 
-// Layout of the caller's workspace: kBwdMaxParts partial rows of dim floats,
-// then one float per row (general path only).
+// Workspace of the backward: nparts partial rows of dim floats (nparts <= kBwdMaxParts),
+// then, on the general path only, one float per row. The size query of the C ABI
+// returns the bound over every path; bwd_plan gives what one call really uses.
 int64_t bwd_workspace_bytes(int64_t rows, int64_t dim) { return ((int64_t)kBwdMaxParts * dim + rows) * 4; }
+
+struct BwdPlan {
+  bool fast;      // the one-pass row kernel (else the general row + column passes)
+  int nparts;     // partial dw rows
+  int64_t bytes;  // workspace bytes this call uses
+};
+
+BwdPlan bwd_plan(const void* h, const void* w, const void* dy, const void* dd, const void* dh, int64_t rows,
+                 int64_t dim) {
+  auto aligned16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  BwdPlan p{};
+  p.fast = dim % kChunk == 0 && dim <= 64 * kChunk * 8 && aligned16(h) && aligned16(dy) && aligned16(w) &&
+           aligned16(dh) && (!dd || aligned16(dd));
+  if (rows <= 0)
+    p.nparts = 0;
+  else if (p.fast)  // at least 4 rows per wave; at most kBwdMaxParts workgroups (two per CU)
+    p.nparts = (int)std::min<int64_t>(cdiv(rows, (int64_t)kRowsPerBlock * 4), kBwdMaxParts);
+  else
+    p.nparts = (int)std::min<int64_t>(rows, kBwdMaxParts);
+  p.bytes = ((int64_t)p.nparts * dim + (p.fast || rows <= 0 ? 0 : rows)) * 4;
+  return p;
+}
 
 template <typename TX, typename TW, typename TO, bool DIRECT>
 int bwd_launch(const void* h, const void* w, const void* dy, const void* dd, void* dh, void* dw, void* ws,
@@ -478,13 +503,9 @@ int bwd_launch(const void* h, const void* w, const void* dy, const void* dd, voi
   const TW* wp = static_cast<const TW*>(w);
   TO* op = static_cast<TO*>(dh);
   float* partial = static_cast<float*>(ws);
-  int nparts = 0;
-  auto aligned16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  const bool fast = dim % kChunk == 0 && dim <= 64 * kChunk * 8 && aligned16(h) && aligned16(dy) && aligned16(w) &&
-                    aligned16(dh) && (!DIRECT || aligned16(dd));
-  if (rows > 0 && fast) {
-    // At least 4 rows per wave; at most kBwdMaxParts workgroups (two per CU).
-    nparts = (int)std::min<int64_t>(cdiv(rows, (int64_t)kRowsPerBlock * 4), kBwdMaxParts);
+  const BwdPlan plan = bwd_plan(h, w, dy, DIRECT ? dd : nullptr, dh, rows, dim);
+  const int nparts = plan.nparts;
+  if (rows > 0 && plan.fast) {
     const int vpl = (int)cdiv(dim / kChunk, 64);
     const size_t lds = (size_t)kRowsPerBlock * dim * sizeof(float);
 #define FERRITE_RMS_BWD_CASE(V)                                                                                    \
@@ -500,12 +521,11 @@ int bwd_launch(const void* h, const void* w, const void* dy, const void* dd, voi
       FERRITE_RMS_BWD_CASE(8);
 #undef FERRITE_RMS_BWD_CASE
   } else if (rows > 0) {
-    float* inv_rows = partial + (int64_t)kBwdMaxParts * dim;
+    float* inv_rows = partial + (int64_t)nparts * dim;
     const int64_t blocks = cdiv(rows, kRowsPerBlock);
     if (blocks > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "rmsnorm_bwd: too many rows");
     hipLaunchKernelGGL((rmsnorm_bwd_rows_generic_kernel<TX, TW, TO, DIRECT>), dim3((unsigned)blocks), dim3(256), 0,
                        stream, hp, wp, gp, dp, op, inv_rows, rows, dim, inv_dim, eps);
-    nparts = (int)std::min<int64_t>(rows, kBwdMaxParts);
     const int64_t cblocks = cdiv(dim, 256);
     if (cblocks > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "rmsnorm_bwd: dim too large");
     hipLaunchKernelGGL((rmsnorm_bwd_cols_kernel<TX>), dim3((unsigned)cblocks, (unsigned)nparts), dim3(256), 0, stream,
@@ -530,6 +550,79 @@ int bwd_dispatch_out(const void* h, const void* w, const void* dy, const void* d
   return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_rmsnorm_bwd: a bf16 dh needs bf16 inputs");
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free backward (ferrite_hip_rmsnorm_bwd_noalloc):
+// the partial dw rows (and inverse RMS per row) live in this file-scope device
+// array instead of a caller's workspace. Each device that loads the library
+// holds its own copy until the process ends. Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in symbol): the
+// device address is looked up once per device with hipGetSymbolAddress, with
+// that device current, and that address is what the kernels receive.
+// ---------------------------------------------------------------------------
+constexpr int kMaxDevices = 64;
+static_assert(FERRITE_RMSNORM_BWD_SCRATCH_BYTES % 256 == 0, "scratch size");
+
+static __device__ __align__(256) float scratch[FERRITE_RMSNORM_BWD_SCRATCH_BYTES / sizeof(float)];
+
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device), or nullptr with the error message set.
+void* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(FERRITE_ERR_LAUNCH, "ferrite_hip_rmsnorm_bwd_noalloc: no current HIP device");
+    return nullptr;
+  }
+  ScratchSlot& slot = g_scratch[dev];
+  std::call_once(slot.once, [&slot] {
+    void* p = nullptr;
+    slot.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    slot.ptr = slot.err == hipSuccess ? p : nullptr;
+  });
+  if (!slot.ptr) {
+    fail(FERRITE_ERR_LAUNCH, std::string("ferrite_hip_rmsnorm_bwd_noalloc: hipGetSymbolAddress(scratch) failed: ") +
+                                 hipGetErrorString(slot.err));
+    return nullptr;
+  }
+  return slot.ptr;
+}
+
+int bwd_entry(const char* name, const void* h, const void* weight, const void* dy, const void* dh_direct, void* dh,
+              void* dweight, void* workspace, bool noalloc, int64_t rows, int64_t dim, int x_dtype, int w_dtype,
+              int dh_dtype, float eps, void* stream) {
+  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype) || !valid_dtype(dh_dtype))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": dtype must be FERRITE_F32 or FERRITE_BF16");
+  if (rows < 0 || dim < 1) return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": need rows >= 0 and dim >= 1");
+  if (!weight || !dweight || (!noalloc && !workspace) || (rows > 0 && (!h || !dy || !dh)))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": null pointer");
+  if (noalloc) {
+    const BwdPlan plan = bwd_plan(h, weight, dy, dh_direct, dh, rows, dim);
+    if (plan.bytes > (int64_t)FERRITE_RMSNORM_BWD_SCRATCH_BYTES)
+      return fail(FERRITE_ERR_INVALID_ARGUMENT,
+                  std::string(name) + ": rows=" + std::to_string(rows) + ", dim=" + std::to_string(dim) + " need " +
+                      std::to_string(plan.bytes) + " bytes of scratch, more than its fixed " +
+                      std::to_string((long long)FERRITE_RMSNORM_BWD_SCRATCH_BYTES) +
+                      " (use ferrite_hip_rmsnorm_bwd with a workspace)");
+    workspace = scratch_on_current_device();
+    if (!workspace) return FERRITE_ERR_LAUNCH;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x_dtype == FERRITE_BF16) {
+    if (w_dtype == FERRITE_BF16)
+      return bwd_dispatch_out<bf16, bf16>(h, weight, dy, dh_direct, dh, dweight, workspace, rows, dim, dh_dtype, eps, s);
+    return bwd_dispatch_out<bf16, float>(h, weight, dy, dh_direct, dh, dweight, workspace, rows, dim, dh_dtype, eps, s);
+  }
+  if (w_dtype == FERRITE_BF16)
+    return bwd_dispatch_out<float, bf16>(h, weight, dy, dh_direct, dh, dweight, workspace, rows, dim, dh_dtype, eps, s);
+  return bwd_dispatch_out<float, float>(h, weight, dy, dh_direct, dh, dweight, workspace, rows, dim, dh_dtype, eps, s);
+}
+
 }  // namespace
 }  // namespace ferrite
 
@@ -552,20 +645,14 @@ extern "C" int64_t ferrite_hip_rmsnorm_bwd_workspace(int64_t rows, int64_t dim) 
 extern "C" int ferrite_hip_rmsnorm_bwd(const void* h, const void* weight, const void* dy, const void* dh_direct,
                                        void* dh, void* dweight, void* workspace, int64_t rows, int64_t dim,
                                        int x_dtype, int w_dtype, int dh_dtype, float eps, void* stream) {
-  using namespace ferrite;
-  const char* name = "ferrite_hip_rmsnorm_bwd";
-  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype) || !valid_dtype(dh_dtype))
-    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": dtype must be FERRITE_F32 or FERRITE_BF16");
-  if (rows < 0 || dim < 1) return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": need rows >= 0 and dim >= 1");
-  if (!weight || !dweight || !workspace || (rows > 0 && (!h || !dy || !dh)))
-    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": null pointer");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (x_dtype == FERRITE_BF16) {
-    if (w_dtype == FERRITE_BF16)
-      return bwd_dispatch_out<bf16, bf16>(h, weight, dy, dh_direct, dh, dweight, workspace, rows, dim, dh_dtype, eps, s);
-    return bwd_dispatch_out<bf16, float>(h, weight, dy, dh_direct, dh, dweight, workspace, rows, dim, dh_dtype, eps, s);
-  }
-  if (w_dtype == FERRITE_BF16)
-    return bwd_dispatch_out<float, bf16>(h, weight, dy, dh_direct, dh, dweight, workspace, rows, dim, dh_dtype, eps, s);
-  return bwd_dispatch_out<float, float>(h, weight, dy, dh_direct, dh, dweight, workspace, rows, dim, dh_dtype, eps, s);
+  return ferrite::bwd_entry("ferrite_hip_rmsnorm_bwd", h, weight, dy, dh_direct, dh, dweight, workspace, false, rows,
+                            dim, x_dtype, w_dtype, dh_dtype, eps, stream);
+}
+
+extern "C" int ferrite_hip_rmsnorm_bwd_noalloc(const void* h, const void* weight, const void* dy,
+                                               const void* dh_direct, void* dh, void* dweight, int64_t rows,
+                                               int64_t dim, int x_dtype, int w_dtype, int dh_dtype, float eps,
+                                               void* stream) {
+  return ferrite::bwd_entry("ferrite_hip_rmsnorm_bwd_noalloc", h, weight, dy, dh_direct, dh, dweight, nullptr, true,
+                            rows, dim, x_dtype, w_dtype, dh_dtype, eps, stream);
 }

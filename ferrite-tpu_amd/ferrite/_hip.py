@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libferrite_
 
 F32 = 0
 BF16 = 1
+RMSNORM_BWD_SCRATCH_BYTES = 8 << 20  # FERRITE_RMSNORM_BWD_SCRATCH_BYTES
 GELU = 1
 GELU_GRAD = 2
 OK = 0
@@ -38,6 +39,10 @@ SIGNATURES: dict[str, tuple] = {
     "ferrite_hip_rmsnorm_bwd": (
         _c_int,
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_f32, _vp],
+    ),
+    "ferrite_hip_rmsnorm_bwd_noalloc": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_f32, _vp],
     ),
     "ferrite_hip_matmul": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _vp]),
     "ferrite_hip_matmul_workspace": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_int]),

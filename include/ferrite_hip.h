@@ -103,6 +103,26 @@ int ferrite_hip_rmsnorm_bwd(const void* h, const void* weight, const void* dy, c
                             int dh_dtype, float eps, void* stream);
 
 /*
+ * ferrite_hip_rmsnorm_bwd without a workspace argument, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving/training
+ * loops, harnesses that forbid hipMalloc. No counterpart in the reference (XLA
+ * owns its scratch there). Same arguments minus `workspace`, same kernels and
+ * bitwise the same results. Its scratch (the partial dweight rows) is a fixed
+ * FERRITE_RMSNORM_BWD_SCRATCH_BYTES device array inside the library, one per
+ * GPU, held until the process ends; the call itself allocates nothing. A shape
+ * needing more scratch fails with FERRITE_ERR_INVALID_ARGUMENT (the fast path
+ * needs min(512, ceil(rows / 16)) * dim * 4 bytes, so any rows with dim <= 4096;
+ * unaligned or other dims also need 4 * rows more). Every call on one GPU uses
+ * that GPU's one array: calls that overlap in time on the same GPU (two streams,
+ * two threads) race and give wrong dweight. Nothing in the array needs to
+ * start at zero.
+ */
+#define FERRITE_RMSNORM_BWD_SCRATCH_BYTES (8u << 20)
+int ferrite_hip_rmsnorm_bwd_noalloc(const void* h, const void* weight, const void* dy, const void* dh_direct,
+                                    void* dh, void* dweight, int64_t rows, int64_t dim, int x_dtype, int w_dtype,
+                                    int dh_dtype, float eps, void* stream);
+
+/*
  * out[M, N] = x[M, K] @ y[K, N] with f32 accumulation (matmul.py:27-38, :52-86).
  * in_dtype FERRITE_BF16 uses bf16 MFMA; FERRITE_F32 uses fp32 MFMA (true fp32
  * products, the reference's Precision.HIGHEST, _compat.py:17-25). Ragged shapes

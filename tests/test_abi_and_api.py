@@ -25,7 +25,7 @@ def _declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     declared = _declared_symbols()
-    assert len(declared) == 25
+    assert len(declared) == 26
     out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH], capture_output=True, text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s(\w+)", out))
     missing = [s for s in declared if s not in exported]
@@ -51,6 +51,16 @@ def test_abi_argument_checks_return_codes():
     assert lib.ferrite_hip_rmsnorm_bwd(1, 1, None, None, 1, 1, 1, 4, 8, _hip.BF16, _hip.F32, _hip.BF16, 1e-6, None) == 1
     assert "null" in _hip.last_error()
     assert lib.ferrite_hip_rmsnorm_bwd(1, 1, 1, None, 1, 1, 1, 4, 8, _hip.F32, _hip.F32, _hip.BF16, 1e-6, None) == 1
+    # the allocation-free backward: shapes beyond its fixed scratch are refused before any device call
+    a = 1 << 12  # 16-byte aligned stand-in addresses: the fast path's plan (512 partial rows of dim floats)
+    assert lib.ferrite_hip_rmsnorm_bwd_noalloc(a, a, a, None, a, a, 1 << 20, 8192, _hip.BF16, _hip.F32, _hip.BF16,
+                                               1e-6, None) == 1
+    assert "scratch" in _hip.last_error() and str(_hip.RMSNORM_BWD_SCRATCH_BYTES) in _hip.last_error()
+    assert lib.ferrite_hip_rmsnorm_bwd_noalloc(a, a, a, None, a, a, 16, 8, _hip.BF16, 9, _hip.BF16, 1e-6, None) == 1
+    assert "dtype" in _hip.last_error()
+    assert lib.ferrite_hip_rmsnorm_bwd_noalloc(a, a, None, None, a, a, 16, 8, _hip.BF16, _hip.F32, _hip.BF16, 1e-6,
+                                               None) == 1
+    assert "null" in _hip.last_error()
     # AdamW: workspace query and argument checks (host arrays are inspected before any launch)
     assert lib.ferrite_hip_adamw_workspace(75) == (3 * 2048 + 4) * 4
     assert lib.ferrite_hip_adamw_workspace(-1) == -1
