@@ -118,12 +118,14 @@ struct Stager {
   typedef typename Elem<T>::vec vec;
   vec v[kJobsPerThread][4];
   uint32_t voff[kJobsPerThread][4];  // byte offset of each job row inside a tile (aligned path)
+  int ld;                            // element stride between rows (d, or more for a column slab)
 
   // Aligned rows use raw buffer loads: the tile's first row is folded into the
   // buffer base, each lane's offset inside the tile is fixed, and the hardware
   // range check returns zeros for rows past the end and for padded columns
   // (whose offset is kOutOfRange), so the staging has no branches.
-  __device__ __forceinline__ explicit Stager(int d) {
+  // `d` columns are valid; rows lie `ld_` elements apart (0: ld = d).
+  __device__ __forceinline__ explicit Stager(int d, int ld_ = 0) : ld(ld_ ? ld_ : d) {
     if constexpr (ALIGNED) {
       const int t = threadIdx.x;
 #pragma unroll
@@ -133,18 +135,18 @@ struct Stager {
         const int c0 = cg * kVec;
         const bool ok = job < kJobs && c0 < d;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) voff[j][i] = ok ? (uint32_t)(((rg * 4 + i) * d + c0) * (int)sizeof(T)) : kOutOfRange;
+        for (int i = 0; i < 4; ++i) voff[j][i] = ok ? (uint32_t)(((rg * 4 + i) * ld + c0) * (int)sizeof(T)) : kOutOfRange;
       }
     }
   }
 
-  // Rows [r0, r0 + ROWS) of a [nrows, d] matrix (row stride d) at `base`.
+  // Rows [r0, r0 + ROWS) of a [nrows, d] matrix (row stride ld) at `base`.
   __device__ __forceinline__ void load(const T* __restrict__ base, int r0, int nrows, int d) {
     const int t = threadIdx.x;
     if constexpr (ALIGNED) {
       const int rows_left = nrows - r0 > 0 ? nrows - r0 : 0;
       const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<T*>(base) + (int64_t)r0 * d, (short)0, rows_left * d * (int)sizeof(T), 0x00020000);
+          const_cast<T*>(base) + (int64_t)r0 * ld, (short)0, rows_left * ld * (int)sizeof(T), 0x00020000);
 #pragma unroll
       for (int j = 0; j < kJobsPerThread; ++j)
 #pragma unroll
@@ -162,7 +164,7 @@ struct Stager {
         const int row = r0 + rg * 4 + i;
         const bool rok = job < kJobs && row < nrows;
 #pragma unroll
-        for (int e = 0; e < kVec; ++e) v[j][i][e] = (rok && c0 + e < d) ? base[row * d + c0 + e] : (T)0.f;
+        for (int e = 0; e < kVec; ++e) v[j][i][e] = (rok && c0 + e < d) ? base[(int64_t)row * ld + c0 + e] : (T)0.f;
       }
     }
   }
@@ -1517,6 +1519,417 @@ __global__ __launch_bounds__(kThreads, 1) void attn_dkv_kernel(const T* __restri
 }
 
 // ===========================================================================
+// Wide head dims (D = 128 * nc, nc >= 2): the forward for D > 256, dQ and dK/dV
+// for D >= 256 (the reference accepts any multiple of 128, flash_attention.py:
+// 341-343). The products that contract over D (S = Q K^T, dP = dO V^T) run over
+// the nc 128-column slabs of the operands, each staged through LDS in turn. The
+// products that produce D columns (O, dQ, dK, dV) keep the accumulators of one
+// 128-column output slab, chosen by the workgroup's place in the grid, so nc
+// workgroups recompute a tile's scores and each writes its own slab. Register
+// and LDS use therefore do not grow with D. Tile shapes, fragment layouts,
+// masking and the exp2-domain softmax are those of the kernels above at D = 128.
+// ===========================================================================
+constexpr int kSlab = 128;
+
+template <typename T>
+struct Wide {
+  static constexpr int BQ = 128;                  // queries per workgroup (forward, dQ)
+  static constexpr int BKV = 128;                 // keys per workgroup (dK/dV)
+  static constexpr int BS = AttnTiles<T>::kStep;  // streamed rows per step (64 bf16, 32 f32)
+  static constexpr int NT = BS / 32;
+  static constexpr int KS = kSlab / 16;  // 16-wide k chunks of one slab
+  static constexpr int DT = kSlab / 32;  // 32-column output tiles of one slab
+  static constexpr int kRowBytes = BS * RowTile<T, kSlab>::kPitch;
+  static constexpr int kTrBytes = kSlab * 128;
+  static constexpr int kFwdLds = kRowBytes + kTrBytes;
+  static constexpr int kDqLds = 2 * kRowBytes + kTrBytes;
+  static constexpr int kDkvLds = 2 * kRowBytes + 2 * kTrBytes + 2 * BS * 4;
+};
+
+// Workgroup -> (head, tile, output slab): heads fastest, then tiles (the
+// heaviest causal tiles first where `heavy_last`), then slabs.
+struct WideCoord {
+  int bh, tile, slab;
+  __device__ WideCoord(int bh_count, int n_tiles, bool heavy_last) {
+    bh = blockIdx.x % bh_count;
+    const int rest = blockIdx.x / bh_count;
+    const int t = rest % n_tiles;
+    tile = heavy_last ? n_tiles - 1 - t : t;
+    slab = rest / n_tiles;
+  }
+};
+
+template <typename T, bool ALIGNED>
+__global__ __launch_bounds__(kThreads, ALIGNED ? 2 : 1) void attn_fwd_wide_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                                   const T* __restrict__ v, T* __restrict__ o,
+                                                                   float* __restrict__ lse, int bh_count, int Sq,
+                                                                   int Sk, int d, int causal, float scale_log2,
+                                                                   int neg_q, int n_qtiles) {
+  typedef Wide<T> F;
+  typedef typename Elem<T>::frag frag;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char* kl = smem;                 // K rows of one slab
+  char* vl = smem + F::kRowBytes;  // V^T of the output slab
+
+  const int nc = d / kSlab;
+  const WideCoord wc(bh_count, n_qtiles, true);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int q0 = wc.tile * F::BQ;
+  const int q0w = q0 + wave * 32;
+  const int qrow = q0w + l32;
+
+  const T* qb = q + (int64_t)wc.bh * Sq * d;
+  const T* kb = k + (int64_t)wc.bh * Sk * d;
+  const T* vb = v + (int64_t)wc.bh * Sk * d;
+
+  const int q_last = min(q0 + F::BQ, Sq) - 1;
+  const int n_tiles = causal ? min(q_last, Sk - 1) / F::BS + 1 : (Sk + F::BS - 1) / F::BS;
+  const bool wave_active = q0w < Sq;
+  const int wave_tiles = !wave_active ? 0 : causal ? min(q0w + 31, Sq - 1) / F::BS + 1 : n_tiles;
+
+  f32x16 acc[F::DT];
+#pragma unroll
+  for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[u][r] = 0.f;
+  float m = -INFINITY;
+  float lsum[4] = {0.f, 0.f, 0.f, 0.f};
+  Stager<T, kSlab, F::BS, ALIGNED> ks(kSlab, d), vs(kSlab, d);
+
+  for (int j = 0; j < n_tiles; ++j) {
+    const int kv0 = j * F::BS;
+    const bool work = j < wave_tiles;
+    // S^T = K Q^T over the slabs: s[t][r] is key kv0 + t*32 + g*16 + r, query qrow.
+    f32x16 s[F::NT];
+#pragma unroll
+    for (int t = 0; t < F::NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+    for (int c = 0; c < nc; ++c) {
+      ks.load(kb + c * kSlab, kv0, Sk, kSlab);
+      __syncthreads();  // every wave is done with the previous slab
+      ks.store_rows(kl);
+      __syncthreads();
+      if (work) {
+        frag qf[F::KS];
+        if (neg_q)
+          load_row_frags<T, kSlab, ALIGNED, true>(qf, qb + c * kSlab, q0w, Sq, kSlab, d);
+        else
+          load_row_frags<T, kSlab, ALIGNED, false>(qf, qb + c * kSlab, q0w, Sq, kSlab, d);
+        lds_mfma_pipeline<F::KS * F::NT>(
+            [&](int i) { return RowTile<T, kSlab>::frag(kl, (i % F::NT) * 32 + l32, (i / F::NT) * 16 + g * 8); },
+            [&](int i, const frag& a) { mma32(a, qf[i / F::NT], s[i % F::NT]); });
+      }
+    }
+    // V^T of the output slab. Its previous readers finished before the slab
+    // loop's barriers above.
+    vs.load(vb + wc.slab * kSlab, kv0, Sk, kSlab);
+    vs.store_transposed(vl);
+    __syncthreads();
+    if (!work) continue;
+
+    if ((causal && kv0 + F::BS - 1 > q0w) || kv0 + F::BS > Sk) {
+      const int lim = causal ? min(qrow, Sk - 1) : Sk - 1;
+#pragma unroll
+      for (int t = 0; t < F::NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[t][r] = (kv0 + t * 32 + g * 16 + r > lim) ? -INFINITY : s[t][r];
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < F::NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+    mx = lane32_max(mx) * scale_log2;
+    if (__any(mx > m + kRescaleThreshold)) {
+      const float m_new = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lsum[i] *= alpha;
+#pragma unroll
+      for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[u][r] *= alpha;
+      m = m_new;
+    }
+    const float neg_m = -m;
+    frag pf[F::NT][2];
+#pragma unroll
+    for (int t = 0; t < F::NT; ++t) {
+      float p[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][r], scale_log2, neg_m));
+        lsum[r & 3] += p[r];
+      }
+      to_frag(p, pf[t][0]);
+      to_frag(p + 8, pf[t][1]);
+    }
+    // O^T (this slab) += V^T P^T
+    lds_mfma_pipeline<F::DT * F::NT * 2>(
+        [&](int i) {
+          const int c = i / F::DT;
+          return TrTile<T>::frag(vl, (i % F::DT) * 32 + l32, (c >> 1) * 32 + g * 16 + (c & 1) * 8);
+        },
+        [&](int i, const frag& a) {
+          const int c = i / F::DT;
+          mma32(a, pf[c >> 1][c & 1], acc[i % F::DT]);
+        });
+  }
+
+  if (!wave_active) return;
+  const float l = lane32_sum((lsum[0] + lsum[1]) + (lsum[2] + lsum[3]));
+  const float inv = 1.0f / l;
+  store_acc_rows<T, kSlab, ALIGNED>(acc, o + (int64_t)wc.bh * Sq * d + wc.slab * kSlab, qrow, Sq, kSlab, inv, d);
+  if (wc.slab == 0 && g == 0 && qrow < Sq) lse[(int64_t)wc.bh * Sq + qrow] = (m + __builtin_amdgcn_logf(l)) * kLn2;
+}
+
+template <typename T, bool ALIGNED>
+__global__ __launch_bounds__(kThreads, ALIGNED ? 2 : 1) void attn_dq_wide_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                                  const T* __restrict__ v, const T* __restrict__ dout,
+                                                                  const float* __restrict__ lse,
+                                                                  const float* __restrict__ delta, T* __restrict__ dq,
+                                                                  int bh_count, int Sq, int Sk, int d, int causal,
+                                                                  float scale, float scale_log2, int n_qtiles) {
+  typedef Wide<T> F;
+  typedef typename Elem<T>::frag frag;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char* kl = smem;                     // K rows of one slab
+  char* vl = smem + F::kRowBytes;      // V rows of the same slab
+  char* ktl = smem + 2 * F::kRowBytes;  // K^T of the output slab
+
+  const int nc = d / kSlab;
+  const WideCoord wc(bh_count, n_qtiles, true);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int q0 = wc.tile * F::BQ;
+  const int q0w = q0 + wave * 32;
+  const int qrow = q0w + l32;
+
+  const T* qb = q + (int64_t)wc.bh * Sq * d;
+  const T* dob = dout + (int64_t)wc.bh * Sq * d;
+  const T* kb = k + (int64_t)wc.bh * Sk * d;
+  const T* vb = v + (int64_t)wc.bh * Sk * d;
+
+  const int q_last = min(q0 + F::BQ, Sq) - 1;
+  const int n_tiles = causal ? min(q_last, Sk - 1) / F::BS + 1 : (Sk + F::BS - 1) / F::BS;
+  const bool wave_active = q0w < Sq;
+  const int wave_tiles = !wave_active ? 0 : causal ? min(q0w + 31, Sq - 1) / F::BS + 1 : n_tiles;
+  const bool qok = qrow < Sq;
+  const float lse2 = qok ? lse[(int64_t)wc.bh * Sq + qrow] * kLog2e : 0.f;
+  const float dl = qok ? delta[(int64_t)wc.bh * Sq + qrow] : 0.f;
+
+  f32x16 acc[F::DT];
+#pragma unroll
+  for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[u][r] = 0.f;
+  Stager<T, kSlab, F::BS, ALIGNED> ks(kSlab, d), vs(kSlab, d);
+
+  for (int j = 0; j < n_tiles; ++j) {
+    const int kv0 = j * F::BS;
+    const bool work = j < wave_tiles;
+    // S^T = K Q^T and dP^T = V dO^T over the slabs: [t][r] is key kv0 + t*32 + g*16 + r, query qrow.
+    f32x16 s[F::NT], dp[F::NT];
+#pragma unroll
+    for (int t = 0; t < F::NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[t][r] = 0.f;
+        dp[t][r] = 0.f;
+      }
+    for (int c = 0; c < nc; ++c) {
+      ks.load(kb + c * kSlab, kv0, Sk, kSlab);
+      vs.load(vb + c * kSlab, kv0, Sk, kSlab);
+      __syncthreads();
+      ks.store_rows(kl);
+      vs.store_rows(vl);
+      __syncthreads();
+      if (work) {
+        frag qf[F::KS], dof[F::KS];
+        load_row_frags<T, kSlab, ALIGNED>(qf, qb + c * kSlab, q0w, Sq, kSlab, d);
+        load_row_frags<T, kSlab, ALIGNED>(dof, dob + c * kSlab, q0w, Sq, kSlab, d);
+#pragma unroll
+        for (int kk = 0; kk < F::KS; ++kk)
+#pragma unroll
+          for (int t = 0; t < F::NT; ++t) {
+            mma32(RowTile<T, kSlab>::frag(kl, t * 32 + l32, kk * 16 + g * 8), qf[kk], s[t]);
+            mma32(RowTile<T, kSlab>::frag(vl, t * 32 + l32, kk * 16 + g * 8), dof[kk], dp[t]);
+          }
+      }
+    }
+    ks.load(kb + wc.slab * kSlab, kv0, Sk, kSlab);
+    ks.store_transposed(ktl);
+    __syncthreads();
+    if (!work) continue;
+
+    const bool need_mask = (causal && kv0 + F::BS - 1 > q0w) || (kv0 + F::BS > Sk);
+    frag dsf[F::NT][2];
+#pragma unroll
+    for (int t = 0; t < F::NT; ++t) {
+      float ds[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = __builtin_amdgcn_exp2f(s[t][r] * scale_log2 - lse2);
+        if (need_mask) {
+          const int kv = kv0 + t * 32 + g * 16 + r;
+          if (kv >= Sk || (causal && kv > qrow)) p = 0.f;
+        }
+        ds[r] = p * (dp[t][r] - dl);
+      }
+      to_frag(ds, dsf[t][0]);
+      to_frag(ds + 8, dsf[t][1]);
+    }
+    // dQ^T (this slab) += K^T dS^T
+#pragma unroll
+    for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+      for (int t = 0; t < F::NT; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          mma32(TrTile<T>::frag(ktl, u * 32 + l32, t * 32 + g * 16 + h * 8), dsf[t][h], acc[u]);
+  }
+  if (!wave_active) return;
+  store_acc_rows<T, kSlab, ALIGNED>(acc, dq + (int64_t)wc.bh * Sq * d + wc.slab * kSlab, qrow, Sq, kSlab, scale, d);
+}
+
+template <typename T, bool ALIGNED>
+__global__ __launch_bounds__(kThreads, 1) void attn_dkv_wide_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                                   const T* __restrict__ v, const T* __restrict__ dout,
+                                                                   const float* __restrict__ lse,
+                                                                   const float* __restrict__ delta, T* __restrict__ dk,
+                                                                   T* __restrict__ dv, int bh_count, int Sq, int Sk,
+                                                                   int d, int causal, float scale, float scale_log2,
+                                                                   int n_ktiles) {
+  typedef Wide<T> F;
+  typedef typename Elem<T>::frag frag;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char* ql = smem;                          // Q rows of one slab
+  char* dol = ql + F::kRowBytes;            // dO rows of the same slab
+  char* qtl = dol + F::kRowBytes;           // Q^T of the output slab
+  char* dotl = qtl + F::kTrBytes;           // dO^T of the output slab
+  float* lsel = reinterpret_cast<float*>(dotl + F::kTrBytes);
+  float* dll = lsel + F::BS;
+
+  const int nc = d / kSlab;
+  const WideCoord wc(bh_count, n_ktiles, false);  // heaviest (first) key tiles first
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int k0 = wc.tile * F::BKV;
+  const int k0w = k0 + wave * 32;
+  const int kvrow = k0w + l32;
+
+  const T* qb = q + (int64_t)wc.bh * Sq * d;
+  const T* dob = dout + (int64_t)wc.bh * Sq * d;
+  const T* kb = k + (int64_t)wc.bh * Sk * d;
+  const T* vb = v + (int64_t)wc.bh * Sk * d;
+  const float* lseb = lse + (int64_t)wc.bh * Sq;
+  const float* db = delta + (int64_t)wc.bh * Sq;
+
+  const int first = causal ? k0 / F::BS : 0;
+  const int n_qt = (Sq + F::BS - 1) / F::BS;
+  const bool wave_active = k0w < Sk;
+
+  f32x16 dka[F::DT], dva[F::DT];
+#pragma unroll
+  for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dka[u][r] = 0.f;
+      dva[u][r] = 0.f;
+    }
+  Stager<T, kSlab, F::BS, ALIGNED> qs(kSlab, d), dos(kSlab, d);
+
+  for (int it = first; it < n_qt; ++it) {
+    const int qs0 = it * F::BS;
+    // Causal: this wave's keys see queries >= k0w only.
+    const bool work = wave_active && !(causal && qs0 + F::BS - 1 < k0w);
+    // S = Q K^T and dP = dO V^T over the slabs: [t][r] is query qs0 + t*32 + g*16 + r, key kvrow.
+    f32x16 s[F::NT], dp[F::NT];
+#pragma unroll
+    for (int t = 0; t < F::NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[t][r] = 0.f;
+        dp[t][r] = 0.f;
+      }
+    for (int c = 0; c < nc; ++c) {
+      qs.load(qb + c * kSlab, qs0, Sq, kSlab);
+      dos.load(dob + c * kSlab, qs0, Sq, kSlab);
+      __syncthreads();
+      qs.store_rows(ql);
+      dos.store_rows(dol);
+      __syncthreads();
+      if (work) {
+        frag kf[F::KS], vf[F::KS];
+        load_row_frags<T, kSlab, ALIGNED>(kf, kb + c * kSlab, k0w, Sk, kSlab, d);
+        load_row_frags<T, kSlab, ALIGNED>(vf, vb + c * kSlab, k0w, Sk, kSlab, d);
+#pragma unroll
+        for (int kk = 0; kk < F::KS; ++kk)
+#pragma unroll
+          for (int t = 0; t < F::NT; ++t) {
+            mma32(RowTile<T, kSlab>::frag(ql, t * 32 + l32, kk * 16 + g * 8), kf[kk], s[t]);
+            mma32(RowTile<T, kSlab>::frag(dol, t * 32 + l32, kk * 16 + g * 8), vf[kk], dp[t]);
+          }
+      }
+    }
+    // The output slab's Q^T and dO^T and the step's statistics; their
+    // previous readers finished before the slab loop's barriers above.
+    qs.load(qb + wc.slab * kSlab, qs0, Sq, kSlab);
+    dos.load(dob + wc.slab * kSlab, qs0, Sq, kSlab);
+    if (threadIdx.x < F::BS) {
+      const int row = qs0 + threadIdx.x;
+      // Rows past Sq get lse = +inf so that P = 0 there.
+      lsel[threadIdx.x] = row < Sq ? lseb[row] * kLog2e : INFINITY;
+      dll[threadIdx.x] = row < Sq ? db[row] : 0.f;
+    }
+    qs.store_transposed(qtl);
+    dos.store_transposed(dotl);
+    __syncthreads();
+    if (!work) continue;
+
+    const bool need_mask = causal && qs0 < k0w + 31;
+    frag pf[F::NT][2], dsf[F::NT][2];
+#pragma unroll
+    for (int t = 0; t < F::NT; ++t) {
+      float p[16], ds[16];
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const f32x4 ls = *reinterpret_cast<const f32x4*>(lsel + t * 32 + g * 16 + r4 * 4);
+        const f32x4 dd = *reinterpret_cast<const f32x4*>(dll + t * 32 + g * 16 + r4 * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = r4 * 4 + e;
+          float pv = __builtin_amdgcn_exp2f(s[t][r] * scale_log2 - ls[e]);
+          if (need_mask && kvrow > qs0 + t * 32 + g * 16 + r) pv = 0.f;
+          p[r] = pv;
+          ds[r] = pv * (dp[t][r] - dd[e]);
+        }
+      }
+      to_frag(p, pf[t][0]);
+      to_frag(p + 8, pf[t][1]);
+      to_frag(ds, dsf[t][0]);
+      to_frag(ds + 8, dsf[t][1]);
+    }
+    // dV^T += dO^T P ; dK^T += Q^T dS (this slab)
+#pragma unroll
+    for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+      for (int t = 0; t < F::NT; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          mma32(TrTile<T>::frag(dotl, u * 32 + l32, t * 32 + g * 16 + h * 8), pf[t][h], dva[u]);
+          mma32(TrTile<T>::frag(qtl, u * 32 + l32, t * 32 + g * 16 + h * 8), dsf[t][h], dka[u]);
+        }
+  }
+  if (!wave_active) return;
+  const int64_t off = (int64_t)wc.bh * Sk * d + wc.slab * kSlab;
+  store_acc_rows<T, kSlab, ALIGNED>(dka, dk + off, kvrow, Sk, kSlab, scale, d);
+  store_acc_rows<T, kSlab, ALIGNED>(dva, dv + off, kvrow, Sk, kSlab, 1.0f, d);
+}
+
+// ===========================================================================
 // Backward, bf16 with D in {64, 128}: streamed tiles read as rows and transposed
 // ===========================================================================
 // The backward kernels read each streamed 64-row tile twice: as row
@@ -2115,12 +2528,10 @@ int check_shape(const char* name, const Shape& s, int dtype, int causal, bool bw
     return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": need b, h, sq, sk, d >= 1");
   if (causal && s.sq != s.sk)
     return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": causal attention needs sq == sk");
-  const int64_t dmax = bwd ? 128 : 256;
-  if (s.d > dmax || (s.d > 128 && s.d != 256))
-    return fail(FERRITE_ERR_INVALID_ARGUMENT,
-                std::string(name) + ": head_dim " + std::to_string(s.d) +
-                    (bwd ? " not supported (backward supports head_dim <= 128)"
-                         : " not supported (head_dim <= 128 or == 256)"));
+  (void)bwd;
+  if (s.d > 128 && s.d % kSlab != 0)
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": head_dim " + std::to_string(s.d) +
+                                                  " not supported (head_dim <= 128 or a multiple of 128)");
   if (s.b * s.h > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, std::string(name) + ": b*h too large");
   // In-kernel offsets within one (b, h) head are 32-bit byte offsets.
   const int64_t head_bytes = (s.sq > s.sk ? s.sq : s.sk) * s.d * (dtype == FERRITE_BF16 ? 2 : 4);
@@ -2295,6 +2706,61 @@ int dkv_launch(const void* q, const void* k, const void* v, const void* dout, co
   return check_launch("ferrite_flash_attention_bwd_dkv");
 }
 
+// Wide head dims: grid = heads x tiles x 128-column output slabs.
+template <typename T, bool AL>
+int fwd_wide_launch(const void* q, const void* k, const void* v, void* o, float* lse, const Shape& s, int causal,
+                    float scale, hipStream_t stream) {
+  typedef Wide<T> F;
+  const int64_t nq = cdiv(s.sq, F::BQ), bh = s.b * s.h, nc = s.d / kSlab;
+  if (nq * bh * nc > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: grid too large");
+  float c = scale * kLog2e;  // see fwd_launch: a positive multiplier, the sign moved onto q
+  const int neg_q = c < 0.f;
+  c = fmaxf(fabsf(c), 1e-30f);
+  auto kern = attn_fwd_wide_kernel<T, AL>;
+  set_lds(kern, F::kFwdLds);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh * nc)), dim3(kThreads), F::kFwdLds, stream,
+                     static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), static_cast<T*>(o),
+                     lse, (int)bh, (int)s.sq, (int)s.sk, (int)s.d, causal, c, neg_q, (int)nq);
+  return check_launch("ferrite_flash_attention_fwd");
+}
+
+template <typename T, bool AL>
+int dq_wide_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
+                   void* dq, const Shape& s, int causal, float scale, hipStream_t stream) {
+  typedef Wide<T> F;
+  const int64_t nq = cdiv(s.sq, F::BQ), bh = s.b * s.h, nc = s.d / kSlab;
+  if (nq * bh * nc > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq: grid too large");
+  auto kern = attn_dq_wide_kernel<T, AL>;
+  set_lds(kern, F::kDqLds);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh * nc)), dim3(kThreads), F::kDqLds, stream,
+                     static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                     static_cast<const T*>(dout), lse, delta, static_cast<T*>(dq), (int)bh, (int)s.sq, (int)s.sk,
+                     (int)s.d, causal, scale, scale * kLog2e, (int)nq);
+  return check_launch("ferrite_flash_attention_bwd_dq");
+}
+
+template <typename T, bool AL>
+int dkv_wide_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                    const float* delta, void* dk, void* dv, const Shape& s, int causal, float scale,
+                    hipStream_t stream) {
+  typedef Wide<T> F;
+  const int64_t nk = cdiv(s.sk, F::BKV), bh = s.b * s.h, nc = s.d / kSlab;
+  if (nk * bh * nc > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dkv: grid too large");
+  auto kern = attn_dkv_wide_kernel<T, AL>;
+  set_lds(kern, F::kDkvLds);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh * nc)), dim3(kThreads), F::kDkvLds, stream,
+                     static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                     static_cast<const T*>(dout), lse, delta, static_cast<T*>(dk), static_cast<T*>(dv), (int)bh,
+                     (int)s.sq, (int)s.sk, (int)s.d, causal, scale, scale * kLog2e, (int)nk);
+  return check_launch("ferrite_flash_attention_bwd_dkv");
+}
+
+// (dtype, aligned) dispatch of a wide launcher.
+#define FERRITE_WIDE(LAUNCH, dtype, aligned, ...)                                                       \
+  return (dtype) == FERRITE_BF16                                                                        \
+             ? ((aligned) ? LAUNCH<bf16, true>(__VA_ARGS__) : LAUNCH<bf16, false>(__VA_ARGS__))         \
+             : ((aligned) ? LAUNCH<float, true>(__VA_ARGS__) : LAUNCH<float, false>(__VA_ARGS__))
+
 // Dispatch over (dtype, padded D, aligned) for a launcher template L.
 #define FERRITE_DISPATCH(LAUNCH, s, dtype, aligned, ...)                                        \
   do {                                                                                          \
@@ -2328,6 +2794,7 @@ extern "C" int ferrite_hip_attn_fwd(const void* q, const void* k, const void* v,
   const bool al = d % (dtype == FERRITE_BF16 ? 8 : 4) == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
                   aligned16(o);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d > 256) FERRITE_WIDE(fwd_wide_launch, dtype, al, q, k, v, o, lse, s, causal, scale, st);
 #define FERRITE_DISPATCH_256(LAUNCH, T, aligned, ...) \
   return (aligned) ? LAUNCH<T, 256, true>(__VA_ARGS__) : LAUNCH<T, 256, false>(__VA_ARGS__)
   FERRITE_DISPATCH(fwd_launch, s, dtype, al, q, k, v, o, lse, s, causal, scale, st);
@@ -2368,6 +2835,7 @@ extern "C" int ferrite_hip_attn_bwd_dkv(const void* q, const void* k, const void
   const bool al = d % (dtype == FERRITE_BF16 ? 8 : 4) == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
                   aligned16(dout) && aligned16(dk) && aligned16(dv);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d > 128) FERRITE_WIDE(dkv_wide_launch, dtype, al, q, k, v, dout, lse, delta, dk, dv, s, causal, scale, st);
 #define FERRITE_DISPATCH_256(LAUNCH, T, aligned, ...) \
   return fail(FERRITE_ERR_INVALID_ARGUMENT, "unreachable head_dim")
   FERRITE_DISPATCH(dkv_launch, s, dtype, al, q, k, v, dout, lse, delta, dk, dv, s, causal, scale, st);
@@ -2476,6 +2944,7 @@ extern "C" int ferrite_hip_attn_bwd_dq(const void* q, const void* k, const void*
   const bool al = d % (dtype == FERRITE_BF16 ? 8 : 4) == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
                   aligned16(dout) && aligned16(dq);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d > 128) FERRITE_WIDE(dq_wide_launch, dtype, al, q, k, v, dout, lse, delta, dq, s, causal, scale, st);
 #define FERRITE_DISPATCH_256(LAUNCH, T, aligned, ...) \
   return fail(FERRITE_ERR_INVALID_ARGUMENT, "unreachable head_dim")
   FERRITE_DISPATCH(dq_launch, s, dtype, al, q, k, v, dout, lse, delta, dq, s, causal, scale, st);

@@ -237,9 +237,12 @@ int ferrite_hip_adamw(int64_t n_tensors, void* const* params, const void* const*
  * Flash attention forward (flash_attention.py:91-175).
  * q: [B, H, Sq, D]; k, v: [B, H, Sk, D]; o: [B, H, Sq, D], all of `dtype`.
  * lse: f32 [B, H, Sq] = logsumexp_j(scale * q_i . k_j) over the visible keys.
- * causal != 0 masks key j > query i and requires Sq == Sk. Supported head dims:
- * D <= 128 and D == 256 (inputs of other D <= 128 are zero-padded inside the
- * kernel). Sq, Sk >= 1; Sq and Sk need not be multiples of any tile size.
+ * causal != 0 masks key j > query i and requires Sq == Sk. Supported head dims
+ * (those the reference's _validate accepts, flash_attention.py:341-343): any
+ * D <= 128 (zero-padded inside the kernel to 64 or 128) and any multiple of 128
+ * (D > 256 runs slab-wise: 128 output columns per workgroup, the scores
+ * recomputed per slab). The same holds for every backward entry point below.
+ * Sq, Sk >= 1; Sq and Sk need not be multiples of any tile size.
  */
 int ferrite_hip_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t b, int64_t h,
                          int64_t sq, int64_t sk, int64_t d, int dtype, int causal, float scale, void* stream);

@@ -86,10 +86,14 @@ def test_abi_argument_checks_return_codes():
     # causal needs sq == sk
     assert lib.ferrite_hip_attn_fwd(1, 1, 1, 1, 1, 1, 1, 128, 256, 64, _hip.BF16, 1, 0.125, None) == 1
     assert "sq == sk" in _hip.last_error()
-    # unsupported head dims
-    assert lib.ferrite_hip_attn_fwd(1, 1, 1, 1, 1, 1, 1, 128, 128, 384, _hip.BF16, 1, 0.1, None) == 1
-    assert lib.ferrite_hip_attn_bwd_dq(1, 1, 1, 1, 1, 1, 1, 1, 1, 128, 128, 256, _hip.BF16, 1, 0.1, None) == 1
-    assert "backward" in _hip.last_error()
+    # head dims the reference refuses (above 128 and not a multiple of 128) are refused here too;
+    # every multiple of 128 is taken, forward and backward (flash_attention.py:341-343)
+    for d in (200, 320, 136):
+        assert lib.ferrite_hip_attn_fwd(1, 1, 1, 1, 1, 1, 1, 128, 128, d, _hip.BF16, 1, 0.1, None) == 1
+        assert "multiple of 128" in _hip.last_error()
+        assert lib.ferrite_hip_attn_bwd_dq(1, 1, 1, 1, 1, 1, 1, 1, 1, 128, 128, d, _hip.BF16, 1, 0.1, None) == 1
+        assert lib.ferrite_hip_attn_bwd_dkv(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 128, 128, d, _hip.BF16, 1, 0.1, None) == 1
+        assert "multiple of 128" in _hip.last_error()
     assert lib.ferrite_hip_add_rmsnorm(None, None, None, None, None, 4, 0, 1, 1, 1e-6, None) == 1
     # rows == 0 is a valid no-op and launches nothing
     assert lib.ferrite_hip_rmsnorm(None, None, None, 0, 16, 1, 1, 1e-6, None) == 0

@@ -52,9 +52,27 @@ def test_forward_bf16(dev):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("s,d,bs", [(256, 128, BlockSizes()), (384, 64, BlockSizes(128, 128, 64, 128))])
+@pytest.mark.parametrize("s,d", [(256, 384), (128, 512), (256, 1024)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_forward_wide_head_dims(dev, causal, s, d, dtype):
+    """Head dims above 256 (any multiple of 128 passes the reference's _validate,
+    flash_attention.py:341-343): the slab-wise forward, f32 at 2e-5 and bf16 at 2e-2; lse to 1e-3."""
+    q, k, v = _qkv(60 + d, (1, 2, s, d), dtype)
+    qt, kt, vt = (to_dev(a, dtype, dev) for a in (q, k, v))
+    out, lse = _flash_forward(qt, kt, vt, causal=causal, scale=d ** -0.5)
+    ref, lse_ref = oatt.forward(q, k, v, causal=causal)
+    tol = 2e-5 if dtype == "f32" else 2e-2
+    np.testing.assert_allclose(to_np(out), ref, atol=tol, rtol=tol)
+    assert max_abs(to_np(lse), lse_ref) <= 1e-3
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("s,d,bs", [(256, 128, BlockSizes()), (384, 64, BlockSizes(128, 128, 64, 128)),
+                                    (256, 256, BlockSizes(64, 128)), (256, 384, BlockSizes()),
+                                    (128, 512, BlockSizes())])
 def test_backward_matches_reference(dev, causal, s, d, bs):
-    """tests/test_flash_attention.py:35-47 (f32, 5e-4)."""
+    """tests/test_flash_attention.py:35-47 (f32, 5e-4), plus the head dims above 128 that the
+    reference's _validate accepts (multiples of 128; its kernels are generic in d)."""
     q, k, v = _qkv(6, (1, 2, s, d), "f32")
     do = normal(9, q.shape)
     _, dq, dk, dv = _grads(q, k, v, do, dev, "f32", causal, bs)
@@ -62,9 +80,11 @@ def test_backward_matches_reference(dev, causal, s, d, bs):
         np.testing.assert_allclose(a, b, atol=5e-4, rtol=5e-4, err_msg=f"d{name}")
 
 
-def test_backward_bf16_is_close(dev):
-    """tests/test_flash_attention.py:50-58: loss = sum(f32(out)^2), relative Frobenius < 5e-2."""
-    q, k, v = _qkv(10, (1, 2, 256, 128), "bf16")
+@pytest.mark.parametrize("d", [128, 256, 512])
+def test_backward_bf16_is_close(dev, d):
+    """tests/test_flash_attention.py:50-58: loss = sum(f32(out)^2), relative Frobenius < 5e-2
+    (d = 128 as there; 256 and 512 run the slab-wise backward)."""
+    q, k, v = _qkv(10, (1, 2, 256, d), "bf16")
     qt, kt, vt = (to_dev(a, "bf16", dev).requires_grad_() for a in (q, k, v))
     (flash_attention(qt, kt, vt, causal=True).float() ** 2).sum().backward()
     o, _ = oatt.forward(q, k, v, causal=True)
@@ -208,6 +228,9 @@ def _abi_case(dev, b, h, sq, sk, d, dtype, causal, seed, scale, fused=False):
     (1, 2, 150, 150, 30, "f32", True),      # f32 unaligned path
     (1, 1, 33, 33, 128, "f32", True),
     (1, 1, 1, 1, 64, "bf16", True),         # single token
+    (1, 2, 200, 200, 256, "bf16", True),    # wide head dims: ragged, slab-wise dQ and dK/dV
+    (1, 1, 100, 260, 384, "f32", False),    # three slabs, non-causal, sk != sq
+    (2, 1, 77, 77, 512, "bf16", True),      # four slabs
 ])
 @pytest.mark.parametrize("scale", ["default", 0.37])
 @pytest.mark.parametrize("fused", [False, True], ids=["delta_pass", "delta_in_dq"])
