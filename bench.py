@@ -165,56 +165,91 @@ def bench_attention(b, h, t, d, steps, warmup, seed=7):
     }
 
 
-def bench_rmsnorm(rows, dim, steps, warmup, sets=24):
-    """add+RMSNorm over `sets` rotating buffer sets (24 x 33.5 MB = 805 MB > the 256 MB MALL),
-    launched through a captured HIP graph so host launch cost does not pace the 4 us kernels."""
+def _rmsnorm_sets(rows, dim, sets, seed=0):
     import torch
 
-    from ferrite import _hip
-
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev).manual_seed(0)
+    g = torch.Generator(device=dev).manual_seed(seed)
     w = (1 + 0.1 * torch.randn(dim, device=dev, generator=g)).to(torch.bfloat16)
     bufs = []
     for _ in range(sets):
         x = torch.randn(rows, dim, device=dev, generator=g).to(torch.bfloat16)
         r = torch.randn(rows, dim, device=dev, generator=g).to(torch.bfloat16)
         bufs.append((x, r, torch.empty_like(x), torch.empty_like(x)))
-    lib = _hip.lib()
+    return w, bufs
 
-    def launch_all():
-        st = torch.cuda.current_stream().cuda_stream
-        for x, r, hh, y in bufs:
-            _hip.check(lib.ferrite_hip_add_rmsnorm(x.data_ptr(), r.data_ptr(), w.data_ptr(), hh.data_ptr(), y.data_ptr(),
-                                                   rows, dim, _hip.BF16, _hip.BF16, 1e-6, st), "add_rmsnorm")
+
+def _graph_time(launch_all, iters, warmup, per):
+    """Seconds per launch of `launch_all` (which enqueues `per` launches) replayed from a captured graph."""
+    import torch
 
     launch_all()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         launch_all()
-    per_replay = _events_time(graph.replay, max(steps, 10), warmup)
-    t = per_replay / sets
-    nbytes = 4 * rows * dim * 2 + dim * 2  # read x, r, w; write h, y
-    # Same kernels launched eagerly from Python, for reference.
-    t_eager = _events_time(launch_all, max(steps // 2, 5), 2) / sets
+    t = _events_time(graph.replay, iters, warmup) / per
+    del graph
+    return t
 
-    # A plain device copy moving the same bytes (x -> h, r -> y), replayed the same way: the
-    # bandwidth a streaming kernel of this size gets on this part.
-    def copy_all():
+
+def bench_rmsnorm(rows, dim, steps, warmup, sets=24):
+    """add+RMSNorm over `sets` rotating buffer sets (24 x 33.5 MB = 805 MB > the 256 MB MALL),
+    launched through a captured HIP graph so host launch cost does not pace the 4 us kernels.
+
+    Beside it, the streaming ceiling of this part for the same access pattern: the library's
+    non-temporal two-buffer copy (ferrite_hip_stream_copy2: x -> h and r -> y, same bytes, same
+    rotation and replay), and both kernels again at 16x the size (537 MB per launch, 3 sets), where
+    the per-launch ramp no longer counts and the rate is the HBM read+write stream's."""
+    import torch
+
+    from ferrite import _hip
+
+    lib = _hip.lib()
+    nbytes = 4 * rows * dim * 2 + dim * 2  # read x, r, w; write h, y
+    copy_bytes = 4 * rows * dim * 2
+
+    def norm_all(w, bufs, n):
+        st = torch.cuda.current_stream().cuda_stream
+        for x, r, hh, y in bufs:
+            _hip.check(lib.ferrite_hip_add_rmsnorm(x.data_ptr(), r.data_ptr(), w.data_ptr(), hh.data_ptr(), y.data_ptr(),
+                                                   n, dim, _hip.BF16, _hip.BF16, 1e-6, st), "add_rmsnorm")
+
+    def copy_all(bufs, n):
+        st = torch.cuda.current_stream().cuda_stream
+        for x, r, hh, y in bufs:
+            _hip.check(lib.ferrite_hip_stream_copy2(x.data_ptr(), r.data_ptr(), hh.data_ptr(), y.data_ptr(),
+                                                    n * dim * 2, st), "stream_copy2")
+
+    w, bufs = _rmsnorm_sets(rows, dim, sets)
+    t = _graph_time(lambda: norm_all(w, bufs, rows), max(steps, 10), warmup, sets)
+    t_eager = _events_time(lambda: norm_all(w, bufs, rows), max(steps // 2, 5), 2) / sets
+    t_copy = _graph_time(lambda: copy_all(bufs, rows), max(steps, 10), warmup, sets)
+
+    def torch_copy_all():
         for x, r, hh, y in bufs:
             hh.copy_(x)
             y.copy_(r)
 
-    copy_all()
-    torch.cuda.synchronize()
-    cgraph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(cgraph):
-        copy_all()
-    t_copy = _events_time(cgraph.replay, max(steps, 10), warmup) / sets
-    return {"shape": [rows, dim], "us": t * 1e6, "gbs": nbytes / t / 1e9, "bytes": nbytes,
-            "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS, "buffer_sets": sets, "eager_us": t_eager * 1e6,
-            "copy_same_bytes_us": t_copy * 1e6, "copy_same_bytes_gbs": (4 * rows * dim * 2) / t_copy / 1e9}
+    t_tcopy = _graph_time(torch_copy_all, max(steps, 10), warmup, sets)
+    del bufs
+    big_rows, big_sets = 16 * rows, 3
+    w2, big = _rmsnorm_sets(big_rows, dim, big_sets, seed=1)
+    t_big = _graph_time(lambda: norm_all(w2, big, big_rows), 10, 2, big_sets)
+    t_big_copy = _graph_time(lambda: copy_all(big, big_rows), 10, 2, big_sets)
+    del big
+    torch.cuda.empty_cache()
+    big_bytes, big_copy_bytes = 4 * big_rows * dim * 2 + dim * 2, 4 * big_rows * dim * 2
+    ceiling = max(copy_bytes / t_copy, big_copy_bytes / t_big_copy, big_bytes / t_big) / 1e9
+    gbs = nbytes / t / 1e9
+    return {"shape": [rows, dim], "us": t * 1e6, "gbs": gbs, "bytes": nbytes,
+            "frac_hbm": gbs / PEAK_HBM_GBS, "buffer_sets": sets, "eager_us": t_eager * 1e6,
+            "stream_copy_same_bytes_us": t_copy * 1e6, "stream_copy_same_bytes_gbs": copy_bytes / t_copy / 1e9,
+            "torch_copy_same_bytes_us": t_tcopy * 1e6, "torch_copy_same_bytes_gbs": copy_bytes / t_tcopy / 1e9,
+            "x16_size": {"shape": [big_rows, dim], "add_rmsnorm_us": t_big * 1e6,
+                         "add_rmsnorm_gbs": big_bytes / t_big / 1e9, "stream_copy_us": t_big_copy * 1e6,
+                         "stream_copy_gbs": big_copy_bytes / t_big_copy / 1e9},
+            "measured_ceiling_gbs": ceiling, "frac_of_measured_ceiling": gbs / ceiling}
 
 
 def bench_matmul(steps, warmup):

@@ -265,10 +265,14 @@ int launch(const void* x, const void* r, const void* w, void* h, void* y, int64_
       hipLaunchKernelGGL((rmsnorm_rows_kernel<TX, TW, RES, V, DEPTH, false>), pgrid(DEPTH), block, 0, stream, xp,    \
                          rp, wp, hp, yp, rows, (int)dim, inv_dim, eps);                                            \
   } while (0)
+    // Rows of up to 1024 elements: two rows in flight per wave and two workgroups per
+    // CU where the rows allow (at [4096, 1024]: 6.73 -> 6.58 us; at [65536, 1024]
+    // 100.1 -> 92.4 us, the rate of a plain two-buffer streaming copy; four rows
+    // per wave with one workgroup per CU, or one row with four, are slower).
     if (vpl <= 1)
       FERRITE_RMS_CASE(1, 4);
     else if (vpl <= 2)
-      FERRITE_RMS_CASE(2, 4);
+      FERRITE_RMS_CASE(2, 2);
     else if (vpl <= 4)
       FERRITE_RMS_CASE(4, 2);
     else
@@ -551,6 +555,36 @@ int bwd_dispatch_out(const void* h, const void* w, const void* dy, const void* d
 }
 
 // ---------------------------------------------------------------------------
+// Streaming copy of two buffers (a -> a_out, b -> b_out): add+RMSNorm's access
+// pattern (two 16-byte non-temporal loads and two stores per lane and 2 KB
+// unit) with no arithmetic, to measure the HBM ceiling a kernel of that shape
+// can reach. Persistent grid: wave w copies units w, w + waves, ... (one unit =
+// 2 KB of each buffer, two 16-byte words per lane).
+// ---------------------------------------------------------------------------
+constexpr int kCopyUnit = 2048;
+
+__global__ __launch_bounds__(256) void stream_copy2_kernel(const char* __restrict__ a, const char* __restrict__ b,
+                                                           char* __restrict__ a_out, char* __restrict__ b_out,
+                                                           int64_t units, int64_t tail_words) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); u < units; u += nwaves) {
+    const int64_t o0 = u * kCopyUnit + lane * 16, o1 = o0 + 1024;
+    const u32x4 a0 = ld16_nt(a + o0), a1 = ld16_nt(a + o1), b0 = ld16_nt(b + o0), b1 = ld16_nt(b + o1);
+    st16_nt(a_out + o0, a0);
+    st16_nt(a_out + o1, a1);
+    st16_nt(b_out + o0, b0);
+    st16_nt(b_out + o1, b1);
+  }
+  // The last partial unit: 16-byte words, one per thread of block 0.
+  if (blockIdx.x == 0 && threadIdx.x < tail_words) {
+    const int64_t o = units * kCopyUnit + (int64_t)threadIdx.x * 16;
+    st16_nt(a_out + o, ld16_nt(a + o));
+    st16_nt(b_out + o, ld16_nt(b + o));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Scratch of the allocation-free backward (ferrite_hip_rmsnorm_bwd_noalloc):
 // the partial dw rows (and inverse RMS per row) live in this file-scope device
 // array instead of a caller's workspace. Each device that loads the library
@@ -655,4 +689,22 @@ extern "C" int ferrite_hip_rmsnorm_bwd_noalloc(const void* h, const void* weight
                                                void* stream) {
   return ferrite::bwd_entry("ferrite_hip_rmsnorm_bwd_noalloc", h, weight, dy, dh_direct, dh, dweight, nullptr, true,
                             rows, dim, x_dtype, w_dtype, dh_dtype, eps, stream);
+}
+
+extern "C" int ferrite_hip_stream_copy2(const void* a, const void* b, void* a_out, void* b_out, int64_t bytes,
+                                        void* stream) {
+  using namespace ferrite;
+  if (bytes < 0 || bytes % 16 != 0)
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_stream_copy2: bytes must be a multiple of 16");
+  if (bytes == 0) return FERRITE_OK;
+  auto aligned16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (!a || !b || !a_out || !b_out || !aligned16(a) || !aligned16(b) || !aligned16(a_out) || !aligned16(b_out))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_stream_copy2: null or unaligned pointer");
+  const int64_t units = bytes / kCopyUnit, tail = (bytes % kCopyUnit) / 16;
+  // 512 workgroups (two per CU) measured best at 33.5 MB and at 537 MB per buffer pair.
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(512, cdiv(units, 4)));
+  hipLaunchKernelGGL(stream_copy2_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const char*>(a), static_cast<const char*>(b), static_cast<char*>(a_out),
+                     static_cast<char*>(b_out), units, tail);
+  return check_launch("ferrite_hip_stream_copy2");
 }

@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_f32, _vp],
     ),
+    "ferrite_hip_stream_copy2": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _vp]),
     "ferrite_hip_matmul": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _vp]),
     "ferrite_hip_matmul_workspace": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_int]),
     "ferrite_hip_matmul_ex": (

@@ -123,6 +123,15 @@ int ferrite_hip_rmsnorm_bwd_noalloc(const void* h, const void* weight, const voi
                                     int dh_dtype, float eps, void* stream);
 
 /*
+ * a_out <- a and b_out <- b, `bytes` each, with 16-byte non-temporal loads and
+ * stores: add+RMSNorm's access pattern (two streams in, two out) without its
+ * arithmetic. No counterpart in the reference; it measures the HBM ceiling for
+ * HBM-bound kernels of that shape (bench.py reports it beside add+RMSNorm).
+ * bytes % 16 == 0; all pointers 16-byte aligned; the buffers must not overlap.
+ */
+int ferrite_hip_stream_copy2(const void* a, const void* b, void* a_out, void* b_out, int64_t bytes, void* stream);
+
+/*
  * out[M, N] = x[M, K] @ y[K, N] with f32 accumulation (matmul.py:27-38, :52-86).
  * in_dtype FERRITE_BF16 uses bf16 MFMA; FERRITE_F32 uses fp32 MFMA (true fp32
  * products, the reference's Precision.HIGHEST, _compat.py:17-25). Ragged shapes

@@ -25,7 +25,7 @@ def _declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     declared = _declared_symbols()
-    assert len(declared) == 26
+    assert len(declared) == 27
     out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH], capture_output=True, text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s(\w+)", out))
     missing = [s for s in declared if s not in exported]
@@ -95,6 +95,10 @@ def test_abi_argument_checks_return_codes():
         assert lib.ferrite_hip_attn_bwd_dkv(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 128, 128, d, _hip.BF16, 1, 0.1, None) == 1
         assert "multiple of 128" in _hip.last_error()
     assert lib.ferrite_hip_add_rmsnorm(None, None, None, None, None, 4, 0, 1, 1, 1e-6, None) == 1
+    # the streaming copy: size and alignment checks; zero bytes is a no-op
+    assert lib.ferrite_hip_stream_copy2(None, None, None, None, 0, None) == 0
+    assert lib.ferrite_hip_stream_copy2(16, 16, 16, 16, 24, None) == 1 and "multiple of 16" in _hip.last_error()
+    assert lib.ferrite_hip_stream_copy2(16, 8, 16, 16, 32, None) == 1 and "unaligned" in _hip.last_error()
     # rows == 0 is a valid no-op and launches nothing
     assert lib.ferrite_hip_rmsnorm(None, None, None, 0, 16, 1, 1, 1e-6, None) == 0
 

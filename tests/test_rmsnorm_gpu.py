@@ -213,3 +213,23 @@ def test_bf16_autograd_uses_the_kernel(dev):
     for g in (xt.grad, rt.grad):
         assert max_abs(to_np(g), ref_dh) <= 2e-2
     assert max_abs(to_np(wt.grad), ref_dw) <= 1e-3 * np.abs(ref_dw).max()
+
+
+@pytest.mark.parametrize("nbytes", [16, 2048, 2048 * 1000 + 48, 4096 * 1024 * 2])
+def test_stream_copy2_is_exact(dev, nbytes):
+    """ferrite_hip_stream_copy2 (the streaming ceiling bench.py measures beside add+RMSNorm) copies
+    both buffers bitwise, partial 2 KB units included, and writes nothing past them."""
+    from ferrite import _hip
+
+    n = nbytes // 4
+    g = torch.Generator(device=dev).manual_seed(5)
+    a = torch.randint(-2**31, 2**31 - 1, (n,), generator=g, device=dev, dtype=torch.int32)
+    b = torch.randint(-2**31, 2**31 - 1, (n,), generator=g, device=dev, dtype=torch.int32)
+    ao = torch.full((n + 64,), 7, device=dev, dtype=torch.int32)
+    bo = torch.full((n + 64,), 7, device=dev, dtype=torch.int32)
+    rc = _hip.lib().ferrite_hip_stream_copy2(a.data_ptr(), b.data_ptr(), ao.data_ptr(), bo.data_ptr(), nbytes,
+                                             _hip.stream_of(a))
+    _hip.check(rc, "stream_copy2")
+    torch.cuda.synchronize()
+    assert torch.equal(ao[:n], a) and torch.equal(bo[:n], b)
+    assert bool((ao[n:] == 7).all()) and bool((bo[n:] == 7).all())
