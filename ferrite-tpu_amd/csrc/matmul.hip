@@ -78,10 +78,10 @@ struct Gemm {
                                                  int64_t ld) {
     vec v;
     if constexpr (ALIGNED) {
-      if (row < rows && col < cols)
-        v = *reinterpret_cast<const vec*>(p + row * ld + col);
-      else
-        for (int e = 0; e < kVec; ++e) v[e] = (T)0.f;
+      // Zero, then the load when in range (a zeroing loop in the else branch was kept
+      // as a scratch array by the compiler: 48 bytes per lane of spill).
+      v = __builtin_bit_cast(vec, u32x4{0u, 0u, 0u, 0u});
+      if (row < rows && col < cols) v = *reinterpret_cast<const vec*>(p + row * ld + col);
     } else {
 #pragma unroll
       for (int e = 0; e < kVec; ++e) v[e] = (row < rows && col + e < cols) ? p[row * ld + col + e] : (T)0.f;
@@ -125,8 +125,14 @@ struct Gemm {
       for (int e = 0; e < kVec; ++e) {
         const int n = cg * kVec + e;
         if constexpr (sizeof(T) == 2) {
-          bf16x4 w4 = {s.b[j][0][e], s.b[j][1][e], s.b[j][2][e], s.b[j][3][e]};
-          *reinterpret_cast<bf16x4*>(bs + lds_off<T>(n, kg * 4)) = w4;
+          // Element e of the four k-rows, gathered from 32-bit words with shifts and
+          // masks (element extraction from bf16 vectors went through scratch memory).
+          uint32_t w[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) w[r] = __builtin_bit_cast(u32x4, s.b[j][r])[e >> 1];
+          const uint32_t lo = (e & 1) ? (w[0] >> 16) | (w[1] & 0xffff0000u) : (w[0] & 0xffffu) | (w[1] << 16);
+          const uint32_t hi = (e & 1) ? (w[2] >> 16) | (w[3] & 0xffff0000u) : (w[2] & 0xffffu) | (w[3] << 16);
+          *reinterpret_cast<u32x2*>(bs + lds_off<T>(n, kg * 4)) = u32x2{lo, hi};
         } else {
           f32x4 w4 = {s.b[j][0][e], s.b[j][1][e], s.b[j][2][e], s.b[j][3][e]};
           *reinterpret_cast<f32x4*>(bs + lds_off<T>(n, kg * 4)) = w4;
@@ -715,8 +721,12 @@ int launch_gemm_dma_t(const void* x, const void* y, void* out, int64_t M, int64_
   constexpr int kLds = 2 * (OperandTile<!XT>::kBytes + OperandTile<YT>::kBytes);
   const dim3 grid((unsigned)(tiles_m * tiles_n * slices));
   if (slices == 1) {
-    const bool w4 = use_four_waves(M, N, K);
-    auto kern = w4 ? gemm_dma_kernel<TO, XT, YT, 256, 2, EPI, 4> : gemm_dma_kernel<TO, XT, YT, 256, 2, EPI, 8>;
+    // The GELU epilogues keep eight waves: with four, the 128 x 128 accumulators of a wave
+    // and the epilogue's operands do not fit its registers (12 bytes per lane spilled).
+    const bool w4 = EPI == kEpiNone && use_four_waves(M, N, K);
+    auto kern = gemm_dma_kernel<TO, XT, YT, 256, 2, EPI, 8>;
+    if constexpr (EPI == kEpiNone)
+      if (w4) kern = gemm_dma_kernel<TO, XT, YT, 256, 2, EPI, 4>;
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
     hipLaunchKernelGGL(kern, grid, dim3(w4 ? 256 : G::kThreads), kLds, stream, static_cast<const bf16*>(x),
                        static_cast<const bf16*>(y), static_cast<TO*>(out), (int)M, (int)N, (int)K, (int)tiles_m,
@@ -781,8 +791,10 @@ extern "C" int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, in
                 "ferrite_hip_matmul: transposed operands need bf16, K % 64 == 0, N % 8 == 0, M % 8 == 0 for a "
                 "transposed x, and 16-byte aligned pointers");
   if (in_dtype == FERRITE_BF16) {
-    if (out_dtype == FERRITE_BF16) return launch_gemm<bf16, bf16, 256, 256, 64, 2, 2>(x, y, out, m, n, k, s);
-    return launch_gemm<bf16, float, 256, 256, 64, 2, 2>(x, y, out, m, n, k, s);
+    // Shapes the DMA kernel does not take (ragged K, unaligned rows or pointers): four waves
+    // of 64 x 64 outputs per 128 x 128 tile (256 x 256 tiles spilled 48 bytes per lane).
+    if (out_dtype == FERRITE_BF16) return launch_gemm<bf16, bf16, 128, 128, 64, 2, 2>(x, y, out, m, n, k, s);
+    return launch_gemm<bf16, float, 128, 128, 64, 2, 2>(x, y, out, m, n, k, s);
   }
   // f32: 128 x 128 tiles of four waves reach ~80% of the fp32 MFMA peak at 4096^3; a
   // problem with fewer such tiles than CUs (1000^3 has 64) runs 64 x 64 tiles of two
