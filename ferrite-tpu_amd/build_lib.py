@@ -33,6 +33,15 @@ HIPCC_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
+# Per-source additions. attention.hip: MFMA results in VGPRs rather than AGPRs. The backward's
+# softmax gradient reads the S and dP accumulators on the VALU; with AGPR accumulators every
+# read is an extra v_accvgpr_read (a quarter of dK/dV's VALU instructions). Measured A/B on one
+# MI355X, outputs bitwise equal: dK/dV 166.8 -> 159.9 us at 4x16x2048x128 and 199.7 -> 182.9 us
+# at 1x8x8192x64; the forward and dQ kernels (already all-VGPR) are unchanged.
+SOURCE_FLAGS = {
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
 
 def _hipcc() -> str:
     for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
@@ -47,7 +56,7 @@ def _sources() -> list[str]:
 
 def _compile(src: str, verbose: bool, save_temps: str | None) -> str:
     obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     cwd = None
     if save_temps:  # temporaries (including the gfx950 .s) land in the working directory
         os.makedirs(save_temps, exist_ok=True)
