@@ -520,6 +520,7 @@ struct PpKTile {
   static __host__ __device__ constexpr int block_off(int b) { return b * kStride; }
   // Row that lane L of the instruction filling block b loads.
   static __host__ __device__ constexpr int dma_row(int b, int L) { return b + (L / kChunks) * kBlocks; }
+  static __host__ __device__ constexpr int dma_chunk(int L) { return L % kChunks; }
   static __device__ __forceinline__ bool dma_lane(int) { return true; }
 };
 
@@ -543,6 +544,7 @@ struct PpVTile {
   static __host__ __device__ constexpr int dma_row(int b, int L) {
     return (b & 3) + 4 * (L / kChunks) + 4 * kRowsPerBlock * (b >> 2);
   }
+  static __host__ __device__ constexpr int dma_chunk(int L) { return L % kChunks; }
   static __device__ __forceinline__ bool dma_lane(int) { return true; }
 };
 
@@ -568,7 +570,7 @@ struct PpDma {
     const int lane = threadIdx.x & 63;
     const int r = Layout::dma_row(gw, lane);
     const int src = PERM ? perm_src(r) : r;
-    voff = Layout::dma_lane(lane) ? (uint32_t)((src * d + (lane % Layout::kChunks) * 8) * 2) : 0x80000000u;
+    voff = Layout::dma_lane(lane) ? (uint32_t)((src * d + Layout::dma_chunk(lane) * 8) * 2) : 0x80000000u;
   }
 
   // Buffer descriptor of rows [r0, nrows) of `base` (rows past nrows read as zeros).
@@ -1959,6 +1961,7 @@ struct BwdTile {
   // lanes 32-63 of its DMA instruction are switched off (they write zeros
   // into the unused half).
   static __host__ __device__ constexpr int dma_row(int b, int L) { return b + 16 * (L / kChunks); }
+  static __host__ __device__ constexpr int dma_chunk(int L) { return L % kChunks; }
   static __device__ __forceinline__ bool dma_lane(int L) { return L / kChunks < 4; }
   // Row fragment (physical rows 32 half + l32, bytes 32 kk + 16 g): lane base
   // plus row_at(half, kk).
@@ -1971,14 +1974,73 @@ struct BwdTile {
   }
   static __host__ __device__ constexpr int tr_at(int half, int h, int u) { return off(32 * half + 16 * h, 64 * u); }
   static constexpr int kTrHi = off(8, 0);
+  // A lane's fragment addresses: a base plus a constant.
+  struct Bases {
+    int r, t;
+    __device__ __forceinline__ explicit Bases(int lane) : r(row_base(lane)), t(tr_base(lane)) {}
+  };
+  static __device__ __forceinline__ int row(const Bases& b, int half, int kk) { return b.r + row_at(half, kk); }
+  static __device__ __forceinline__ int tr(const Bases& b, int half, int h, int u) { return b.t + tr_at(half, h, u); }
+};
+
+// Compact tile for D = 64 (128-byte rows): 8 KB of rows in 8 blocks of 8
+// consecutive physical rows (row p in block p / 8 at position p % 8), the
+// 16-byte chunks of each row XOR-swizzled by swz8(p % 8), and 128 bytes
+// between blocks (a 1152-byte stride). A 16-lane pass of row reads (16
+// consecutive rows, one chunk) then meets 16 different 16-byte bank slots,
+// and a 32-lane pass of transposed reads (four consecutive rows, 64 bytes
+// each) 32 different 8-byte bank pairs; a CPU model of the lane addresses
+// confirms both patterns conflict-free. Every DMA lane carries data (BwdTile
+// at D = 64 leaves half of each 1 KB block, and half of each DMA instruction,
+// empty), so a tile takes 8 DMA instructions instead of 16, and a 4-slot ring
+// of Q, dO and statistics takes 79 KB: two workgroups share a CU. Rows are in
+// the permuted MFMA output order, as in BwdTile. The XOR makes the chunk
+// offset lane-dependent, so a lane keeps one base per 32-byte column (row
+// reads) and per 64-byte output tile (transposed reads).
+struct BwdTileC64 {
+  static constexpr int kRowBytes = 128;
+  static constexpr int kChunks = 8;
+  static constexpr int kBlocks = 8;
+  static constexpr int kStride = 1024 + 128;
+  static constexpr int kBytes = 7 * kStride + 1024;
+  static __host__ __device__ constexpr int swz8(int t) { return (t & 1) | ((t & 2) << 1) | ((t & 4) >> 1); }
+  static __host__ __device__ constexpr int off(int p, int byte) {
+    return (p >> 3) * kStride + (p & 7) * kRowBytes + 16 * ((byte >> 4) ^ swz8(p & 7)) + (byte & 15);
+  }
+  static __host__ __device__ constexpr int block_off(int b) { return b * kStride; }
+  // Lane L of the instruction filling block b writes LDS bytes 16 L .. 16 L + 15 of the block:
+  // physical row 8 b + L / 8, physical chunk L % 8, which holds logical chunk (L % 8) ^ swz8(L / 8).
+  static __host__ __device__ constexpr int dma_row(int b, int L) { return 8 * b + L / 8; }
+  static __host__ __device__ constexpr int dma_chunk(int L) { return (L % 8) ^ swz8(L / 8); }
+  static __device__ __forceinline__ bool dma_lane(int) { return true; }
+  static constexpr int kTrHi = kStride;  // eight physical rows further: the next block
+  struct Bases {
+    int r[4], t[2];
+    __device__ __forceinline__ explicit Bases(int lane) {
+      const int l32 = lane & 31, g = lane >> 5;
+      // Row fragment: physical row 32 half + l32, logical chunk 2 kk + g.
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) r[kk] = off(l32, 32 * kk + 16 * g);
+      // Transposed fragment: physical row 32 half + 16 h + 4 g + (lane & 15) / 4,
+      // logical byte 64 u + 32 ((lane >> 4) & 1) + 8 (lane & 3).
+      const int tp = 4 * g + ((lane & 15) >> 2);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) t[u] = off(tp, 64 * u + 32 * ((lane >> 4) & 1) + 8 * (lane & 3));
+    }
+  };
+  static __device__ __forceinline__ int row(const Bases& b, int half, int kk) { return b.r[kk] + 4 * half * kStride; }
+  static __device__ __forceinline__ int tr(const Bases& b, int half, int h, int u) {
+    return b.t[u] + (4 * half + 2 * h) * kStride;
+  }
 };
 
 template <int D>
 struct DkvPp {
   static constexpr int kWaves = 4, kThreads = 64 * kWaves;
   static constexpr int BKV = 32 * kWaves, BQ = 64, KS = D / 16, DT = D / 32;
-  typedef BwdTile<D> Tile;
+  typedef std::conditional_t<D == 64, BwdTileC64, BwdTile<D>> Tile;
   static constexpr int kSlots = 4;
+  static constexpr int kMinBlocks = D == 64 ? 2 : 1;  // workgroups per CU the LDS admits
   static constexpr int kStatBytes = 2048;  // lse at +0, delta at +1024: one DMA instruction each
   static constexpr int kSlotBytes = 2 * Tile::kBytes + kStatBytes;
   static constexpr int kLds = kSlots * kSlotBytes;
@@ -2012,12 +2074,13 @@ __device__ __forceinline__ void stat_dma(const float* base, int r0, int nrows, c
 // slot.
 // SAMEP: Q and dO share a row pitch (dense tensors), so one DMA descriptor serves both.
 template <int D, bool SAMEP = true>
-__global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+__global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                             const bf16* __restrict__ v, const bf16* __restrict__ dout,
                                                             const float* __restrict__ lse,
                                                             const float* __restrict__ delta, bf16* __restrict__ dk,
                                                             bf16* __restrict__ dv, int bh_count, int Sq, int Sk, int d,
-                                                            int causal, float scale, float scale_log2, AttnViews vw) {
+                                                            int causal, float scale, float scale_log2, AttnViews vw,
+                                                            int n_ktiles, int zig) {
   typedef DkvPp<D> F;
   typedef typename F::Tile Tile;
   constexpr int KS = F::KS, DT = F::DT;
@@ -2027,9 +2090,14 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
   constexpr int kTileDma = 2 * F::kDma + 2;
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
-  // Heaviest (first) key blocks first.
+  // Heaviest (first) key blocks first. zig (a grid resident all at once, two
+  // workgroups per CU): the second half of the grid takes the light blocks in
+  // rising order, so block b and block b + grid / 2, which share a CU, pair a
+  // long and a short causal sweep.
   const int bh = blockIdx.x % bh_count;
-  const int kt = (int)(blockIdx.x / bh_count);
+  const int blk = (int)(blockIdx.x / bh_count);
+  const int first_half = n_ktiles - n_ktiles / 2;
+  const int kt = !zig || blk < first_half ? blk : n_ktiles - 1 - (blk - first_half);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
@@ -2048,16 +2116,15 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
 
   // Query tiles first .. first + nt - 1 (tile t in ring slot t % kSlots),
   // halves 0 .. nh - 1 (half x: tile x / 2, queries 32 (x % 2) .. of it).
-  // At D = 128 a sweep of fewer than three tiles is run as three: the tiles
-  // past the end of the queries arrive as zeros (Q, dO, lse and delta all 0),
-  // so their p = exp2(0) = 1 meets dO = 0 in dV and dS = p (0 - 0) = 0 in dK,
-  // and they add exact zeros. One code path for every length keeps the
-  // register allocation of the pipeline from splitting over the short cases,
-  // which cost 38 spilled registers there. D = 64 has registers to spare and
-  // keeps separate short paths (the padded form measured 2-3% slower).
-  constexpr bool kShortPaths = D != 128;
+  // A sweep of fewer than three tiles is run as three: the tiles past the end
+  // of the queries arrive as zeros (Q, dO, lse and delta all 0), so their
+  // p = exp2(0) = 1 meets dO = 0 in dV and dS = p (0 - 0) = 0 in dK, and they
+  // add exact zeros. One code path for every length keeps the register
+  // allocation of the pipeline from splitting over short cases (38 spilled
+  // registers at D = 128 with separate short paths; at D = 64 the single path
+  // is what fits two waves per SIMD).
   const int first = causal ? k0 / F::BQ : 0;
-  const int nt = max((Sq + F::BQ - 1) / F::BQ - first, kShortPaths ? 1 : 3);
+  const int nt = max((Sq + F::BQ - 1) / F::BQ - first, 3);
   const int nh = 2 * nt;
 
   bf16x8 kf[KS], vf[KS];
@@ -2099,8 +2166,7 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
       dka[u][r] = 0.f;
       dva[u][r] = 0.f;
     }
-  const int rbase = Tile::row_base(lane);
-  const int tbase = Tile::tr_base(lane);
+  const typename Tile::Bases tb(lane);
 
   f32x16 sa, dpa;               // S and dP of one half (register r: query 16 g + r, key kvrow)
   bf16x8 pf[2][2], dsf[2][2];  // [half parity][8-query chunk]: P and dS fragments
@@ -2141,10 +2207,8 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
     auto read = [&](int f) -> bf16x8 {
       int i;
       if (which(f, i))
-        return *reinterpret_cast<const bf16x8*>(sl_n + ((i & 1) ? Tile::kBytes : 0) + rbase +
-                                                Tile::row_at(half_n, i >> 1));
-      return tr_frag(sl_p + ((i & 1) ? 0 : Tile::kBytes) + tbase + Tile::tr_at(half_p, (i >> 1) & 1, i >> 2),
-                     Tile::kTrHi);
+        return *reinterpret_cast<const bf16x8*>(sl_n + ((i & 1) ? Tile::kBytes : 0) + Tile::row(tb, half_n, i >> 1));
+      return tr_frag(sl_p + ((i & 1) ? 0 : Tile::kBytes) + Tile::tr(tb, half_p, (i >> 1) & 1, i >> 2), Tile::kTrHi);
     };
     auto prod = [&](int f, const bf16x8& a) {
       int i;
@@ -2247,37 +2311,27 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_sw_kernel(const bf16* __restr
     lds_barrier();
   };
   // Half-step h: SDP for h + 1 < nh, SG for 0 <= h < nh, GRAD for 1 <= h <= nh
-  // (nh is even, >= 2, and >= 6 without the short paths). The causal mask can only touch halves 0 .. 3 of
+  // (nh is even and >= 6). The causal mask can only touch halves 0 .. 3 of
   // the sweep (the diagonal block): the first half-steps apply it on every
   // wave, where it is a no-op for halves below the wave's keys.
   sync_tile();
   stage(P1(), T_(), F_(), F_(), F_(), -1);
   stage(P0(), T_(), T_(), T_(), F_(), 0);
   sync_tile();
-  if (kShortPaths && nh == 2) {
-    stage(P1(), F_(), T_(), T_(), T_(), 1);
-    stage(P0(), F_(), F_(), F_(), T_(), 2);
-  } else {
-    stage(P1(), T_(), T_(), T_(), T_(), 1);
-    stage(P0(), T_(), T_(), T_(), T_(), 2);
+  stage(P1(), T_(), T_(), T_(), T_(), 1);
+  stage(P0(), T_(), T_(), T_(), T_(), 2);
+  sync_tile();
+  stage(P1(), T_(), T_(), T_(), T_(), 3);
+  stage(P0(), T_(), T_(), F_(), T_(), 4);
+  // Full, unmasked half-steps in pairs, then the last two.
+  for (int h = 5; h + 1 <= nh - 2; h += 2) {
     sync_tile();
-    if (kShortPaths && nh == 4) {
-      stage(P1(), F_(), T_(), T_(), T_(), 3);
-      stage(P0(), F_(), F_(), F_(), T_(), 4);
-    } else {
-      stage(P1(), T_(), T_(), T_(), T_(), 3);
-      stage(P0(), T_(), T_(), F_(), T_(), 4);
-      // Full, unmasked half-steps in pairs, then the last two.
-      for (int h = 5; h + 1 <= nh - 2; h += 2) {
-        sync_tile();
-        stage(P1(), T_(), T_(), F_(), T_(), h);
-        stage(P0(), T_(), T_(), F_(), T_(), h + 1);
-      }
-      sync_tile();
-      stage(P1(), F_(), T_(), F_(), T_(), nh - 1);
-      stage(P0(), F_(), F_(), F_(), T_(), nh);
-    }
+    stage(P1(), T_(), T_(), F_(), T_(), h);
+    stage(P0(), T_(), T_(), F_(), T_(), h + 1);
   }
+  sync_tile();
+  stage(P1(), F_(), T_(), F_(), T_(), nh - 1);
+  stage(P0(), F_(), F_(), F_(), T_(), nh);
   wait_vmem<0>();
 
   if (k0w >= Sk) return;
@@ -2681,10 +2735,11 @@ int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout,
   const AttnViews vw = views ? *views : dense_views(s);
   auto kern = vw.q.r == vw.dout.r ? attn_dkv_sw_kernel<D, true> : attn_dkv_sw_kernel<D, false>;
   set_lds(kern, F::kLds);
+  const int zig = causal && F::kMinBlocks == 2 && nk * bh <= 2 * (int64_t)cu_count();
   hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
                      delta, static_cast<bf16*>(dk), static_cast<bf16*>(dv), (int)bh, (int)s.sq, (int)s.sk, (int)s.d,
-                     causal, scale, scale * kLog2e, vw);
+                     causal, scale, scale * kLog2e, vw, (int)nk, zig);
   return check_launch("ferrite_flash_attention_bwd_dkv");
 }
 
