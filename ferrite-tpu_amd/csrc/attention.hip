@@ -2062,7 +2062,8 @@ __device__ __forceinline__ void stat_dma(const float* base, int r0, int nrows, c
                : "memory", "m0");
 }
 
-// dK, dV, software-pipelined (the forward's scheme). Half-step h of a wave
+// dK, dV, software-pipelined (the forward's scheme); D = 64 (D = 128 runs
+// attn_dkv_rs_kernel below, which splits a key block over two waves). Half-step h of a wave
 // (32 queries) first issues dV^T += dO^T P and dK^T += Q^T dS for half h - 1
 // and turns the S and dP of half h into P and dS on the VALU between those
 // products, then issues S = Q K^T and dP = dO V^T for half h + 1 into the same
@@ -2337,6 +2338,351 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
   if (k0w >= Sk) return;
   store_acc_rows<bf16, D, true>(dka, dk + vw.dk.at(bh, vw.heads), kvrow, Sk, d, scale, vw.dk.r);
   store_acc_rows<bf16, D, true>(dva, dv + vw.dv.at(bh, vw.heads), kvrow, Sk, d, 1.0f, vw.dv.r);
+}
+
+// dK, dV at D = 128 with the work of each 32-key block split over the two
+// waves of a SIMD. Wave w < 4 (role A) computes S = Q K^T, P and
+// dV^T += dO^T P for keys k0 + 32 w; wave w + 4 (role B, on the same SIMD)
+// computes dP = dO V^T, dS = P (dP - delta) and dK^T += Q^T dS for the same
+// keys. A hands P to B through LDS in f32, before any rounding, so dS is the
+// reference's p * (dp - di) (flash_attention.py:191-193) exactly as in the
+// one-wave kernel above. Each wave holds one accumulator set (64 registers)
+// and one of K and V (32), so two waves fit on a SIMD and the VALU work of
+// one overlaps the products of the other; the one-wave kernel, which holds
+// both, takes 286 registers and runs one wave per SIMD.
+// Half-step h (32 queries): A runs dV for half h - 1 with the softmax of half
+// h between its products, then S for half h + 1; B runs dP for half h with dS
+// of half h - 1 between its products (P from A, written in half-step h - 1),
+// then dK for half h - 1. One workgroup barrier per half-step orders the P
+// exchange (two buffers) and the three-slot Q / dO ring: tile t is read in
+// half-steps 2t - 1 .. 2t + 2, and its DMA goes out in half-step 2t - 3 into
+// the slot tile t - 3 left.
+struct DkvRs {
+  static constexpr int D = 128, kWaves = 8, kThreads = 64 * kWaves;
+  static constexpr int BKV = 128, BQ = 64, KS = D / 16, DT = D / 32;
+  typedef BwdTile<128> Tile;
+  static constexpr int kSlots = 3;
+  static constexpr int kStatBytes = 2048;  // lse at +0 (wave 0 loads it), delta at +1024 (wave 4)
+  static constexpr int kSlotBytes = 2 * Tile::kBytes + kStatBytes;
+  static constexpr int kXBytes = 4 * 4096;  // P of one half for the four SIMD pairs (f32)
+  static constexpr int kLds = kSlots * kSlotBytes + 2 * kXBytes;
+  static constexpr int kDma = Tile::kBlocks / kWaves;  // per wave per tile, for Q and for dO
+};
+
+template <bool SAMEP>
+__global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                            const bf16* __restrict__ v, const bf16* __restrict__ dout,
+                                                            const float* __restrict__ lse,
+                                                            const float* __restrict__ delta, bf16* __restrict__ dk,
+                                                            bf16* __restrict__ dv, int bh_count, int Sq, int Sk, int d,
+                                                            int causal, float scale, float scale_log2, AttnViews vw,
+                                                            int n_ktiles, int zig) {
+  typedef DkvRs F;
+  typedef F::Tile Tile;
+  constexpr int KS = F::KS, DT = F::DT;
+  constexpr int kAhead = 3;
+  // Per wave and tile: Q blocks, dO blocks, and the statistics row (waves 0 and 4 only).
+  constexpr int kTileDma = 2 * F::kDma + 1;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  // Heaviest (first) key blocks first; zig as in attn_dkv_sw_kernel.
+  const int bh = blockIdx.x % bh_count;
+  const int blk = (int)(blockIdx.x / bh_count);
+  const int first_half = n_ktiles - n_ktiles / 2;
+  const int kt = !zig || blk < first_half ? blk : n_ktiles - 1 - (blk - first_half);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pair = wave & 3, role = wave >> 2;
+  const int lane = threadIdx.x & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int k0 = kt * F::BKV;
+  const int k0w = k0 + 32 * pair;
+  const int kvrow = k0w + l32;
+
+  const int ldq = (int)vw.q.r, lddo = (int)vw.dout.r;
+  const bf16* qb = q + vw.q.at(bh, vw.heads);
+  const bf16* dob = dout + vw.dout.at(bh, vw.heads);
+  const float* lseb = lse + (int64_t)bh * Sq;
+  const float* db = delta + (int64_t)bh * Sq;
+
+  // Sweeps of fewer than three tiles run as three (zero tiles add exact
+  // zeros, as in attn_dkv_sw_kernel).
+  const int first = causal ? k0 / F::BQ : 0;
+  const int nt = max((Sq + F::BQ - 1) / F::BQ - first, 3);
+  const int nh = 2 * nt;
+
+  const PpDma<Tile, true, F::kWaves> dma(wave, ldq);
+  const PpDma<Tile, true, F::kWaves> dma_do(wave, SAMEP ? ldq : lddo);
+  auto slot = [&](int t) { return smem + (t % F::kSlots) * F::kSlotBytes; };
+  char* const xring = smem + F::kSlots * F::kSlotBytes;
+  // P of half h, pair p: chunk c (four queries) of lane L at xbuf(h) + p 4096 + c 1024 + 16 L.
+  auto xbuf = [&](int h) { return xring + (h & 1) * F::kXBytes + pair * 4096; };
+  // DMA instruction qd of tile t; rows past the end of the queries arrive as
+  // zeros (empty buffer range), which the padded sweeps rely on.
+  auto dma_part = [&](int t, int qd) {
+    char* sl = slot(t);
+    const int r0 = (first + t) * F::BQ;
+    if (qd < F::kDma)
+      dma.issue_one(qb, r0, Sq, ldq, sl, qd);
+    else if (qd < 2 * F::kDma)
+      (SAMEP ? dma : dma_do).issue_one(dob, r0, Sq, SAMEP ? ldq : lddo, sl + Tile::kBytes, qd - F::kDma);
+    else if (pair == 0)
+      stat_dma(role ? db : lseb, r0, Sq, sl + 2 * Tile::kBytes + role * 1024);
+  };
+#pragma unroll
+  for (int qd = 0; qd < kTileDma; ++qd) dma_part(0, qd);
+
+  const typename Tile::Bases tb(lane);
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+
+  // Barrier opening half-step h. Tile t's DMA goes out in half-step 2t - 3 and
+  // is first read in half-step 2t - 1: before an odd half-step every DMA of
+  // this wave has landed; before an even one nothing new is needed.
+  auto sync = [&](int h) {
+    if (h & 1) wait_vmem<0>();
+    lds_barrier();
+  };
+  // The DMA of tile (h + 3) / 2 in odd half-steps, one instruction per
+  // product slot from the first.
+  auto dma_at = [&](int h, int f) {
+    if ((h & 1) && f < kTileDma) dma_part((h + 3) >> 1, f);
+  };
+
+  if (role == 0) {
+    // ---- role A: S, P, dV ----
+    const bf16* kb = k + vw.k.at(bh, vw.heads);
+    bf16x8 kf[KS];
+    load_row_frags<bf16, 128, true, false>(kf, kb, k0w, Sk, d, (int)vw.k.r);
+    f32x16 dva[DT];
+#pragma unroll
+    for (int u = 0; u < DT; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dva[u][r] = 0.f;
+    f32x16 sa[2];       // S of a half (register r: query 16 g + r, key kvrow), by parity
+    bf16x8 pf[2][2];    // [parity][8-query chunk]: P fragments
+
+    auto stage = [&](auto P_, auto GRAD_, auto SG_, auto MASK_, auto SDP_, int h) __attribute__((always_inline)) {
+      constexpr int P = decltype(P_)::value;
+      constexpr bool GRAD = decltype(GRAD_)::value, SG = decltype(SG_)::value;
+      constexpr bool MASK = decltype(MASK_)::value, SDP = decltype(SDP_)::value;
+      const f32x16& sc = sa[P];
+      f32x16& sn = sa[1 - P];
+      bf16x8(&pc)[2] = pf[P];
+      const bf16x8(&pp)[2] = pf[1 - P];
+      const char* sl_n = slot((h + 1) >> 1);  // S of half h + 1: Q rows
+      const int half_n = (h + 1) & 1;
+      const char* sl_p = slot((h - 1) >> 1);  // dV of half h - 1: dO^T
+      const int half_p = (h - 1) & 1;
+      const int half_c = h & 1;
+      // The S products come first and the dV products, with the softmax between
+      // them, second: B's VALU work sits in the first half of its half-step, so
+      // the two waves of a SIMD alternate between products and VALU work.
+      constexpr int NS = SDP ? KS : 0;       // S: k-chunk i
+      constexpr int NG = GRAD ? 2 * DT : 0;  // dV: output tile u = i / 2, query chunk i % 2
+      constexpr int NF = NS + NG;
+      auto read = [&](int f) -> bf16x8 {
+        if (f < NS) return *reinterpret_cast<const bf16x8*>(sl_n + Tile::row(tb, half_n, f));
+        const int i = f - NS;
+        return tr_frag(sl_p + Tile::kBytes + Tile::tr(tb, half_p, i & 1, i >> 1), Tile::kTrHi);
+      };
+      auto prod = [&](int f, const bf16x8& a) {
+        if (f < NS) {
+          if (f == 0)
+            sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kf[0], f32x16{}, 0, 0, 0);
+          else
+            mma32(a, kf[f], sn);
+        } else {
+          const int i = f - NS;
+          mma32(a, pp[i & 1], dva[i >> 1]);
+        }
+      };
+      // Softmax of half h: element r (query 16 g + r of the half).
+      const float* st = reinterpret_cast<const float*>(slot(h >> 1) + 2 * Tile::kBytes) + 32 * half_c + 16 * g;
+      const int qh = (first + (h >> 1)) * F::BQ + 32 * half_c + 16 * g;
+      char* const xw = xbuf(h) + 16 * lane;
+      f32x4 ls[2];
+      float pv[8];
+      f32x4 p4;
+      auto sg_elem = [&](int r) {
+        if ((r & 3) == 0 && (r >> 2) + 1 < 4) ls[((r >> 2) + 1) & 1] = *reinterpret_cast<const f32x4*>(st + 4 * ((r >> 2) + 1));
+        const f32x4& l4 = ls[(r >> 2) & 1];
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, -l4[r & 3] * kLog2e));
+        if constexpr (MASK) p = (causal && kvrow > qh + r) ? 0.f : p;
+        pv[r & 7] = p;
+        p4[r & 3] = p;
+        if ((r & 3) == 3) *reinterpret_cast<f32x4*>(xw + (r >> 2) * 1024) = p4;
+        if ((r & 7) == 7) {
+          to_frag(pv, pc[r >> 3]);
+          pin(pc[r >> 3]);
+        }
+      };
+      if constexpr (SG) ls[0] = *reinterpret_cast<const f32x4*>(st);
+      if constexpr (NF > 0) {
+        bf16x8 buf[NF];
+#pragma unroll
+        for (int f = 0; f < kAhead && f < NF; ++f) buf[f] = read(f);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          if (f + kAhead < NF) buf[f + kAhead] = read(f + kAhead);
+          dma_at(h, f);
+          prod(f, buf[f]);
+          if constexpr (SG && NG > 0) {
+            if (f >= NS) {
+#pragma unroll
+              for (int r = (f - NS) * (16 / NG); r < (f - NS + 1) * (16 / NG); ++r) sg_elem(r);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int f = 0; f < kTileDma; ++f) dma_at(h, f);
+      }
+      if constexpr (SG && NG == 0) {
+        // No dV products to hide it behind (the first half-step): the softmax last.
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sg_elem(r);
+      }
+    };
+    // Half-step h: GRAD (dV) for 1 <= h <= nh, SG for 0 <= h < nh, SDP (S) for
+    // h + 1 < nh; the mask covers halves 0 .. 3 (the diagonal block).
+    sync(-1);
+    stage(P1(), F_(), F_(), F_(), T_(), -1);
+    sync(0);
+    stage(P0(), F_(), T_(), T_(), T_(), 0);
+    sync(1);
+    stage(P1(), T_(), T_(), T_(), T_(), 1);
+    sync(2);
+    stage(P0(), T_(), T_(), T_(), T_(), 2);
+    sync(3);
+    stage(P1(), T_(), T_(), T_(), T_(), 3);
+    sync(4);
+    stage(P0(), T_(), T_(), F_(), T_(), 4);
+    for (int h = 5; h + 1 <= nh - 2; h += 2) {
+      sync(h);
+      stage(P1(), T_(), T_(), F_(), T_(), h);
+      sync(h + 1);
+      stage(P0(), T_(), T_(), F_(), T_(), h + 1);
+    }
+    sync(nh - 1);
+    stage(P1(), T_(), T_(), F_(), F_(), nh - 1);
+    sync(nh);
+    stage(P0(), T_(), F_(), F_(), F_(), nh);
+    wait_vmem<0>();
+    if (k0w >= Sk) return;
+    store_acc_rows<bf16, 128, true>(dva, dv + vw.dv.at(bh, vw.heads), kvrow, Sk, d, 1.0f, vw.dv.r);
+  } else {
+    // ---- role B: dP, dS, dK ----
+    const bf16* vb = v + vw.v.at(bh, vw.heads);
+    bf16x8 vf[KS];
+    load_row_frags<bf16, 128, true, false>(vf, vb, k0w, Sk, d, (int)vw.v.r);
+    f32x16 dka[DT];
+#pragma unroll
+    for (int u = 0; u < DT; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dka[u][r] = 0.f;
+    f32x16 dpa[2];   // dP of a half, by parity
+    bf16x8 dsf[2];   // dS fragments of the half the stage's dK products use
+
+    auto stage = [&](auto P_, auto SDP_, auto SG_, auto GRAD_, int h) __attribute__((always_inline)) {
+      constexpr int P = decltype(P_)::value;
+      constexpr bool SDP = decltype(SDP_)::value, SG = decltype(SG_)::value, GRAD = decltype(GRAD_)::value;
+      f32x16& dpn = dpa[P];             // dP of half h
+      const f32x16& dpc = dpa[1 - P];   // dP of half h - 1
+      const char* sl_c = slot(h >> 1);  // dP of half h: dO rows
+      const int half_c = h & 1;
+      const char* sl_p = slot((h - 1) >> 1);  // dS and dK of half h - 1: Q^T, delta
+      const int half_p = (h - 1) & 1;
+      constexpr int NS = SDP ? KS : 0;       // dP: k-chunk i
+      constexpr int NG = GRAD ? 2 * DT : 0;  // dK: output tile u = i / 2, query chunk i % 2
+      constexpr int NF = NS + NG;
+      auto read = [&](int f) -> bf16x8 {
+        if (f < NS) return *reinterpret_cast<const bf16x8*>(sl_c + Tile::kBytes + Tile::row(tb, half_c, f));
+        const int i = f - NS;
+        return tr_frag(sl_p + Tile::tr(tb, half_p, i & 1, i >> 1), Tile::kTrHi);
+      };
+      auto prod = [&](int f, const bf16x8& a) {
+        if (f < NS) {
+          if (f == 0)
+            dpn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, vf[0], f32x16{}, 0, 0, 0);
+          else
+            mma32(a, vf[f], dpn);
+        } else {
+          const int i = f - NS;
+          mma32(a, dsf[i & 1], dka[i >> 1]);
+        }
+      };
+      // dS of half h - 1: element r (query 16 g + r), P from A's half-step h - 1.
+      const float* st = reinterpret_cast<const float*>(sl_p + 2 * Tile::kBytes) + 256 + 32 * half_p + 16 * g;
+      const char* xr = xbuf(h - 1) + 16 * lane;
+      f32x4 dl[2], px[2];
+      float dsv[8];
+      auto sg_elem = [&](int r) {
+        if ((r & 3) == 0 && (r >> 2) + 1 < 4) {
+          const int c = (r >> 2) + 1;
+          dl[c & 1] = *reinterpret_cast<const f32x4*>(st + 4 * c);
+          px[c & 1] = *reinterpret_cast<const f32x4*>(xr + c * 1024);
+        }
+        const float p = px[(r >> 2) & 1][r & 3];
+        dsv[r & 7] = p * (dpc[r] - dl[(r >> 2) & 1][r & 3]);
+        if ((r & 7) == 7) {
+          to_frag(dsv, dsf[r >> 3]);
+          pin(dsf[r >> 3]);
+        }
+      };
+      if constexpr (SG) {
+        dl[0] = *reinterpret_cast<const f32x4*>(st);
+        px[0] = *reinterpret_cast<const f32x4*>(xr);
+      }
+      if constexpr (SG && NS == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sg_elem(r);
+      }
+      if constexpr (NF > 0) {
+        bf16x8 buf[NF];
+#pragma unroll
+        for (int f = 0; f < kAhead && f < NF; ++f) buf[f] = read(f);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          if (f + kAhead < NF) buf[f + kAhead] = read(f + kAhead);
+          dma_at(h, f);
+          prod(f, buf[f]);
+          if constexpr (SG && NS > 0) {
+            if (f < NS) {
+#pragma unroll
+              for (int r = f * (16 / NS); r < (f + 1) * (16 / NS); ++r) sg_elem(r);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int f = 0; f < kTileDma; ++f) dma_at(h, f);
+      }
+    };
+    // Half-step h: SDP (dP) for 0 <= h < nh, SG (dS) and GRAD (dK) for 1 <= h <= nh.
+    sync(-1);
+    stage(P1(), F_(), F_(), F_(), -1);
+    sync(0);
+    stage(P0(), T_(), F_(), F_(), 0);
+    for (int h = 1; h + 1 <= nh - 1; h += 2) {
+      sync(h);
+      stage(P1(), T_(), T_(), T_(), h);
+      sync(h + 1);
+      stage(P0(), T_(), T_(), T_(), h + 1);
+    }
+    sync(nh - 1);
+    stage(P1(), T_(), T_(), T_(), nh - 1);
+    sync(nh);
+    stage(P0(), F_(), T_(), T_(), nh);
+    wait_vmem<0>();
+    if (k0w >= Sk) return;
+    store_acc_rows<bf16, 128, true>(dka, dk + vw.dk.at(bh, vw.heads), kvrow, Sk, d, scale, vw.dk.r);
+  }
 }
 
 // W waves of 32 queries; SLOTS K/V tile slots in LDS (3: tiles t + 1 and t + 2
@@ -2733,14 +3079,26 @@ int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout,
   const int64_t bh = s.b * s.h;
   if (nk * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dkv: grid too large");
   const AttnViews vw = views ? *views : dense_views(s);
-  auto kern = vw.q.r == vw.dout.r ? attn_dkv_sw_kernel<D, true> : attn_dkv_sw_kernel<D, false>;
-  set_lds(kern, F::kLds);
-  const int zig = causal && F::kMinBlocks == 2 && nk * bh <= 2 * (int64_t)cu_count();
-  hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
-                     static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
-                     delta, static_cast<bf16*>(dk), static_cast<bf16*>(dv), (int)bh, (int)s.sq, (int)s.sk, (int)s.d,
-                     causal, scale, scale * kLog2e, vw, (int)nk, zig);
-  return check_launch("ferrite_flash_attention_bwd_dkv");
+  if constexpr (D == 128) {
+    // Two waves per SIMD with the work of a key block split between them.
+    typedef DkvRs R;
+    auto kern = vw.q.r == vw.dout.r ? attn_dkv_rs_kernel<true> : attn_dkv_rs_kernel<false>;
+    set_lds(kern, R::kLds);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(R::kThreads), R::kLds, stream, static_cast<const bf16*>(q),
+                       static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
+                       delta, static_cast<bf16*>(dk), static_cast<bf16*>(dv), (int)bh, (int)s.sq, (int)s.sk, (int)s.d,
+                       causal, scale, scale * kLog2e, vw, (int)nk, 0);
+    return check_launch("ferrite_flash_attention_bwd_dkv");
+  } else {
+    auto kern = vw.q.r == vw.dout.r ? attn_dkv_sw_kernel<D, true> : attn_dkv_sw_kernel<D, false>;
+    set_lds(kern, F::kLds);
+    const int zig = causal && F::kMinBlocks == 2 && nk * bh <= 2 * (int64_t)cu_count();
+    hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
+                       static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
+                       delta, static_cast<bf16*>(dk), static_cast<bf16*>(dv), (int)bh, (int)s.sq, (int)s.sk, (int)s.d,
+                       causal, scale, scale * kLog2e, vw, (int)nk, zig);
+    return check_launch("ferrite_flash_attention_bwd_dkv");
+  }
 }
 
 template <typename T, int D, bool AL>
