@@ -941,16 +941,39 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
   // K_0 and K_1 go out first; stage j then loads K_{j+3} and V_{j+1}.
   const PpDma<KT, true, F::kWaves> kdma(wave, ldk);
   const PpDma<VT, false, F::kWaves> vdma(wave, ldv);
+  // Full-width (d == D) Q rows come by DMA as whole rows (a row per kQCh lanes,
+  // 16-byte chunks XOR-swizzled by row) into K slot 2 and the V slots, which
+  // the DMA reaches only from stage -1 on; loaded into registers directly,
+  // every load instruction touches 32 rows (32 cache lines for 1 KB). Each
+  // wave reads its own rows back after sync(-1).
+  constexpr int kQRow = 2 * D, kQCh = kQRow / 16, kQRpi = 1024 / kQRow;
+  static_assert(2 * KT::kBytes + F::kWaves * 32 * RB * kQRow <= F::kLds, "the Q rows fit the idle ring slots");
+  const bool q_lds = d == D;
+  char* const qst = smem + 2 * KT::kBytes + wave * (32 * RB * kQRow);
   kdma.issue(kb, 0, S, ldk, kring);
+  if (q_lds) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int r0 = q0w + 32 * rb;
+      const u32x4 rs = buffer_rsrc(qb + (int64_t)r0 * ldq, r0 < S ? (uint32_t)((S - r0) * ldq * 2) : 0u);
+#pragma unroll
+      for (int i = 0; i < 32 / kQRpi; ++i) {
+        const int rr = kQRpi * i + lane / kQCh, c = (lane % kQCh) ^ (rr & (kQCh - 1));
+        dma16(rs, qst + rb * 32 * kQRow + 1024 * i, (uint32_t)((rr * ldq + 8 * c) * 2));
+      }
+    }
+  }
   kdma.issue(kb, F::BK, S, ldk, kring + KT::kBytes);
 
   bf16x8 qf[RB][KS];
+  if (!q_lds) {
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    if (neg_q)
-      load_row_frags<bf16, D, true, true>(qf[rb], qb, q0w + 32 * rb, S, d, ldq);
-    else
-      load_row_frags<bf16, D, true, false>(qf[rb], qb, q0w + 32 * rb, S, d, ldq);
+    for (int rb = 0; rb < RB; ++rb) {
+      if (neg_q)
+        load_row_frags<bf16, D, true, true>(qf[rb], qb, q0w + 32 * rb, S, d, ldq);
+      else
+        load_row_frags<bf16, D, true, false>(qf[rb], qb, q0w + 32 * rb, S, d, ldq);
+    }
   }
 
   const int kbase = KT::off(l32, g * 16);
@@ -1147,6 +1170,24 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
   // This wave's stages: QK of tile 0; QK + softmax for tiles 0 .. n_w - 2
   // (with PV from tile 1 on); the diagonal tile's masked softmax; the last PV.
   sync(-1);
+  if (q_lds) {
+    // This wave's Q rows have landed (sync(-1) waited for them); the barrier
+    // keeps stage -1's DMA (K_2, V_0) off the staging until every wave has
+    // read its rows.
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int kc = 0; kc < KS; ++kc) {
+        const int c = 2 * kc + g;
+        qf[rb][kc] = *reinterpret_cast<const bf16x8*>(qst + rb * 32 * kQRow + l32 * kQRow + ((c ^ (l32 & (kQCh - 1))) * 16));
+        if (neg_q) {
+          u32x4 w = __builtin_bit_cast(u32x4, qf[rb][kc]);
+          w ^= 0x80008000u;
+          qf[rb][kc] = __builtin_bit_cast(bf16x8, w);
+        }
+      }
+    lds_barrier();
+  }
   if (n_w > 0)
     stage(P1(), T_(), F_(), F_(), F_(), -1);
   else
@@ -1193,13 +1234,50 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
   }
   wait_vmem<0>();
 
+  if (d < D) {
+    if (n_w == 0) return;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int row = q0w + 32 * rb + l32;
+      const float l = lane32_sum(lsum[rb]);
+      store_acc_rows<bf16, D, true>(acc[rb], o + vw.o.at(bh, vw.heads), row, S, d, 1.0f / l, vw.o.r);
+      if (g == 0 && row < S) lse[(int64_t)bh * S + row] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
+    }
+    return;
+  }
+  // Full-width rows go out through LDS: a lane's accumulator registers hold
+  // 4-column pieces of one row, and stored directly each store instruction
+  // touches 32 rows (32 cache lines for 512 bytes; the stores of a workgroup
+  // then took ~4000 cycles on MI355X). Each wave writes its rows into its own
+  // part of the (now idle) rings, 16-byte chunks XOR-swizzled by row, and
+  // reads them back 16 bytes per lane so that every store instruction writes
+  // whole rows. The barrier: every wave has left its last stage and its ring
+  // reads, and every DMA (this wave's waited just above) has landed.
+  constexpr int kRowBytes = 2 * D, kCh = kRowBytes / 16, kRowsPerInst = 64 / kCh;
+  static_assert(F::kWaves * 32 * RB * kRowBytes <= F::kLds, "every wave's rows fit the rings");
+  lds_barrier();
   if (n_w == 0) return;
+  char* const ot = smem + wave * (32 * RB * kRowBytes);
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    const int row = q0w + 32 * rb + l32;
+    const int r = 32 * rb + l32;
     const float l = lane32_sum(lsum[rb]);
-    store_acc_rows<bf16, D, true>(acc[rb], o + vw.o.at(bh, vw.heads), row, S, d, 1.0f / l, vw.o.r);
-    if (g == 0 && row < S) lse[(int64_t)bh * S + row] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
+    const float inv = 1.0f / l;
+    if (g == 0 && q0w + r < S) lse[(int64_t)bh * S + q0w + r] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
+#pragma unroll
+    for (int u = 0; u < DT; ++u)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq)
+        *reinterpret_cast<bf16x4*>(ot + r * kRowBytes + (((4 * u + qq) ^ (r & (kCh - 1))) * 16) + 8 * g) =
+            bf16x4{(bf16)(acc[rb][u][4 * qq] * inv), (bf16)(acc[rb][u][4 * qq + 1] * inv),
+                   (bf16)(acc[rb][u][4 * qq + 2] * inv), (bf16)(acc[rb][u][4 * qq + 3] * inv)};
+  }
+  bf16* const orows = o + vw.o.at(bh, vw.heads);
+#pragma unroll
+  for (int i = 0; i < 32 * RB / kRowsPerInst; ++i) {
+    const int r = i * kRowsPerInst + lane / kCh, c = lane % kCh;
+    const bf16x8 val = *reinterpret_cast<const bf16x8*>(ot + r * kRowBytes + ((c ^ (r & (kCh - 1))) * 16));
+    if (q0w + r < S) *reinterpret_cast<bf16x8*>(orows + (int64_t)(q0w + r) * vw.o.r + 8 * c) = val;
   }
 }
 

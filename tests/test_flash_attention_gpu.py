@@ -252,6 +252,17 @@ def test_causal_tile_edges_via_abi(dev, b, h, s, d, fused):
     _abi_case(dev, b, h, s, s, d, "bf16", True, seed=37, scale=1.0 / np.sqrt(d), fused=fused)
 
 
+@pytest.mark.parametrize("b,h,s,d", [
+    (1, 2, 512, 128),   # full-width rows: Q by DMA through LDS, the sign flipped after the read
+    (2, 1, 256, 64),
+    (1, 1, 320, 80),    # d < D: Q loaded directly, the sign flipped on load
+])
+def test_negative_scale_via_abi(dev, b, h, s, d):
+    """A negative softmax scale: the forward negates q instead (its row statistics need a
+    positive multiplier), on both ways the causal sweep kernel loads q."""
+    _abi_case(dev, b, h, s, s, d, "bf16", True, seed=43, scale=-0.2)
+
+
 @pytest.mark.parametrize("d", [64, 128])
 def test_rising_scores_force_rescales(dev, d):
     """Scores that grow along the key axis raise every row's running max by far more than 2^8
