@@ -289,6 +289,36 @@ __device__ __forceinline__ void store_acc_rows(const f32x16 (&acc)[D / 32], T* _
   }
 }
 
+// Full-width (d == D) bf16 rows of a wave's accumulators through LDS. A lane's
+// accumulator registers hold 4-column pieces of one row (register r of tile u
+// is column 32 u + 8 (r / 4) + 4 g + r % 4 of row l32), so stored directly
+// every store instruction touches 32 rows (32 cache lines for 512 bytes; the
+// stores of one forward workgroup took ~4000 cycles on MI355X). The rows go
+// into this wave's 32 x 2D-byte LDS region (16-byte chunks XOR-swizzled by
+// row) and come back 16 bytes per lane, so that each store instruction writes
+// whole rows, 2D / 16 lanes per row. The caller keeps other waves' reads and
+// DMA off the region; one wave's LDS writes and reads are processed in order.
+// Rows row0 + r at or past nrows are skipped.
+template <int D>
+__device__ __forceinline__ void store_acc_rows_lds(const f32x16 (&acc)[D / 32], char* lds, bf16* __restrict__ out,
+                                                   int64_t row0, int64_t nrows, float mul, int64_t ld) {
+  constexpr int kRowBytes = 2 * D, kCh = kRowBytes / 16, kRowsPerInst = 64 / kCh;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int u = 0; u < D / 32; ++u)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq)
+      *reinterpret_cast<bf16x4*>(lds + l32 * kRowBytes + (((4 * u + qq) ^ (l32 & (kCh - 1))) * 16) + 8 * g) =
+          bf16x4{(bf16)(acc[u][4 * qq] * mul), (bf16)(acc[u][4 * qq + 1] * mul), (bf16)(acc[u][4 * qq + 2] * mul),
+                 (bf16)(acc[u][4 * qq + 3] * mul)};
+#pragma unroll
+  for (int i = 0; i < 32 / kRowsPerInst; ++i) {
+    const int r = i * kRowsPerInst + lane / kCh, c = lane % kCh;
+    const bf16x8 val = *reinterpret_cast<const bf16x8*>(lds + r * kRowBytes + ((c ^ (r & (kCh - 1))) * 16));
+    if (row0 + r < nrows) *reinterpret_cast<bf16x8*>(out + (row0 + r) * ld + 8 * c) = val;
+  }
+}
+
 // Element strides of one tensor seen as [B, H, rows, d] with contiguous columns:
 // between batches, heads and rows. A dense [B, H, S, d] tensor has (H S d, S d, d);
 // the q part of a token-major [B, S, 3, H, d] projection has (3 S H d, d, 3 H d).
@@ -1245,39 +1275,21 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
     }
     return;
   }
-  // Full-width rows go out through LDS: a lane's accumulator registers hold
-  // 4-column pieces of one row, and stored directly each store instruction
-  // touches 32 rows (32 cache lines for 512 bytes; the stores of a workgroup
-  // then took ~4000 cycles on MI355X). Each wave writes its rows into its own
-  // part of the (now idle) rings, 16-byte chunks XOR-swizzled by row, and
-  // reads them back 16 bytes per lane so that every store instruction writes
-  // whole rows. The barrier: every wave has left its last stage and its ring
-  // reads, and every DMA (this wave's waited just above) has landed.
-  constexpr int kRowBytes = 2 * D, kCh = kRowBytes / 16, kRowsPerInst = 64 / kCh;
-  static_assert(F::kWaves * 32 * RB * kRowBytes <= F::kLds, "every wave's rows fit the rings");
+  // Full-width rows go out through LDS (store_acc_rows_lds), each wave in its
+  // own part of the (now idle) rings. The barrier: every wave has left its last
+  // stage and its ring reads, and every DMA (this wave's waited above) has
+  // landed.
+  static_assert(F::kWaves * 32 * RB * 2 * D <= F::kLds, "every wave's rows fit the rings");
   lds_barrier();
   if (n_w == 0) return;
-  char* const ot = smem + wave * (32 * RB * kRowBytes);
+  char* const ot = smem + wave * (32 * RB * 2 * D);
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    const int r = 32 * rb + l32;
+    const int row = q0w + 32 * rb + l32;
     const float l = lane32_sum(lsum[rb]);
-    const float inv = 1.0f / l;
-    if (g == 0 && q0w + r < S) lse[(int64_t)bh * S + q0w + r] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
-#pragma unroll
-    for (int u = 0; u < DT; ++u)
-#pragma unroll
-      for (int qq = 0; qq < 4; ++qq)
-        *reinterpret_cast<bf16x4*>(ot + r * kRowBytes + (((4 * u + qq) ^ (r & (kCh - 1))) * 16) + 8 * g) =
-            bf16x4{(bf16)(acc[rb][u][4 * qq] * inv), (bf16)(acc[rb][u][4 * qq + 1] * inv),
-                   (bf16)(acc[rb][u][4 * qq + 2] * inv), (bf16)(acc[rb][u][4 * qq + 3] * inv)};
-  }
-  bf16* const orows = o + vw.o.at(bh, vw.heads);
-#pragma unroll
-  for (int i = 0; i < 32 * RB / kRowsPerInst; ++i) {
-    const int r = i * kRowsPerInst + lane / kCh, c = lane % kCh;
-    const bf16x8 val = *reinterpret_cast<const bf16x8*>(ot + r * kRowBytes + ((c ^ (r & (kCh - 1))) * 16));
-    if (q0w + r < S) *reinterpret_cast<bf16x8*>(orows + (int64_t)(q0w + r) * vw.o.r + 8 * c) = val;
+    if (g == 0 && row < S) lse[(int64_t)bh * S + row] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
+    store_acc_rows_lds<D>(acc[rb], ot + rb * 32 * 2 * D, o + vw.o.at(bh, vw.heads), q0w + 32 * rb, S, 1.0f / l,
+                          vw.o.r);
   }
 }
 
@@ -2413,6 +2425,17 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
   stage(P0(), F_(), F_(), F_(), T_(), nh);
   wait_vmem<0>();
 
+  if (d == D) {
+    // Whole-row stores through LDS (store_acc_rows_lds); the barrier keeps the
+    // other waves' last reads and DMA off this wave's region of the ring.
+    static_assert(4 * 32 * 2 * D <= F::kLds, "every wave's rows fit the ring");
+    lds_barrier();
+    if (k0w >= Sk) return;
+    char* const ot = smem + wave * (32 * 2 * D);
+    store_acc_rows_lds<D>(dka, ot, dk + vw.dk.at(bh, vw.heads), k0w, Sk, scale, vw.dk.r);
+    store_acc_rows_lds<D>(dva, ot, dv + vw.dv.at(bh, vw.heads), k0w, Sk, 1.0f, vw.dv.r);
+    return;
+  }
   if (k0w >= Sk) return;
   store_acc_rows<bf16, D, true>(dka, dk + vw.dk.at(bh, vw.heads), kvrow, Sk, d, scale, vw.dk.r);
   store_acc_rows<bf16, D, true>(dva, dv + vw.dv.at(bh, vw.heads), kvrow, Sk, d, 1.0f, vw.dv.r);
@@ -2650,6 +2673,12 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
     sync(nh);
     stage(P0(), T_(), F_(), F_(), F_(), nh);
     wait_vmem<0>();
+    if (d == 128) {
+      lds_barrier();  // as role B's: whole-row stores through LDS
+      if (k0w >= Sk) return;
+      store_acc_rows_lds<128>(dva, smem + wave * (32 * 256), dv + vw.dv.at(bh, vw.heads), k0w, Sk, 1.0f, vw.dv.r);
+      return;
+    }
     if (k0w >= Sk) return;
     store_acc_rows<bf16, 128, true>(dva, dv + vw.dv.at(bh, vw.heads), kvrow, Sk, d, 1.0f, vw.dv.r);
   } else {
@@ -2758,6 +2787,16 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
     sync(nh);
     stage(P0(), F_(), T_(), T_(), nh);
     wait_vmem<0>();
+    if (d == 128) {
+      // Whole-row stores through LDS (store_acc_rows_lds), each wave in its own
+      // 8 KB of the ring; the barrier (role A passes one too) keeps the other
+      // waves' last reads and DMA off it.
+      static_assert(8 * 32 * 256 <= DkvRs::kLds, "every wave's rows fit the ring");
+      lds_barrier();
+      if (k0w >= Sk) return;
+      store_acc_rows_lds<128>(dka, smem + wave * (32 * 256), dk + vw.dk.at(bh, vw.heads), k0w, Sk, scale, vw.dk.r);
+      return;
+    }
     if (k0w >= Sk) return;
     store_acc_rows<bf16, 128, true>(dka, dk + vw.dk.at(bh, vw.heads), kvrow, Sk, d, scale, vw.dk.r);
   }
@@ -2980,6 +3019,17 @@ __global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __r
     grad_q(sl, 1, dsf);
   }
 
+  if (D == 128 && d == D) {
+    // Whole-row stores through LDS (store_acc_rows_lds); the barrier keeps the
+    // other waves' last reads off this wave's region (every DMA has landed: the
+    // last tile's wait was vmcnt(0)). At D = 64 (two workgroups per CU, 128-byte
+    // rows) the direct stores measured as fast.
+    static_assert(W * 32 * 2 * D <= F::kLds, "every wave's rows fit the ring");
+    lds_barrier();
+    if (!wave_active) return;
+    store_acc_rows_lds<D>(acc, smem + wave * (32 * 2 * D), dq + vw.dq.at(bh, vw.heads), q0w, Sq, scale, vw.dq.r);
+    return;
+  }
   if (!wave_active) return;
   store_acc_rows<bf16, D, true>(acc, dq + vw.dq.at(bh, vw.heads), qrow, Sq, d, scale, vw.dq.r);
 }
