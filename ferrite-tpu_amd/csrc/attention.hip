@@ -289,6 +289,34 @@ __device__ __forceinline__ void store_acc_rows(const f32x16 (&acc)[D / 32], T* _
   }
 }
 
+// 32 full-width rows (row0 .. row0 + 31; rows at or past nrows arrive as
+// zeros) of a bf16 operand with D columns and row pitch ld, by DMA into LDS at
+// dst as whole rows: a row per D / 8 lanes and 1 KB per instruction, 16-byte
+// chunks XOR-swizzled by row. Loaded straight into fragments, every load
+// instruction touches 32 rows (32 cache lines for 1 KB). row_frags_lds reads
+// back the fragments load_row_frags would load.
+template <int D>
+__device__ __forceinline__ void dma_rows32(const bf16* base, int row0, int nrows, int ld, char* dst) {
+  constexpr int kRow = 2 * D, kCh = kRow / 16, kRpi = 1024 / kRow;
+  const int lane = threadIdx.x & 63;
+  const u32x4 rs = buffer_rsrc(base + (int64_t)row0 * ld, row0 < nrows ? (uint32_t)((nrows - row0) * ld * 2) : 0u);
+#pragma unroll
+  for (int i = 0; i < 32 / kRpi; ++i) {
+    const int rr = kRpi * i + lane / kCh, c = (lane % kCh) ^ (rr & (kCh - 1));
+    dma16(rs, dst + 1024 * i, (uint32_t)((rr * ld + 8 * c) * 2));
+  }
+}
+template <int D>
+__device__ __forceinline__ void row_frags_lds(bf16x8 (&f)[D / 16], const char* src) {
+  constexpr int kRow = 2 * D, kCh = kRow / 16;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int kc = 0; kc < D / 16; ++kc) {
+    const int c = 2 * kc + g;
+    f[kc] = *reinterpret_cast<const bf16x8*>(src + l32 * kRow + ((c ^ (l32 & (kCh - 1))) * 16));
+  }
+}
+
 // Full-width (d == D) bf16 rows of a wave's accumulators through LDS. A lane's
 // accumulator registers hold 4-column pieces of one row (register r of tile u
 // is column 32 u + 8 (r / 4) + 4 g + r % 4 of row l32), so stored directly
@@ -971,27 +999,19 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
   // K_0 and K_1 go out first; stage j then loads K_{j+3} and V_{j+1}.
   const PpDma<KT, true, F::kWaves> kdma(wave, ldk);
   const PpDma<VT, false, F::kWaves> vdma(wave, ldv);
-  // Full-width (d == D) Q rows come by DMA as whole rows (a row per kQCh lanes,
+  // Full-width (d == D) Q rows come by DMA as whole rows (a row per D / 8 lanes,
   // 16-byte chunks XOR-swizzled by row) into K slot 2 and the V slots, which
   // the DMA reaches only from stage -1 on; loaded into registers directly,
   // every load instruction touches 32 rows (32 cache lines for 1 KB). Each
   // wave reads its own rows back after sync(-1).
-  constexpr int kQRow = 2 * D, kQCh = kQRow / 16, kQRpi = 1024 / kQRow;
+  constexpr int kQRow = 2 * D;
   static_assert(2 * KT::kBytes + F::kWaves * 32 * RB * kQRow <= F::kLds, "the Q rows fit the idle ring slots");
   const bool q_lds = d == D;
   char* const qst = smem + 2 * KT::kBytes + wave * (32 * RB * kQRow);
   kdma.issue(kb, 0, S, ldk, kring);
   if (q_lds) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const int r0 = q0w + 32 * rb;
-      const u32x4 rs = buffer_rsrc(qb + (int64_t)r0 * ldq, r0 < S ? (uint32_t)((S - r0) * ldq * 2) : 0u);
-#pragma unroll
-      for (int i = 0; i < 32 / kQRpi; ++i) {
-        const int rr = kQRpi * i + lane / kQCh, c = (lane % kQCh) ^ (rr & (kQCh - 1));
-        dma16(rs, qst + rb * 32 * kQRow + 1024 * i, (uint32_t)((rr * ldq + 8 * c) * 2));
-      }
-    }
+    for (int rb = 0; rb < RB; ++rb) dma_rows32<D>(qb, q0w + 32 * rb, S, ldq, qst + rb * 32 * kQRow);
   }
   kdma.issue(kb, F::BK, S, ldk, kring + KT::kBytes);
 
@@ -1205,17 +1225,17 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
     // keeps stage -1's DMA (K_2, V_0) off the staging until every wave has
     // read its rows.
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+    for (int rb = 0; rb < RB; ++rb) {
+      row_frags_lds<D>(qf[rb], qst + rb * 32 * kQRow);
+      if (neg_q) {
 #pragma unroll
-      for (int kc = 0; kc < KS; ++kc) {
-        const int c = 2 * kc + g;
-        qf[rb][kc] = *reinterpret_cast<const bf16x8*>(qst + rb * 32 * kQRow + l32 * kQRow + ((c ^ (l32 & (kQCh - 1))) * 16));
-        if (neg_q) {
+        for (int kc = 0; kc < KS; ++kc) {
           u32x4 w = __builtin_bit_cast(u32x4, qf[rb][kc]);
           w ^= 0x80008000u;
           qf[rb][kc] = __builtin_bit_cast(bf16x8, w);
         }
       }
+    }
     lds_barrier();
   }
   if (n_w > 0)
@@ -2551,11 +2571,22 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
     if ((h & 1) && f < kTileDma) dma_part((h + 3) >> 1, f);
   };
 
+  // Full-width K (role A) or V (role B) rows come by row-coalesced DMA
+  // (dma_rows32) into tile slot 2 and the P exchange, which nothing writes
+  // before stage 0 (P) and stage 1 (tile 2's DMA); each wave reads its rows
+  // back in stage -1.
+  static_assert(F::kSlots == 3 && F::kSlotBytes + 2 * F::kXBytes >= 8 * 32 * 256, "the K/V rows fit the idle LDS");
+  const bool rows_lds = d == 128;
+  char* const rst = smem + 2 * F::kSlotBytes + wave * (32 * 256);
+
   if (role == 0) {
     // ---- role A: S, P, dV ----
     const bf16* kb = k + vw.k.at(bh, vw.heads);
     bf16x8 kf[KS];
-    load_row_frags<bf16, 128, true, false>(kf, kb, k0w, Sk, d, (int)vw.k.r);
+    if (rows_lds)
+      dma_rows32<128>(kb, k0w, Sk, (int)vw.k.r, rst);
+    else
+      load_row_frags<bf16, 128, true, false>(kf, kb, k0w, Sk, d, (int)vw.k.r);
     f32x16 dva[DT];
 #pragma unroll
     for (int u = 0; u < DT; ++u)
@@ -2651,6 +2682,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
     // Half-step h: GRAD (dV) for 1 <= h <= nh, SG for 0 <= h < nh, SDP (S) for
     // h + 1 < nh; the mask covers halves 0 .. 3 (the diagonal block).
     sync(-1);
+    if (rows_lds) row_frags_lds<128>(kf, rst);
     stage(P1(), F_(), F_(), F_(), T_(), -1);
     sync(0);
     stage(P0(), F_(), T_(), T_(), T_(), 0);
@@ -2685,7 +2717,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
     // ---- role B: dP, dS, dK ----
     const bf16* vb = v + vw.v.at(bh, vw.heads);
     bf16x8 vf[KS];
-    load_row_frags<bf16, 128, true, false>(vf, vb, k0w, Sk, d, (int)vw.v.r);
+    if (rows_lds)
+      dma_rows32<128>(vb, k0w, Sk, (int)vw.v.r, rst);
+    else
+      load_row_frags<bf16, 128, true, false>(vf, vb, k0w, Sk, d, (int)vw.v.r);
     f32x16 dka[DT];
 #pragma unroll
     for (int u = 0; u < DT; ++u)
@@ -2773,6 +2808,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
     };
     // Half-step h: SDP (dP) for 0 <= h < nh, SG (dS) and GRAD (dK) for 1 <= h <= nh.
     sync(-1);
+    if (rows_lds) row_frags_lds<128>(vf, rst);
     stage(P1(), F_(), F_(), F_(), -1);
     sync(0);
     stage(P0(), T_(), F_(), F_(), 0);

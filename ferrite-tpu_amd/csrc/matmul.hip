@@ -519,48 +519,58 @@ __global__ __launch_bounds__(64 * W, W == 8 ? 2 : 1) void gemm_dma_kernel(const 
 
   // Epilogue: acc[j][i] is a C^T tile; register r of lane (l32, g) is
   // C[m0 + wm0 + 32 i + l32][n0 + wn0 + 32 j + (r / 4) * 8 + g * 4 + r % 4].
-  // The gradient epilogue's pre-activations are all loaded first, so their
-  // latency is paid once rather than once per store.
-  constexpr int UJ = EPI == kEpiGeluGrad ? YF : 1, UI = EPI == kEpiGeluGrad ? XF : 1;
-  bf16x4 ua[UJ][UI][4];
-  if constexpr (EPI == kEpiGeluGrad) {
-#pragma unroll
-    for (int j = 0; j < YF; ++j)
-#pragma unroll
-      for (int i = 0; i < XF; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int m = m0 + wm0 + 32 * i + l32, n = n0 + wn0 + 32 * j + 8 * q + 4 * g;
-          ua[j][i][q] = m < M && n < N ? *reinterpret_cast<const bf16x4*>(aux + (int64_t)m * N + n) : bf16x4{};
-        }
-  }
-  // Row group i outermost: a row's YF * 32 columns (whole 128-byte lines) go out in
-  // consecutive stores; with the column tiles outermost the halves of each line were
-  // written 16 stores apart and half-written lines reached HBM twice (1.5x the bytes).
+  // Stored straight from there, every store instruction would touch 32 rows
+  // (32 cache lines for 512 bytes). Each 32-row group of the wave's outputs
+  // goes through the wave's own part of the (now idle) stage ring instead:
+  // written as 16-byte chunks XOR-swizzled by row, read back 16 bytes per lane,
+  // so that each store instruction writes whole row segments of the wave's
+  // YF * 32 columns. The barrier: every wave has finished its fragment reads
+  // and every DMA has landed (each wave waited for its own just above).
+  constexpr int kEs = sizeof(TO), kRowBytes = YF * 32 * kEs, kCh = kRowBytes / 16, kRowsPerInst = 64 / kCh;
+  constexpr int kPer = 16 / kEs;  // outputs per 16-byte chunk
+  static_assert(W * 32 * kRowBytes <= SLOTS * kStageBytes, "every wave's row group fits the stage ring");
+  lds_barrier();
+  char* const ep = smem + wave * (32 * kRowBytes);
 #pragma unroll
   for (int i = 0; i < XF; ++i) {
 #pragma unroll
-    for (int j = 0; j < YF; ++j) {
-      const int m = m0 + wm0 + 32 * i + l32;
-      if (m >= M) continue;
+    for (int j = 0; j < YF; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn0 + 32 * j + 8 * q + 4 * g;
-        if (n >= N) continue;  // N % 8 == 0: a quad is either all in or all out
-        TO* dst = out + (int64_t)m * N + n;
-        if constexpr (EPI != kEpiNone) {
-          const bf16x4 v = {(bf16)acc[j][i][4 * q], (bf16)acc[j][i][4 * q + 1], (bf16)acc[j][i][4 * q + 2],
-                            (bf16)acc[j][i][4 * q + 3]};
-          if constexpr (EPI == kEpiGelu)
-            gelu_store(v, reinterpret_cast<bf16*>(dst), aux + (int64_t)m * N + n);
-          else
-            gelu_grad_store(v, ua[j][i < UI ? i : 0][q], reinterpret_cast<bf16*>(dst));
-        } else if constexpr (sizeof(TO) == 2) {
-          *reinterpret_cast<bf16x4*>(dst) = bf16x4{(bf16)acc[j][i][4 * q], (bf16)acc[j][i][4 * q + 1],
-                                                   (bf16)acc[j][i][4 * q + 2], (bf16)acc[j][i][4 * q + 3]};
+        if constexpr (kEs == 2) {
+          const int ch = 4 * j + q;  // columns 32 j + 8 q .. + 7; this lane's half 4 g .. + 3
+          *reinterpret_cast<bf16x4*>(ep + l32 * kRowBytes + ((ch ^ (l32 & (kCh - 1))) * 16) + 8 * g) =
+              bf16x4{(bf16)acc[j][i][4 * q], (bf16)acc[j][i][4 * q + 1], (bf16)acc[j][i][4 * q + 2],
+                     (bf16)acc[j][i][4 * q + 3]};
         } else {
-          *reinterpret_cast<f32x4*>(dst) =
+          const int ch = 8 * j + 2 * q + g;  // columns 32 j + 8 q + 4 g .. + 3
+          *reinterpret_cast<f32x4*>(ep + l32 * kRowBytes + ((ch ^ (l32 & (kCh - 1))) * 16)) =
               f32x4{acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]};
+        }
+      }
+    const int mg = m0 + wm0 + 32 * i;
+#pragma unroll
+    for (int rr = 0; rr < 32 / kRowsPerInst; ++rr) {
+      const int r = rr * kRowsPerInst + lane / kCh, c = lane % kCh;
+      const int m = mg + r, n = n0 + wn0 + c * kPer;
+      const u32x4 w4 = *reinterpret_cast<const u32x4*>(ep + r * kRowBytes + ((c ^ (r & (kCh - 1))) * 16));
+      // N % 8 == 0: a chunk is either all in or all out.
+      if (m < M && n < N) {
+        TO* dst = out + (int64_t)m * N + n;
+        if constexpr (EPI == kEpiNone) {
+          *reinterpret_cast<u32x4*>(dst) = w4;
+        } else {
+          const bf16x8 v = __builtin_bit_cast(bf16x8, w4);
+          const bf16x4 lo = {v[0], v[1], v[2], v[3]}, hi = {v[4], v[5], v[6], v[7]};
+          bf16* const a = aux + (int64_t)m * N + n;
+          if constexpr (EPI == kEpiGelu) {
+            gelu_store(lo, reinterpret_cast<bf16*>(dst), a);
+            gelu_store(hi, reinterpret_cast<bf16*>(dst) + 4, a + 4);
+          } else {
+            const bf16x8 u = *reinterpret_cast<const bf16x8*>(a);
+            gelu_grad_store(lo, bf16x4{u[0], u[1], u[2], u[3]}, reinterpret_cast<bf16*>(dst));
+            gelu_grad_store(hi, bf16x4{u[4], u[5], u[6], u[7]}, reinterpret_cast<bf16*>(dst) + 4);
+          }
         }
       }
     }
