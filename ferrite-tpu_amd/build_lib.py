@@ -38,8 +38,18 @@ HIPCC_FLAGS = [
 # read is an extra v_accvgpr_read (a quarter of dK/dV's VALU instructions). Measured A/B on one
 # MI355X, outputs bitwise equal: dK/dV 166.8 -> 159.9 us at 4x16x2048x128 and 199.7 -> 182.9 us
 # at 1x8x8192x64; the forward and dQ kernels (already all-VGPR) are unchanged.
+#
+# attention.hip also skips the control-flow structurizer on uniform regions. Every branch of the
+# attention kernels is wave-uniform (tile counts, parities, row-block bounds), and the
+# structurized form of the forward's pipeline tail (the diagonal stage of either parity, the
+# one-tile case) kept the accumulators of sibling paths live across each other: the D = 128
+# forward needed 256 VGPRs and 12 dwords of scratch per lane, written once per wave (5.5 MiB of
+# HBM writes per launch). Without it the same kernel takes 231 VGPRs and no scratch, and every
+# attention kernel uses fewer VGPRs. Measured A/B on one MI355X (medians of 7 interleaved
+# rounds, outputs bitwise equal): forward 73.5 -> 73.2 us at 4x16x2048x128 and 91.0 -> 91.6 us
+# at 1x8x8192x64, dQ with delta 135.6 -> 133.0 us at 1x8x8192x64, the rest unchanged.
 SOURCE_FLAGS = {
-    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-structurizecfg-skip-uniform-regions=true"],
 }
 
 
