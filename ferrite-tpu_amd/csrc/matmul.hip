@@ -89,26 +89,30 @@ struct Gemm {
     return v;
   }
 
+  // Thread t of the tile's kThreads loads its share of the k-step from k0; k from
+  // kend on (the end of K, or of the caller's K slice) reads as zero.
   static __device__ __forceinline__ void load(Stage& s, const T* x, const T* y, int64_t m0, int64_t n0, int64_t k0,
-                                              int64_t M, int64_t N, int64_t K) {
-    const int t = threadIdx.x;
+                                              int64_t M, int64_t N, int64_t K, int64_t kend, int t) {
 #pragma unroll
     for (int i = 0; i < kAVecs; ++i) {
       const int idx = t + kThreads * i;
       const int row = idx / (BK / kVec), cv = idx % (BK / kVec);
-      s.a[i] = load_vec(x, m0 + row, k0 + cv * kVec, M, K, K);
+      s.a[i] = load_vec(x, m0 + row, k0 + cv * kVec, M, kend, K);
     }
 #pragma unroll
     for (int j = 0; j < kBJobs; ++j) {
       const int job = t + kThreads * j;
       const int cg = job % (BN / kVec), kg = job / (BN / kVec);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s.b[j][r] = load_vec(y, k0 + kg * 4 + r, n0 + cg * kVec, K, N, N);
+      for (int r = 0; r < 4; ++r) s.b[j][r] = load_vec(y, k0 + kg * 4 + r, n0 + cg * kVec, kend, N, N);
     }
   }
+  static __device__ __forceinline__ void load(Stage& s, const T* x, const T* y, int64_t m0, int64_t n0, int64_t k0,
+                                              int64_t M, int64_t N, int64_t K) {
+    load(s, x, y, m0, n0, k0, M, N, K, K, threadIdx.x);
+  }
 
-  static __device__ __forceinline__ void store(const Stage& s, char* lds) {
-    const int t = threadIdx.x;
+  static __device__ __forceinline__ void store(const Stage& s, char* lds, int t = threadIdx.x) {
     char* as = lds;
     char* bs = lds + BM * 128;
 #pragma unroll
@@ -153,20 +157,30 @@ struct Gemm {
       for (int i = 0; i < kTM; ++i) fa[i] = read_frag<T>(as, wm0 + i * 32 + l32, kk * 16 + g * 8);
 #pragma unroll
       for (int j = 0; j < kTN; ++j) fb[j] = read_frag<T>(bs, wn0 + j * 32 + l32, kk * 16 + g * 8);
+      if constexpr (sizeof(T) == 4) {
+        // f32: the eight k-steps of every accumulator in turn, so that consecutive
+        // 32x32x2 products go to different accumulators.
 #pragma unroll
-      for (int j = 0; j < kTN; ++j)
+        for (int e = 0; e < 8; ++e)
 #pragma unroll
-        for (int i = 0; i < kTM; ++i) mma32(fb[j], fa[i], acc[j][i]);
+          for (int j = 0; j < kTN; ++j)
+#pragma unroll
+            for (int i = 0; i < kTM; ++i)
+              acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[j][e], fa[i][e], acc[j][i], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int j = 0; j < kTN; ++j)
+#pragma unroll
+          for (int i = 0; i < kTM; ++i) mma32(fb[j], fa[i], acc[j][i]);
+      }
     }
   }
 };
 
-// blockIdx.y is the K slice: k from kslice * blockIdx.y, at most kslice deep (a
-// multiple of BK), into the f32 partial slab blockIdx.y of `out` when split.
 template <typename T, typename TO, int BM, int BN, int BK, int WM, int WN, bool ALIGNED>
 __global__ __launch_bounds__((WM * WN * 64), 1) void gemm_kernel(const T* __restrict__ x, const T* __restrict__ y,
                                                               TO* __restrict__ out, int64_t M, int64_t N, int64_t K,
-                                                              int tiles_n, int64_t kslice) {
+                                                              int tiles_n) {
   typedef Gemm<T, TO, BM, BN, BK, WM, WN, ALIGNED> G;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tile = blockIdx.x;
@@ -183,16 +197,14 @@ __global__ __launch_bounds__((WM * WN * 64), 1) void gemm_kernel(const T* __rest
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
 
-  const int64_t kbeg = kslice * blockIdx.y;
-  out += (int64_t)blockIdx.y * M * N;
-  const int nk = (int)((std::min(K - kbeg, kslice) + BK - 1) / BK);
+  const int nk = (int)((K + BK - 1) / BK);
   typename G::Stage st;
-  G::load(st, x, y, m0, n0, kbeg, M, N, K);
+  G::load(st, x, y, m0, n0, 0, M, N, K);
   G::store(st, smem);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     char* cur = smem + (kt & 1) * G::kStageBytes;
-    if (kt + 1 < nk) G::load(st, x, y, m0, n0, kbeg + (int64_t)(kt + 1) * BK, M, N, K);
+    if (kt + 1 < nk) G::load(st, x, y, m0, n0, (int64_t)(kt + 1) * BK, M, N, K);
     G::compute(cur, acc, wm0, wn0);
     if (kt + 1 < nk) G::store(st, smem + ((kt + 1) & 1) * G::kStageBytes);
     __syncthreads();
@@ -226,6 +238,99 @@ __global__ __launch_bounds__((WM * WN * 64), 1) void gemm_kernel(const T* __rest
           for (int e = 0; e < 4; ++e)
             if (n + e < N) dst[e] = Elem<TO>::from_f32(acc[j][i][q * 4 + e]);
         }
+      }
+    }
+  }
+}
+
+// f32 products with few output tiles (1000^3 has 256 tiles of 64 x 64): S slices of
+// K for one tile in one workgroup of 2S waves, each pair of waves running the
+// two-wave 64 x 64 loop above over its slice from its own pair of LDS stages. At
+// the end slices 1 .. S-1 leave their accumulators in LDS and slice 0 adds them
+// in slice order, so the K split needs no partial slabs in HBM and no second
+// kernel, and the sum's order does not depend on timing. With still fewer tiles,
+// blockIdx.y selects one of several groups of S slices, whose sums go to the f32
+// partial slab blockIdx.y of `out` for gemm_splitk_reduce_kernel.
+template <typename TO, int S, bool ALIGNED>
+__global__ __launch_bounds__(128 * S, 1) void gemm_f32_slices_kernel(const float* __restrict__ x,
+                                                                    const float* __restrict__ y,
+                                                                    TO* __restrict__ out, int64_t M, int64_t N,
+                                                                    int64_t K, int tiles_n, int64_t kslice) {
+  typedef Gemm<float, TO, 64, 64, 32, 1, 2, ALIGNED> G;
+  static_assert(G::kThreads == 128 && G::kTN == 1 && G::kTM == 2, "two waves of 64 x 32 per slice");
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tile = blockIdx.x;
+  const int64_t m0 = (int64_t)(tile / tiles_n) * 64;
+  const int64_t n0 = (int64_t)(tile % tiles_n) * 64;
+  const int slice = threadIdx.x >> 7, t = threadIdx.x & 127;
+  const int wn0 = ((threadIdx.x >> 6) & 1) * 32;
+  char* const lds = smem + slice * 2 * G::kStageBytes;
+
+  f32x16 acc[1][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[0][i][r] = 0.f;
+
+  // Every slice runs the same number of k-steps (the workgroup's barriers are
+  // shared); a short last slice reads zeros past K.
+  const int64_t kbeg = kslice * ((int64_t)blockIdx.y * S + slice), kend = std::min(K, kbeg + kslice);
+  out += (int64_t)blockIdx.y * M * N;
+  const int nk = (int)(kslice / 32);
+  typename G::Stage st;
+  G::load(st, x, y, m0, n0, kbeg, M, N, K, kend, t);
+  G::store(st, lds, t);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    char* cur = lds + (kt & 1) * G::kStageBytes;
+    if (kt + 1 < nk) G::load(st, x, y, m0, n0, kbeg + (int64_t)(kt + 1) * 32, M, N, K, kend, t);
+    G::compute(cur, acc, 0, wn0);
+    if (kt + 1 < nk) G::store(st, lds + ((kt + 1) & 1) * G::kStageBytes, t);
+    __syncthreads();
+  }
+
+  // Slice s > 0 writes register r of accumulator i of its lane to dword
+  // (i * 16 + r) * 128 + t of its exchange area; slice 0 reads the same places.
+  float* const xch = reinterpret_cast<float*>(smem);
+  if (slice > 0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xch[((slice - 1) * 32 + i * 16 + r) * 128 + t] = acc[0][i][r];
+  }
+  __syncthreads();
+  if (slice > 0) return;
+#pragma unroll
+  for (int s2 = 1; s2 < S; ++s2)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[0][i][r] += xch[((s2 - 1) * 32 + i * 16 + r) * 128 + t];
+
+  // Register r of accumulator i of lane (l32, g): C[m0 + i*32 + l32][n0 + wn0 + (r/4)*8 + g*4 + r%4].
+  const int lane = threadIdx.x & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t m = m0 + i * 32 + l32;
+    if (m >= M) continue;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t n = n0 + wn0 + q * 8 + g * 4;
+      TO* dst = out + m * N + n;
+      if (ALIGNED && n + 3 < N) {
+        if constexpr (sizeof(TO) == 2) {
+          bf16x4 v = {(bf16)acc[0][i][q * 4 + 0], (bf16)acc[0][i][q * 4 + 1], (bf16)acc[0][i][q * 4 + 2],
+                      (bf16)acc[0][i][q * 4 + 3]};
+          *reinterpret_cast<bf16x4*>(dst) = v;
+        } else {
+          *reinterpret_cast<f32x4*>(dst) =
+              f32x4{acc[0][i][q * 4 + 0], acc[0][i][q * 4 + 1], acc[0][i][q * 4 + 2], acc[0][i][q * 4 + 3]};
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) dst[e] = Elem<TO>::from_f32(acc[0][i][q * 4 + e]);
       }
     }
   }
@@ -600,44 +705,99 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
 
 template <typename T, typename TO, int BM, int BN, int BK, int WM, int WN, bool AL>
 void launch_gemm_kernel(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, int64_t tiles,
-                        int64_t tiles_n, int slices, int64_t kslice, size_t lds, hipStream_t stream) {
+                        int64_t tiles_n, size_t lds, hipStream_t stream) {
   auto k = gemm_kernel<T, TO, BM, BN, BK, WM, WN, AL>;
   (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  hipLaunchKernelGGL(k, dim3((unsigned)tiles, (unsigned)slices), dim3(WM * WN * 64), lds, stream,
-                     static_cast<const T*>(x), static_cast<const T*>(y), static_cast<TO*>(out), M, N, K, (int)tiles_n,
-                     kslice);
+  hipLaunchKernelGGL(k, dim3((unsigned)tiles), dim3(WM * WN * 64), lds, stream, static_cast<const T*>(x),
+                     static_cast<const T*>(y), static_cast<TO*>(out), M, N, K, (int)tiles_n);
 }
 
 template <typename T, typename TO, int BM, int BN, int BK, int WM, int WN>
-int launch_gemm(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, hipStream_t stream,
-                int slices = 1, void* ws = nullptr) {
+int launch_gemm(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
   typedef Gemm<T, TO, BM, BN, BK, WM, WN, true> G;
   const int64_t tiles_m = cdiv(M, BM), tiles_n = cdiv(N, BN);
   if (tiles_m * tiles_n > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "matmul: output too large");
   const size_t lds = 2 * (size_t)G::kStageBytes;
   auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  const bool aligned = K % Elem<T>::kVec == 0 && N % Elem<T>::kVec == 0 && N % 4 == 0 && a16(x) && a16(y) &&
-                       a16(slices > 1 ? ws : out);
-  const int64_t kslice = slices > 1 ? cdiv(cdiv(K, slices), (int64_t)BK) * BK : K;
-  if (slices > 1) slices = (int)cdiv(K, kslice);
-  if (slices > 1) {
-    if (aligned)
-      launch_gemm_kernel<T, float, BM, BN, BK, WM, WN, true>(x, y, ws, M, N, K, tiles_m * tiles_n, tiles_n, slices,
-                                                             kslice, lds, stream);
-    else
-      launch_gemm_kernel<T, float, BM, BN, BK, WM, WN, false>(x, y, ws, M, N, K, tiles_m * tiles_n, tiles_n, slices,
-                                                              kslice, lds, stream);
+  const bool aligned =
+      K % Elem<T>::kVec == 0 && N % Elem<T>::kVec == 0 && N % 4 == 0 && a16(x) && a16(y) && a16(out);
+  if (aligned)
+    launch_gemm_kernel<T, TO, BM, BN, BK, WM, WN, true>(x, y, out, M, N, K, tiles_m * tiles_n, tiles_n, lds, stream);
+  else
+    launch_gemm_kernel<T, TO, BM, BN, BK, WM, WN, false>(x, y, out, M, N, K, tiles_m * tiles_n, tiles_n, lds, stream);
+  return check_launch("ferrite_matmul");
+}
+
+// The K split of an f32 product with few output tiles (64 x 64 each): S slices per
+// workgroup (gemm_f32_slices_kernel), 4 or 2 while the workgroups' waves stay within
+// two per SIMD and each slice is at least 128 deep (1000^3: 256 tiles x 4 slices x 2
+// waves = two waves per SIMD); when that still fills under half the SIMDs, G groups
+// of S slices in G workgroups per tile, summed by a second pass (512 x 512 x 2048:
+// 64 tiles, S = 4, G = 4).
+struct F32Split {
+  int s, g;
+};
+F32Split f32_split(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = cdiv(M, (int64_t)64) * cdiv(N, (int64_t)64);
+  const int64_t waves = 8 * (int64_t)cu_count();  // two per SIMD
+  int s = K >= 512 ? 4 : K >= 256 ? 2 : 1;
+  while (s > 1 && tiles * 2 * s > waves) s /= 2;
+  int64_t g = 1;
+  if (2 * tiles * 2 * s <= waves && (M * N) % 4 == 0)
+    g = std::min<int64_t>({cdiv(waves, tiles * 2 * s), K / (128 * s), (int64_t)8});
+  return {s, (int)std::max<int64_t>(g, 1)};
+}
+int64_t f32_workspace(int64_t M, int64_t N, int64_t K) {
+  const F32Split sp = f32_split(M, N, K);
+  return sp.g > 1 ? (int64_t)sp.g * M * N * (int64_t)sizeof(float) : 0;
+}
+
+template <typename TO, int S>
+void launch_gemm_f32_slices(const float* x, const float* y, TO* out, int64_t M, int64_t N, int64_t K, int groups,
+                            hipStream_t stream) {
+  typedef Gemm<float, TO, 64, 64, 32, 1, 2, true> G;
+  const int64_t tiles_n = cdiv(N, (int64_t)64), tiles = cdiv(M, (int64_t)64) * tiles_n;
+  const size_t lds = (size_t)S * 2 * G::kStageBytes;
+  static_assert((S - 1) * 32 * 128 * 4 <= S * 2 * G::kStageBytes, "the slices' accumulators fit the stages");
+  const int64_t kslice = cdiv(cdiv(K, (int64_t)S * groups), (int64_t)32) * 32;
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const bool aligned = K % 4 == 0 && N % 4 == 0 && a16(x) && a16(y) && a16(out);
+  auto go = [&](auto kern) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)groups), dim3(128 * S), lds, stream, x, y, out, M, N, K,
+                       (int)tiles_n, kslice);
+  };
+  if (aligned)
+    go(gemm_f32_slices_kernel<TO, S, true>);
+  else
+    go(gemm_f32_slices_kernel<TO, S, false>);
+}
+
+template <typename TO, int S>
+int launch_gemm_f32_split(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, int groups,
+                          void* ws, hipStream_t stream) {
+  const float* xf = static_cast<const float*>(x);
+  const float* yf = static_cast<const float*>(y);
+  if (groups > 1) {
+    launch_gemm_f32_slices<float, S>(xf, yf, static_cast<float*>(ws), M, N, K, groups, stream);
     const int64_t mn = M * N;
     hipLaunchKernelGGL((gemm_splitk_reduce_kernel<TO>), dim3((unsigned)cdiv(mn / 4, 256)), dim3(256), 0, stream,
-                       static_cast<const float*>(ws), static_cast<TO*>(out), mn, slices, nullptr);
-  } else if (aligned) {
-    launch_gemm_kernel<T, TO, BM, BN, BK, WM, WN, true>(x, y, out, M, N, K, tiles_m * tiles_n, tiles_n, 1, K, lds,
-                                                        stream);
+                       static_cast<const float*>(ws), static_cast<TO*>(out), mn, groups, nullptr);
   } else {
-    launch_gemm_kernel<T, TO, BM, BN, BK, WM, WN, false>(x, y, out, M, N, K, tiles_m * tiles_n, tiles_n, 1, K, lds,
-                                                         stream);
+    launch_gemm_f32_slices<TO, S>(xf, yf, static_cast<TO*>(out), M, N, K, 1, stream);
   }
   return check_launch("ferrite_matmul");
+}
+
+template <typename TO>
+int launch_gemm_f32_small(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, void* ws,
+                          int64_t ws_bytes, hipStream_t stream) {
+  F32Split sp = f32_split(M, N, K);
+  if (sp.g > 1 && (ws == nullptr || ws_bytes < f32_workspace(M, N, K) || (reinterpret_cast<uintptr_t>(ws) & 15)))
+    sp.g = 1;
+  if (sp.s == 4) return launch_gemm_f32_split<TO, 4>(x, y, out, M, N, K, sp.g, ws, stream);
+  if (sp.s == 2) return launch_gemm_f32_split<TO, 2>(x, y, out, M, N, K, sp.g, ws, stream);
+  return launch_gemm<float, TO, 64, 64, 32, 1, 2>(x, y, out, M, N, K, stream);
 }
 
 // K slices for a problem with few output tiles: as many slices as keep every
@@ -662,21 +822,9 @@ int64_t splitk_workspace(int64_t M, int64_t N, int64_t K) {
   return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
 }
 
-// f32 products too small for 128 x 128 tiles on every CU run 64 x 64 tiles of two
-// waves; with fewer than two waves per SIMD they also split K, each slice at least
-// 128 deep (1000^3: 256 tiles, 512 waves for 1024 SIMDs, so 4 slices).
+// f32 products too small for 128 x 128 tiles on every CU run 64 x 64 tiles
+// (launch_gemm_f32_small).
 bool f32_small(int64_t M, int64_t N) { return cdiv(M, (int64_t)128) * cdiv(N, (int64_t)128) < cu_count(); }
-int f32_slices(int64_t M, int64_t N, int64_t K) {
-  if (!f32_small(M, N) || (M * N) % 4 != 0) return 1;
-  const int64_t waves = 2 * cdiv(M, (int64_t)64) * cdiv(N, (int64_t)64);
-  const int64_t s = std::min<int64_t>({cdiv(8 * (int64_t)cu_count(), waves), K / 128, (int64_t)8});
-  if (s < 2) return 1;
-  return (int)cdiv(K, cdiv(cdiv(K, s), (int64_t)32) * 32);
-}
-int64_t f32_workspace(int64_t M, int64_t N, int64_t K) {
-  const int s = f32_slices(M, N, K);
-  return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
-}
 
 // Output rows per workgroup. 128-row tiles (k-contiguous x only) halve the work of a
 // tile, so a problem whose 256-row tiles spill into a mostly empty round, or fill
@@ -779,7 +927,8 @@ bool dma_ok(const void* x, const void* y, const void* out, int64_t m, int64_t n,
 
 extern "C" int64_t ferrite_hip_matmul_workspace(int64_t m, int64_t n, int64_t k, int in_dtype) {
   if (m < 1 || n < 1 || k < 1) return -1;
-  return in_dtype == FERRITE_BF16 ? ferrite::splitk_workspace(m, n, k) : ferrite::f32_workspace(m, n, k);
+  if (in_dtype == FERRITE_BF16) return ferrite::splitk_workspace(m, n, k);
+  return ferrite::f32_small(m, n) ? ferrite::f32_workspace(m, n, k) : 0;
 }
 
 extern "C" int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k,
@@ -807,14 +956,11 @@ extern "C" int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, in
     return launch_gemm<bf16, float, 128, 128, 64, 2, 2>(x, y, out, m, n, k, s);
   }
   // f32: 128 x 128 tiles of four waves reach ~80% of the fp32 MFMA peak at 4096^3; a
-  // problem with fewer such tiles than CUs (1000^3 has 64) runs 64 x 64 tiles of two
-  // waves instead, four times the workgroups (1000^3: 81 -> 50 us on MI355X), and splits
-  // K when that still leaves SIMDs idle and the caller gives a workspace.
+  // problem with fewer such tiles than CUs (1000^3 has 64) runs 64 x 64 tiles instead,
+  // with K split inside the workgroup while SIMDs would stay idle.
   if (f32_small(m, n)) {
-    int sl = f32_slices(m, n, k);
-    if (sl > 1 && (!workspace || workspace_bytes < f32_workspace(m, n, k))) sl = 1;
-    if (out_dtype == FERRITE_BF16) return launch_gemm<float, bf16, 64, 64, 32, 1, 2>(x, y, out, m, n, k, s, sl, workspace);
-    return launch_gemm<float, float, 64, 64, 32, 1, 2>(x, y, out, m, n, k, s, sl, workspace);
+    if (out_dtype == FERRITE_BF16) return launch_gemm_f32_small<bf16>(x, y, out, m, n, k, workspace, workspace_bytes, s);
+    return launch_gemm_f32_small<float>(x, y, out, m, n, k, workspace, workspace_bytes, s);
   }
   if (out_dtype == FERRITE_BF16) return launch_gemm<float, bf16, 128, 128, 32, 2, 2>(x, y, out, m, n, k, s);
   return launch_gemm<float, float, 128, 128, 32, 2, 2>(x, y, out, m, n, k, s);
