@@ -115,6 +115,43 @@ def test_every_element_written_and_deterministic(dev):
     assert torch.equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("m,k,n", [
+    (1000, 1000, 1000),  # 4 K slices in each workgroup (the BASELINE f32 shape)
+    (1000, 1003, 999),   # the same, unaligned rows (N % 4 != 0)
+    (512, 2048, 512),    # 4 slices per workgroup x 4 groups of workgroups, summed from the workspace
+    (132, 2050, 67),     # groups of slices, unaligned rows and a ragged last slice
+    (1400, 700, 1400),   # 2 slices per workgroup (4 would exceed two waves per SIMD)
+    (300, 300, 300),     # 2 slices, K under 512
+    (100, 100, 100),     # no split (K too short for 128-deep slices)
+])
+def test_f32_small_products_split_k(dev, m, k, n):
+    """f32 products with few output tiles split K inside the workgroup (and, with very few
+    tiles, across workgroups through the workspace). Every element is written (NaN-prefilled),
+    the result is within 1e-5 of the f64 product relative to its largest magnitude, and two
+    runs are bitwise equal (the slices are summed in a fixed order)."""
+    x, y = uniform(31, (m, k), "f32"), uniform(32, (k, n), "f32")
+    xt, yt = to_dev(x, "f32", dev), to_dev(y, "f32", dev)
+    exact = x.astype(np.float64) @ y.astype(np.float64)
+    lib = _hip.lib()
+    ws_bytes = lib.ferrite_hip_matmul_workspace(m, n, k, _hip.F32)
+    ws = torch.empty(max(ws_bytes, 16) // 4, dtype=torch.float32, device=dev)
+    for out_code, tdt in ((_hip.F32, torch.float32), (_hip.BF16, torch.bfloat16)):
+        outs = []
+        for _ in range(2):
+            o = torch.full((m, n), float("nan"), dtype=tdt, device=dev)
+            _hip.check(lib.ferrite_hip_matmul_ex(xt.data_ptr(), yt.data_ptr(), o.data_ptr(), m, n, k, 0, 0, _hip.F32,
+                                                 out_code, ws.data_ptr(), ws_bytes, _hip.stream_of(xt)), "matmul")
+            torch.cuda.synchronize()
+            outs.append(o.clone())
+        got = to_np(outs[0]).astype(np.float64)
+        assert not np.isnan(got).any()
+        assert torch.equal(outs[0], outs[1])
+        if tdt == torch.float32:
+            assert np.max(np.abs(got - exact)) <= 1e-5 * np.max(np.abs(exact))
+        else:
+            assert np.all(np.abs(got - exact) <= bf16_ulp(exact) + 1e-5 * np.max(np.abs(exact)))
+
+
 @pytest.mark.parametrize("m,k,n", [(300, 128, 264), (257, 192, 520), (1000, 512, 776), (64, 64, 8)])
 def test_bf16_dma_path_tails(dev, m, k, n):
     """bf16 inputs with K a multiple of 64 and N a multiple of 8 take the DMA-fed kernel, whose
