@@ -152,8 +152,9 @@ int ferrite_hip_matmul(const void* x, const void* y, void* out, int64_t m, int64
  * and 16-byte aligned pointers; otherwise the call fails with
  * FERRITE_ERR_INVALID_ARGUMENT. With a workspace of at least
  * ferrite_hip_matmul_workspace(m, n, k, in_dtype) bytes (0 = the shape does not
- * split), a bf16 problem with few output tiles splits K across workgroups and
- * sums the f32 partials in a fixed order (deterministic); with NULL it does not split.
+ * split), a problem with few output tiles (bf16; f32 with very few, after its split
+ * inside each workgroup) splits K across workgroups and sums the f32 partials in a
+ * fixed order (deterministic); with NULL it does not split across workgroups.
  */
 int64_t ferrite_hip_matmul_workspace(int64_t m, int64_t n, int64_t k, int in_dtype);
 int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k, int x_t, int y_t,
