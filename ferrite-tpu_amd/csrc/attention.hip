@@ -946,10 +946,13 @@ __device__ __forceinline__ void pin(bf16x8& f) {
   f = __builtin_bit_cast(bf16x8, w);
 }
 
-template <int D, int RB, int W>
+// KSPLIT = 2: the waves form pairs on one SIMD (waves w and w + W / 2) that
+// take the same rows and split every 64-key tile, keys 0-31 and 32-63; the
+// pair merges its softmax states at the end.
+template <int D, int RB, int W, int KSPLIT = 1>
 struct FwdW {
   static constexpr int kWaves = W, kThreads = 64 * kWaves;
-  static constexpr int BQ = 32 * RB * W, BK = 64;
+  static constexpr int BQ = 32 * RB * W / KSPLIT, BK = 64;
   static constexpr int KS = D / 16, DT = D / 32;
   typedef PpKTile<D> KT;
   typedef PpVTile<D> VT;
@@ -960,11 +963,11 @@ struct FwdW {
   static_assert(KT::kBlocks == VT::kBlocks && kDma >= 1, "K and V tiles split evenly over the waves");
 };
 
-template <int D, int RB, int W, bool ZIG>
-__global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void attn_fwd_sw_kernel(
+template <int D, int RB, int W, bool ZIG, int KSPLIT = 1>
+__global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4 : W == 4 ? 2 : 1)) void attn_fwd_sw_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, bf16* __restrict__ o,
     float* __restrict__ lse, int bh_count, int S, int d, float scale_log2, int neg_q, int n_qtiles, AttnViews vw) {
-  typedef FwdW<D, RB, W> F;
+  typedef FwdW<D, RB, W, KSPLIT> F;
   typedef typename F::KT KT;
   typedef typename F::VT VT;
   constexpr int KS = F::KS, DT = F::DT;
@@ -983,12 +986,18 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
+  // Row block of the wave and, with KSPLIT = 2, its key subtile of every tile
+  // (NKT subtiles of 32 keys per tile and wave).
+  constexpr int WR = W / KSPLIT, NKT = 2 / KSPLIT;
+  const int wr = wave % WR;
+  const int kh = KSPLIT == 1 ? 0 : wave / WR;
   const int q0 = qt * F::BQ;
-  const int q0w = q0 + 32 * RB * wave;
+  const int q0w = q0 + 32 * RB * wr;
   // Tiles of 64 keys: n for the workgroup, n_w for this wave, whose last
-  // tile (keys from 64 (n_w - 1)) is its diagonal.
+  // tile (keys from 64 (n_w - 1)) is its diagonal. The upper key half of the
+  // first 32 rows sees no key at all: that wave computes nothing.
   const int n = (min(q0 + F::BQ, S) - 1) / F::BK + 1;
-  const int n_w = q0w < S ? (q0w + 32 * RB - 1) / F::BK + 1 : 0;
+  const int n_w = q0w < S && !(kh == 1 && q0w == 0) ? (q0w + 32 * RB - 1) / F::BK + 1 : 0;
 
   // Row pitches (elements): d for dense [B, H, S, d] tensors.
   const int ldq = (int)vw.q.r, ldk = (int)vw.k.r, ldv = (int)vw.v.r;
@@ -1026,7 +1035,7 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
     }
   }
 
-  const int kbase = KT::off(l32, g * 16);
+  const int kbase = KT::off(32 * kh + l32, g * 16);
   const int vbase = VT::off((lane >> 5) * 16 + ((lane & 15) >> 2), 2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
   // Diagonal tile: key kt*32 + g*16 + r of the tile is invisible to row
   // rb*32 + l32 of the wave when r > lim[rb][kt].
@@ -1043,8 +1052,8 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
     for (int u = 0; u < DT; ++u)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[rb][u][r] = 0.f;
-  f32x16 s[2][2][RB];   // [buffer][key subtile][row block]: S^T of one tile
-  bf16x8 pf[2][RB][4];  // [buffer][row block][16-key chunk]: P^T fragments
+  f32x16 s[2][NKT][RB];       // [buffer][key subtile][row block]: S^T of one tile
+  bf16x8 pf[2][RB][2 * NKT];  // [buffer][row block][16-key chunk]: P^T fragments
   float m[RB], neg_m[RB], lsum[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
@@ -1076,41 +1085,46 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
     constexpr int P = decltype(P_)::value;
     constexpr bool QK = decltype(QK_)::value, SM = decltype(SM_)::value;
     constexpr bool MASK = decltype(MASK_)::value, PV = decltype(PV_)::value;
-    f32x16(&sn)[2][RB] = s[1 - P];
-    f32x16(&sc)[2][RB] = s[P];
-    bf16x8(&pc)[RB][4] = pf[P];
-    bf16x8(&pp)[RB][4] = pf[1 - P];
+    f32x16(&sn)[NKT][RB] = s[1 - P];
+    f32x16(&sc)[NKT][RB] = s[P];
+    bf16x8(&pc)[RB][2 * NKT] = pf[P];
+    bf16x8(&pp)[RB][2 * NKT] = pf[1 - P];
     const char* kp = kring + ((j + 1) % F::kSlots) * KT::kBytes + kbase;
     const char* vp = vring + ((j - 1 + F::kSlots) % F::kSlots) * VT::kBytes + vbase;
-    constexpr int NFQ = QK ? 2 * KS : 0;  // K fragments (key subtile f % 2, k-chunk f / 2)
-    constexpr int NFV = PV ? 4 * DT : 0;  // V^T fragments (key chunk i / DT, dim tile i % DT)
+    // K fragments: key subtile f % NKT (with KSPLIT = 2 the wave's own, whose
+    // rows kbase already points at), k-chunk f / NKT.
+    constexpr int NFQ = QK ? NKT * KS : 0;
+    // V^T fragments: the wave's key chunk i / DT of 16 keys (chunk 2 kh + i / DT
+    // of the tile with KSPLIT = 2), dim tile i % DT.
+    constexpr int NFV = PV ? 2 * NKT * DT : 0;
     constexpr int NF = NFQ + NFV;
     auto read = [&](int f) -> bf16x8 {
-      if (f < NFQ) return *reinterpret_cast<const bf16x8*>(kp + KT::off(32 * (f & 1), (f >> 1) * 32));
-      const int i = f - NFQ, c = i / DT, u = i % DT;
+      if (f < NFQ) return *reinterpret_cast<const bf16x8*>(kp + KT::off(32 * (f % NKT), (f / NKT) * 32));
+      const int i = f - NFQ, c = 2 * kh + i / DT, u = i % DT;
       return tr_frag(vp + VT::off((c >> 1) * 32 + (c & 1) * 8, u * 64), VT::off(4, 0));
     };
     // Product rb of fragment f.
     auto prod1 = [&](int f, int rb, const bf16x8& a) {
       if (f < NFQ) {
-        const int kt = f & 1, kc = f >> 1;
+        const int kt = f % NKT, kc = f / NKT;
         if (kc == 0)
           sn[kt][rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[rb][0], f32x16{}, 0, 0, 0);
         else
           mma32(a, qf[rb][kc], sn[kt][rb]);
       } else {
-        const int i = f - NFQ, c = i / DT, u = i % DT;
-        mma32(a, pp[rb][c], acc[rb][u]);
+        const int i = f - NFQ, cl = i / DT, u = i % DT;
+        mma32(a, pp[rb][cl], acc[rb][u]);
       }
     };
     float t[RB][2];  // [row block][partial] sums of this tile's p in the lane
-    // Softmax element e of the lane: row block e / 32, key subtile (e / 16) % 2,
-    // register e % 16. Every 8 elements make one P^T fragment.
+    // Softmax element e of the lane: row block e / (16 NKT), key subtile
+    // (e / 16) % NKT of the wave's (kt + kh of the tile), register e % 16.
+    // Every 8 elements make one P^T fragment.
     float p[8];
     auto softmax_elem = [&](int e, const float(&nm)[RB]) {
-      const int rb = e >> 5, kt = (e >> 4) & 1, r = e & 15;
+      const int rb = e / (16 * NKT), kt = (e >> 4) % NKT, r = e & 15;
       float x = sc[kt][rb][r];
-      if constexpr (MASK) x = r > lim[rb][kt] ? -INFINITY : x;
+      if constexpr (MASK) x = r > lim[rb][kt + kh] ? -INFINITY : x;
       p[r & 7] = __builtin_amdgcn_exp2f(__builtin_fmaf(x, scale_log2, nm[rb]));
       t[rb][r & 1] += p[r & 7];
       if ((r & 7) == 7) {
@@ -1121,7 +1135,7 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
         pin(f);
       }
     };
-    constexpr int NE = 32 * RB;  // softmax elements per lane
+    constexpr int NE = 16 * NKT * RB;  // softmax elements per lane
     auto softmax = [&](const float(&nm)[RB]) {
 #pragma unroll
       for (int e = 0; e < NE; ++e) softmax_elem(e, nm);
@@ -1179,11 +1193,11 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
         for (int rb = 0; rb < RB; ++rb) {
           float mx = -INFINITY;
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
+          for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               float x = sc[kt][rb][r];
-              if constexpr (MASK) x = r > lim[rb][kt] ? -INFINITY : x;
+              if constexpr (MASK) x = r > lim[rb][kt + kh] ? -INFINITY : x;
               mx = fmaxf(mx, x);
             }
           const float m_new = fmaxf(m[rb], lane32_max(mx) * scale_log2);
@@ -1286,8 +1300,48 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
   }
   wait_vmem<0>();
 
+  if constexpr (KSPLIT > 1) {
+    // The upper key half hands its accumulators, maxima and partial sums to
+    // the lower half of its rows through the (now idle) rings; the lower half
+    // rescales both to the larger maximum. A wave that computed nothing hands
+    // over zeros and -inf, which weigh nothing.
+    constexpr int kXs = (16 * DT + 2) * 64;  // floats per row block
+    static_assert(RB == 1 && WR * kXs * 4 <= F::kLds, "the upper halves' states fit the rings");
+    float* const xs = reinterpret_cast<float*>(smem) + wr * kXs;
+    lds_barrier();
+    if (kh == 1) {
+#pragma unroll
+      for (int u = 0; u < DT; ++u)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          *reinterpret_cast<f32x4*>(xs + ((u * 4 + r4) * 64 + lane) * 4) =
+              f32x4{acc[0][u][4 * r4], acc[0][u][4 * r4 + 1], acc[0][u][4 * r4 + 2], acc[0][u][4 * r4 + 3]};
+      xs[16 * DT * 64 + lane] = m[0];
+      xs[16 * DT * 64 + 64 + lane] = lsum[0];
+    }
+    lds_barrier();
+    if (kh == 0) {
+      const float m1 = xs[16 * DT * 64 + lane];
+      const float l1 = xs[16 * DT * 64 + 64 + lane];
+      const float mm = fmaxf(m[0], m1);
+      const float a0 = __builtin_amdgcn_exp2f(m[0] - mm), a1 = __builtin_amdgcn_exp2f(m1 - mm);
+#pragma unroll
+      for (int u = 0; u < DT; ++u)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x4 o1 = *reinterpret_cast<const f32x4*>(xs + ((u * 4 + r4) * 64 + lane) * 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[0][u][4 * r4 + e] = acc[0][u][4 * r4 + e] * a0 + o1[e] * a1;
+        }
+      lsum[0] = lsum[0] * a0 + l1 * a1;
+      m[0] = mm;
+    }
+  }
+  // The lower key half of each row block writes (every wave without KSPLIT).
+  const bool writer = kh == 0 && n_w > 0;
+
   if (d < D) {
-    if (n_w == 0) return;
+    if (!writer) return;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const int row = q0w + 32 * rb + l32;
@@ -1303,7 +1357,7 @@ __global__ __launch_bounds__((FwdW<D, RB, W>::kThreads), (W == 4 ? 2 : 1)) void 
   // landed.
   static_assert(F::kWaves * 32 * RB * 2 * D <= F::kLds, "every wave's rows fit the rings");
   lds_barrier();
-  if (n_w == 0) return;
+  if (!writer) return;
   char* const ot = smem + wave * (32 * RB * 2 * D);
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
@@ -2845,10 +2899,13 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
 // W waves of 32 queries; SLOTS K/V tile slots in LDS (3: tiles t + 1 and t + 2
 // load while tile t is used; 2: only t + 1, which halves the LDS so that two
 // workgroups share a CU).
-template <int D, int W = 8, int SLOTS = 3>
+// KSPLIT = 2: waves w and w + W / 2 (one SIMD) take the same queries and
+// split every 64-key tile, keys 0-31 and 32-63; their dQ partials add up at
+// the end.
+template <int D, int W = 8, int SLOTS = 3, int KSPLIT = 1>
 struct DqPp {
   static constexpr int kWaves = W, kThreads = 64 * kWaves;
-  static constexpr int BQ = 32 * kWaves, BK = 64, KS = D / 16, DT = D / 32;
+  static constexpr int BQ = 32 * kWaves / KSPLIT, BK = 64, KS = D / 16, DT = D / 32;
   typedef BwdTile<D> Tile;
   static constexpr int kSlots = SLOTS;
   static constexpr int kSlotBytes = 2 * Tile::kBytes;  // K then V
@@ -2870,8 +2927,8 @@ struct DqPp {
 // FUSED: delta is not read but computed here from O and dO (the rows' dO
 // fragments are loaded anyway) and written out for the dK/dV kernel, which
 // then runs after this one: the separate delta pass over O and dO goes away.
-template <int D, int W, int SLOTS, bool ZIG, bool FUSED = false>
-__global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+template <int D, int W, int SLOTS, bool ZIG, bool FUSED = false, int KSPLIT = 1>
+__global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                                 const bf16* __restrict__ v,
                                                                 const bf16* __restrict__ dout,
                                                                 const float* __restrict__ lse,
@@ -2880,7 +2937,7 @@ __global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __r
                                                                 int d, int causal, float scale, float scale_log2,
                                                                 int n_qtiles, const bf16* __restrict__ o,
                                                                 AttnViews vw) {
-  typedef DqPp<D, W, SLOTS> F;
+  typedef DqPp<D, W, SLOTS, KSPLIT> F;
   typedef typename F::Tile Tile;
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
@@ -2894,7 +2951,10 @@ __global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __r
   const int l32 = lane & 31, g = lane >> 5;
   // 8 waves: SIMD w % 4 holds row blocks 2 (w % 4) and 2 (w % 4) + 1.
   const int q0 = qt * F::BQ;
-  const int q0w = q0 + 32 * (W == 8 ? 2 * (wave & 3) + (wave >> 2) : wave);
+  // With KSPLIT = 2, kh is the wave's half of every key tile.
+  const int kh = KSPLIT == 1 ? 0 : wave / (W / KSPLIT);
+  const int q0w =
+      q0 + 32 * (KSPLIT > 1 ? wave % (W / KSPLIT) : W == 8 ? 2 * (wave & 3) + (wave >> 2) : wave);
   const int qrow = q0w + l32;
 
   // Row pitches (elements; d for dense tensors). K and V share one (the host checks).
@@ -2934,7 +2994,7 @@ __global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __r
 #pragma unroll
       for (int e = 0; e < 8; ++e) part = __builtin_fmaf((float)dof[kk][e], (float)of[kk][e], part);
     dl = lane32_sum(part);
-    if (qok && g == 0) delta[(int64_t)bh * Sq + qrow] = dl;
+    if (qok && g == 0 && kh == 0) delta[(int64_t)bh * Sq + qrow] = dl;
   } else {
     dl = qok ? delta[(int64_t)bh * Sq + qrow] : 0.f;
   }
@@ -3031,32 +3091,77 @@ __global__ __launch_bounds__((64 * W), 2) void attn_dq_pp_kernel(const bf16* __r
   f32x16 s0, dp0, s1, dp1;
   bf16x8 dsf[2];
   auto nop = [] {};
-  for (int t = 0; t < n; ++t) {
-    // Tile t complete for this wave (with three slots tile t + 1 may be in
-    // flight); after the barrier every wave has left tile t - 1's slot, which
-    // tile t + SLOTS - 1 takes.
-    if (SLOTS == 3 && t + 1 < n)
-      wait_vmem<2 * F::kDma>();
-    else
-      wait_vmem<0>();
+  if constexpr (KSPLIT > 1) {
+    static_assert(D == 64, "the split path ends in the direct stores");
+    // This wave's half of every tile: S and dP, dS, then its dQ products.
+    for (int t = 0; t < n; ++t) {
+      if (SLOTS == 3 && t + 1 < n)
+        wait_vmem<2 * F::kDma>();
+      else
+        wait_vmem<0>();
+      lds_barrier();
+      if (t + SLOTS - 1 < n) issue_tile(t + SLOTS - 1);
+      if (t >= n_w) continue;
+      const char* sl = slot(t);
+      const int kv0 = t * F::BK + 32 * kh;
+      sdp(sl, kh, s0, dp0, nop);
+      if (causal && kv0 + 31 > q0w)
+        grad_s(kv0, s0, dp0, dsf, std::true_type{});
+      else
+        grad_s(kv0, s0, dp0, dsf, std::false_type{});
+      grad_q(sl, kh, dsf);
+    }
+    // The upper half adds its dQ partial to the lower half's through the idle
+    // ring (every DMA has landed: the last tile's wait was vmcnt(0)).
+    static_assert(W / KSPLIT * 16 * F::DT * 64 * 4 <= F::kLds, "the partials fit the ring");
+    float* const xs = reinterpret_cast<float*>(smem) + (wave % (W / KSPLIT)) * (16 * F::DT * 64);
     lds_barrier();
-    if (t + SLOTS - 1 < n) issue_tile(t + SLOTS - 1);
-    if (t >= n_w) continue;
-    const char* sl = slot(t);
-    const int kv0 = t * F::BK;
-    const bool mask0 = causal && kv0 + 31 > q0w;
-    const bool mask1 = causal && kv0 + 63 > q0w;
-    sdp(sl, 0, s0, dp0, nop);
-    if (mask0)
-      sdp(sl, 1, s1, dp1, [&] { grad_s(kv0, s0, dp0, dsf, std::true_type{}); });
-    else
-      sdp(sl, 1, s1, dp1, [&] { grad_s(kv0, s0, dp0, dsf, std::false_type{}); });
-    grad_q(sl, 0, dsf);
-    if (mask1)
-      grad_s(kv0 + 32, s1, dp1, dsf, std::true_type{});
-    else
-      grad_s(kv0 + 32, s1, dp1, dsf, std::false_type{});
-    grad_q(sl, 1, dsf);
+    if (kh == 1) {
+#pragma unroll
+      for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          *reinterpret_cast<f32x4*>(xs + ((u * 4 + r4) * 64 + lane) * 4) =
+              f32x4{acc[u][4 * r4], acc[u][4 * r4 + 1], acc[u][4 * r4 + 2], acc[u][4 * r4 + 3]};
+    }
+    lds_barrier();
+    if (kh == 1) return;
+#pragma unroll
+    for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const f32x4 o1 = *reinterpret_cast<const f32x4*>(xs + ((u * 4 + r4) * 64 + lane) * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[u][4 * r4 + e] += o1[e];
+      }
+  } else {
+    for (int t = 0; t < n; ++t) {
+      // Tile t complete for this wave (with three slots tile t + 1 may be in
+      // flight); after the barrier every wave has left tile t - 1's slot, which
+      // tile t + SLOTS - 1 takes.
+      if (SLOTS == 3 && t + 1 < n)
+        wait_vmem<2 * F::kDma>();
+      else
+        wait_vmem<0>();
+      lds_barrier();
+      if (t + SLOTS - 1 < n) issue_tile(t + SLOTS - 1);
+      if (t >= n_w) continue;
+      const char* sl = slot(t);
+      const int kv0 = t * F::BK;
+      const bool mask0 = causal && kv0 + 31 > q0w;
+      const bool mask1 = causal && kv0 + 63 > q0w;
+      sdp(sl, 0, s0, dp0, nop);
+      if (mask0)
+        sdp(sl, 1, s1, dp1, [&] { grad_s(kv0, s0, dp0, dsf, std::true_type{}); });
+      else
+        sdp(sl, 1, s1, dp1, [&] { grad_s(kv0, s0, dp0, dsf, std::false_type{}); });
+      grad_q(sl, 0, dsf);
+      if (mask1)
+        grad_s(kv0 + 32, s1, dp1, dsf, std::true_type{});
+      else
+        grad_s(kv0 + 32, s1, dp1, dsf, std::false_type{});
+      grad_q(sl, 1, dsf);
+    }
   }
 
   if (D == 128 && d == D) {
@@ -3116,14 +3221,14 @@ AttnViews dense_views(const Shape& s) {
   return AttnViews{vq, vk, vk, vq, vq, vq, vk, vk, (int)s.h};
 }
 
-template <int D, int RB = 1, int W = 8, bool ZIG = false>
+template <int D, int RB = 1, int W = 8, bool ZIG = false, int KSPLIT = 1>
 int fwd_sw_launch(const void* q, const void* k, const void* v, void* o, float* lse, const Shape& s, float c, int neg_q,
                   hipStream_t stream, const AttnViews* views = nullptr) {
-  typedef FwdW<D, RB, W> F;
+  typedef FwdW<D, RB, W, KSPLIT> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: grid too large");
-  auto kern = attn_fwd_sw_kernel<D, RB, W, ZIG>;
+  auto kern = attn_fwd_sw_kernel<D, RB, W, ZIG, KSPLIT>;
   set_lds(kern, F::kLds);
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<bf16*>(o), lse, (int)bh,
@@ -3164,15 +3269,19 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
   if constexpr (sizeof(T) == 2 && AL && D <= 128) {
     if (causal && s.sq == s.sk && s.sq % 64 == 0) {
       if constexpr (D == 64) {
-        // 128-row workgroups of 4 waves, two per CU (51 KB of LDS each): the
-        // two workgroups on a CU hide each other's barriers and tails. When
-        // the whole grid is resident at once, the second half of the grid
-        // takes the light tiles in rising order so that each CU pairs a long
-        // and a short tile (1x8x8192x64: 120 -> 91 us on MI355X).
-        typedef FwdW<64, 1, 4> F4;
+        // 128-row workgroups, two per CU (51 KB of LDS each): the two
+        // workgroups on a CU hide each other's barriers and tails. When the
+        // whole grid is resident at once, the second half of the grid takes
+        // the light tiles in rising order so that each CU pairs a long and a
+        // short tile (1x8x8192x64: 120 -> 91 us on MI355X). Each workgroup is
+        // 8 waves that split every key tile between the two waves of a SIMD
+        // (128 VGPRs, four waves per SIMD): the long tile that outlasts its
+        // partner still runs two waves per SIMD (93.7 -> 84.7 us; 8x12x1024x64
+        // 24.4 -> 23.5 us).
+        typedef FwdW<64, 1, 8, 2> F4;
         const bool one_round = cdiv(s.sq, F4::BQ) * s.b * s.h <= 2 * (int64_t)cu_count();
-        return one_round ? fwd_sw_launch<D, 1, 4, true>(q, k, v, o, lse, s, c, neg_q, stream)
-                         : fwd_sw_launch<D, 1, 4, false>(q, k, v, o, lse, s, c, neg_q, stream);
+        return one_round ? fwd_sw_launch<D, 1, 8, true, 2>(q, k, v, o, lse, s, c, neg_q, stream)
+                         : fwd_sw_launch<D, 1, 8, false, 2>(q, k, v, o, lse, s, c, neg_q, stream);
       } else {
         return fwd_sw_launch<D>(q, k, v, o, lse, s, c, neg_q, stream);
       }
@@ -3186,15 +3295,15 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
 }
 
 // o == nullptr: read delta; otherwise compute it from o and dout and write it.
-template <int D, int W, int SLOTS, bool ZIG>
+template <int D, int W, int SLOTS, bool ZIG, int KSPLIT = 1>
 int dq_pp_launch_t(const void* q, const void* k, const void* v, const void* dout, const float* lse, float* delta,
                    void* dq, const Shape& s, int causal, float scale, hipStream_t stream, const void* o,
                    const AttnViews& vw) {
-  typedef DqPp<D, W, SLOTS> F;
+  typedef DqPp<D, W, SLOTS, KSPLIT> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq: grid too large");
-  auto kern = o ? attn_dq_pp_kernel<D, W, SLOTS, ZIG, true> : attn_dq_pp_kernel<D, W, SLOTS, ZIG, false>;
+  auto kern = o ? attn_dq_pp_kernel<D, W, SLOTS, ZIG, true, KSPLIT> : attn_dq_pp_kernel<D, W, SLOTS, ZIG, false, KSPLIT>;
   set_lds(kern, F::kLds);
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
@@ -3209,12 +3318,16 @@ int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, 
                  const AttnViews* views = nullptr) {
   const AttnViews vw = views ? *views : dense_views(s);
   if constexpr (D == 64) {
-    // 128-query workgroups of 4 waves with two LDS slots (67 KB): two share a
-    // CU. A grid resident all at once (the long-context case) pairs long and
-    // short causal sweeps on each CU.
-    typedef DqPp<64, 4, 2> F4;
+    // 128-query workgroups with two LDS slots (67 KB): two share a CU. A grid
+    // resident all at once (the long-context case) pairs long and short causal
+    // sweeps on each CU, and its workgroups are 8 waves that split every key
+    // tile between the two waves of a SIMD, so that the long sweep that
+    // outlasts its partner still runs two waves per SIMD (1x8x8192x64:
+    // 136 -> 122 us). Otherwise 4 waves each take whole tiles (the split
+    // measured 10% slower at 8x12x1024x64).
+    typedef DqPp<64, 8, 2, 2> F4;
     const bool one_round = causal && cdiv(s.sq, F4::BQ) * s.b * s.h <= 2 * (int64_t)cu_count();
-    return one_round ? dq_pp_launch_t<D, 4, 2, true>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw)
+    return one_round ? dq_pp_launch_t<D, 8, 2, true, 2>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw)
                      : dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
   } else {
     return dq_pp_launch_t<D, 8, 3, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
@@ -3461,10 +3574,10 @@ extern "C" int ferrite_hip_attn_fwd_qkv(const void* qkv, void* o, float* lse, in
   c = fmaxf(fabsf(c), 1e-30f);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (d == 64) {
-    typedef FwdW<64, 1, 4> F4;
+    typedef FwdW<64, 1, 8, 2> F4;
     const bool one_round = cdiv(s, F4::BQ) * b * h <= 2 * (int64_t)cu_count();
-    return one_round ? fwd_sw_launch<64, 1, 4, true>(q, k, v, o, lse, sh, c, neg_q, st, &vw)
-                     : fwd_sw_launch<64, 1, 4, false>(q, k, v, o, lse, sh, c, neg_q, st, &vw);
+    return one_round ? fwd_sw_launch<64, 1, 8, true, 2>(q, k, v, o, lse, sh, c, neg_q, st, &vw)
+                     : fwd_sw_launch<64, 1, 8, false, 2>(q, k, v, o, lse, sh, c, neg_q, st, &vw);
   }
   return fwd_sw_launch<128>(q, k, v, o, lse, sh, c, neg_q, st, &vw);
 }
