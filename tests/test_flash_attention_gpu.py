@@ -245,6 +245,8 @@ def test_ragged_and_unaligned_via_abi(dev, b, h, sq, sk, d, dtype, causal, scale
     (1, 2, 320, 128),   # 256 + 64 rows
     (1, 1, 128, 64),
     (1, 2, 128, 80),    # d padded 80 -> 128 on the 64-row-tile path
+    (2, 1, 192, 48),    # d padded 48 -> 64: the key-split forward and dQ with d < D
+    (1, 2, 256, 32),
 ])
 @pytest.mark.parametrize("fused", [False, True], ids=["delta_pass", "delta_in_dq"])
 def test_causal_tile_edges_via_abi(dev, b, h, s, d, fused):
