@@ -76,6 +76,14 @@ def _settle(fn, seconds: float = 0.2) -> None:
         torch.cuda.synchronize()
 
 
+# Where `roofline.traffic` comes from: the counters cannot run inside the timed bench (rocprofv3
+# --pmc is a run of its own), so the line carries the calibrated figure of the committed summary
+# and says so in `traffic_source`.
+TRAFFIC_SOURCE = ("profiles/hbm_traffic.md: rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE runs of "
+                  "bench.py (one counter per run, calibrated against a 256 MiB copy); read from that "
+                  "file, not measured in this run")
+
+
 def _traffic(kernel: str):
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), read from the committed summary."""
     if not os.path.exists(TRAFFIC_FILE):
@@ -95,8 +103,13 @@ def _roofline(name: str, flops: float, nbytes: float, seconds: float, precision:
     from ferrite import platform
     from ferrite.profiling.roofline import analyze
 
-    return analyze(name, flops, nbytes, seconds, peaks=platform.MI355X, precision=precision,
-                   traffic=traffic).bench_fields()
+    fields = analyze(name, flops, nbytes, seconds, peaks=platform.MI355X, precision=precision,
+                     traffic=traffic).bench_fields()
+    if traffic is None:
+        del fields["traffic"]
+    else:
+        fields["traffic_source"] = TRAFFIC_SOURCE
+    return fields
 
 
 def bench_attention(b, h, t, d, steps, warmup, seed=7):
@@ -193,16 +206,52 @@ def _graph_time(launch_all, iters, warmup, per):
     return t
 
 
+def bench_stream_ceilings(nbytes: int = 1 << 30, iters: int = 10):
+    """What this part's HBM streams reach at `nbytes` (1 GiB, far past the 256 MB Infinity Cache):
+    read-only (ferrite_hip_stream_read), write-only (ferrite_hip_stream_fill) and the two-buffer
+    copy of add+RMSNorm's access pattern (ferrite_hip_stream_copy2, half reads and half writes),
+    each the best over a few persistent-grid sizes. The copy's rate is the ceiling of a kernel that
+    reads and writes equal byte counts, as add+RMSNorm does."""
+    import torch
+
+    from ferrite import _hip
+
+    lib, st = _hip.lib(), torch.cuda.current_stream().cuda_stream
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0").random_(0, 255)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
+    sink = torch.empty(4096, dtype=torch.int32, device="cuda:0")
+    half = nbytes // 2
+    read, fill = {}, {}
+    for blocks in (256, 512, 1024, 2048):
+        t = _events_time(lambda: _hip.check(lib.ferrite_hip_stream_read(src.data_ptr(), nbytes, sink.data_ptr(),
+                                                                        blocks, st), "stream_read"), iters, 2)
+        read[blocks] = nbytes / t / 1e9
+        t = _events_time(lambda: _hip.check(lib.ferrite_hip_stream_fill(dst.data_ptr(), nbytes, 0x3F803F80, blocks,
+                                                                        st), "stream_fill"), iters, 2)
+        fill[blocks] = nbytes / t / 1e9
+    # copy2 moves `nbytes` in all: two buffers of nbytes / 4 read, two written
+    t = _events_time(lambda: _hip.check(lib.ferrite_hip_stream_copy2(src.data_ptr(), src.data_ptr() + half // 2,
+                                                                     dst.data_ptr(), dst.data_ptr() + half // 2,
+                                                                     half // 2, st), "stream_copy2"), iters, 2)
+    copy = nbytes / t / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"bytes": nbytes, "read_gbs": max(read.values()), "write_gbs": max(fill.values()),
+            "copy_read_plus_write_gbs": copy, "read_gbs_by_blocks": read, "write_gbs_by_blocks": fill,
+            "copy_frac_of_peak": copy / PEAK_HBM_GBS}
+
+
 def bench_rmsnorm(rows, dim, steps, warmup, sets=24):
     """add+RMSNorm over `sets` rotating buffer sets (24 x 33.5 MB = 805 MB > the 256 MB MALL),
     launched through a captured HIP graph so host launch cost does not pace the ~7 us kernels.
 
-    Beside it, the streaming ceiling of this part for the same access pattern: the library's
-    non-temporal two-buffer copy (ferrite_hip_stream_copy2: x -> h and r -> y, same bytes, same
-    rotation and replay) is the ceiling for these bytes; `frac_of_ceiling_same_bytes` is the
-    kernel's rate over it. Both kernels run again at 16x the size (537 MB per launch, 3 sets),
-    where the per-launch ramp no longer counts and the rate is the HBM read+write stream's;
-    `frac_of_best_stream` is the kernel's rate over the best rate seen at either size."""
+    Beside it, copies of the same access pattern as references: the library's non-temporal
+    two-buffer copy (ferrite_hip_stream_copy2: x -> h and r -> y, same bytes, same rotation and
+    replay) and torch's copy, both at the bench size, and both kernels again at 16x the size (537 MB
+    per launch, 3 sets), where the per-launch ramp no longer counts. `ratio_to_best_copy` is the
+    kernel's rate over the fastest of those copies (a reference-copy ratio, not a ceiling: the
+    kernel can beat a copy of its own bytes). The ceilings of this part's streams are measured by
+    bench_stream_ceilings."""
     import torch
 
     from ferrite import _hip
@@ -243,17 +292,18 @@ def bench_rmsnorm(rows, dim, steps, warmup, sets=24):
     torch.cuda.empty_cache()
     big_bytes, big_copy_bytes = 4 * big_rows * dim * 2 + dim * 2, 4 * big_rows * dim * 2
     same = copy_bytes / t_copy / 1e9
-    best = max(same * 1e9, big_copy_bytes / t_big_copy, big_bytes / t_big) / 1e9
+    torch_same = copy_bytes / t_tcopy / 1e9
+    best_copy = max(same, torch_same, big_copy_bytes / t_big_copy / 1e9)
     gbs = nbytes / t / 1e9
     return {"shape": [rows, dim], "us": t * 1e6, "gbs": gbs, "bytes": nbytes,
             "frac_hbm": gbs / PEAK_HBM_GBS, "buffer_sets": sets, "eager_us": t_eager * 1e6,
             "stream_copy_same_bytes_us": t_copy * 1e6, "stream_copy_same_bytes_gbs": same,
-            "frac_of_ceiling_same_bytes": gbs / same,
-            "torch_copy_same_bytes_us": t_tcopy * 1e6, "torch_copy_same_bytes_gbs": copy_bytes / t_tcopy / 1e9,
+            "torch_copy_same_bytes_us": t_tcopy * 1e6, "torch_copy_same_bytes_gbs": torch_same,
+            "ratio_to_copy_same_bytes": gbs / same,
             "x16_size": {"shape": [big_rows, dim], "add_rmsnorm_us": t_big * 1e6,
                          "add_rmsnorm_gbs": big_bytes / t_big / 1e9, "stream_copy_us": t_big_copy * 1e6,
                          "stream_copy_gbs": big_copy_bytes / t_big_copy / 1e9},
-            "best_stream_gbs": best, "frac_of_best_stream": gbs / best}
+            "best_copy_gbs": best_copy, "ratio_to_best_copy": gbs / best_copy}
 
 
 def bench_matmul(steps, warmup):
@@ -508,6 +558,12 @@ def main(argv=None):
         kernels["attention_long_context"] = bench_attention(1, 8, 8192, 64, max(a.steps // 2, 3), 2, seed=27)
     if a.only in ("rmsnorm", "all"):
         kernels["add_rmsnorm"] = bench_rmsnorm(4096, 1024, a.steps, a.warmup)
+        ceil = bench_stream_ceilings()
+        kernels["hbm_stream_ceilings"] = ceil
+        r = kernels["add_rmsnorm"]
+        # equal reads and writes: the copy's rate is this kernel's ceiling on this part
+        r["frac_of_measured_ceiling"] = r["gbs"] / ceil["copy_read_plus_write_gbs"]
+        r["x16_size"]["frac_of_measured_ceiling"] = r["x16_size"]["add_rmsnorm_gbs"] / ceil["copy_read_plus_write_gbs"]
     if a.only in ("matmul", "all"):
         kernels["matmul"] = bench_matmul(max(a.steps // 2, 3), 2)
     if a.only in ("gpt", "all"):

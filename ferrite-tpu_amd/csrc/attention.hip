@@ -1063,12 +1063,11 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   }
 
   // Stage j loads K_{j+3} and V_{j+1} into the slots that K_j and V_{j-2}
-  // left at its barrier.
-  // Stage j loads K_{j+3} and V_{j+1} into the slots that K_j and V_{j-2}
-  // left at its barrier; this wave's instruction qd is block qd of its K
-  // share, then block qd - kDma of its V share. Issued unconditionally: a
-  // tile past the end has an empty buffer range, so its instructions read
-  // nothing and write zeros into a slot nobody reads again.
+  // left at its barrier (both were last read in stage j - 1); this wave's
+  // instruction qd is block qd of its K share, then block qd - kDma of its V
+  // share. Issued unconditionally: a tile past the end has an empty buffer
+  // range, so its instructions read nothing and write zeros into a slot nobody
+  // reads again.
   auto dma_part = [&](int j, int qd) {
     if (qd < F::kDma)
       kdma.issue_one(kb, (j + 3) * F::BK, S, ldk, kring + ((j + 3) % F::kSlots) * KT::kBytes, qd);
@@ -1089,8 +1088,17 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
     f32x16(&sc)[NKT][RB] = s[P];
     bf16x8(&pc)[RB][2 * NKT] = pf[P];
     bf16x8(&pp)[RB][2 * NKT] = pf[1 - P];
-    const char* kp = kring + ((j + 1) % F::kSlots) * KT::kBytes + kbase;
-    const char* vp = vring + ((j - 1 + F::kSlots) % F::kSlots) * VT::kBytes + vbase;
+    // Stage j reads K_{j+1} and V_{j-1}. The slot offsets pass through an
+    // empty asm: where the compiler can fold them to constants (the unrolled
+    // stage pairs), it hoists a separate lane address for every fragment read
+    // out of the stage loop (the reads' 16-bit offsets cannot reach past 64 KB
+    // of ring), and those addresses spill: the D = 64 key-split kernel wrote
+    // 12 bytes of scratch per lane without this.
+    int koff = ((j + 1) % F::kSlots) * KT::kBytes;
+    int voff = ((j - 1 + F::kSlots) % F::kSlots) * VT::kBytes;
+    asm volatile("" : "+s"(koff), "+s"(voff));
+    const char* kp = kring + koff + kbase;
+    const char* vp = vring + voff + vbase;
     // K fragments: key subtile f % NKT (with KSPLIT = 2 the wave's own, whose
     // rows kbase already points at), k-chunk f / NKT.
     constexpr int NFQ = QK ? NKT * KS : 0;
@@ -3182,10 +3190,10 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
 // ===========================================================================
 // Host side
 // ===========================================================================
+// The kernel's dynamic-LDS limit on the stream's device, raised once per device.
 template <typename K>
-void set_lds(K kernel, int bytes) {
-  // Idempotent; called on every launch because the attribute is per device.
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+int set_lds(K kernel, int bytes, hipStream_t stream) {
+  return allow_lds(reinterpret_cast<const void*>(kernel), bytes, stream, "ferrite_hip_attn");
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -3229,7 +3237,7 @@ int fwd_sw_launch(const void* q, const void* k, const void* v, void* o, float* l
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: grid too large");
   auto kern = attn_fwd_sw_kernel<D, RB, W, ZIG, KSPLIT>;
-  set_lds(kern, F::kLds);
+  if (int rc = set_lds(kern, F::kLds, stream)) return rc;
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<bf16*>(o), lse, (int)bh,
                      (int)s.sq, (int)s.d, c, neg_q, (int)nq, views ? *views : dense_views(s));
@@ -3244,7 +3252,7 @@ int fwd_pp_launch(const void* q, const void* k, const void* v, void* o, float* l
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: grid too large");
   auto kern = attn_fwd_pp_kernel<D>;
-  set_lds(kern, F::kLds);
+  if (int rc = set_lds(kern, F::kLds, stream)) return rc;
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<bf16*>(o), lse, (int)bh,
                      (int)s.sq, (int)s.sk, (int)s.d, causal, c, neg_q, (int)nq);
@@ -3259,7 +3267,7 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: grid too large");
   auto kern = attn_fwd_kernel<T, D, AL>;
-  set_lds(kern, F::kLds);
+  if (int rc = set_lds(kern, F::kLds, stream)) return rc;
   // The kernel takes the row max on raw scores, which needs a positive
   // multiplier: a negative scale negates q instead, and a zero scale becomes a
   // tiny positive one (uniform weights either way).
@@ -3279,7 +3287,7 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
         // partner still runs two waves per SIMD (93.7 -> 84.7 us; 8x12x1024x64
         // 24.4 -> 23.5 us).
         typedef FwdW<64, 1, 8, 2> F4;
-        const bool one_round = cdiv(s.sq, F4::BQ) * s.b * s.h <= 2 * (int64_t)cu_count();
+        const bool one_round = cdiv(s.sq, F4::BQ) * s.b * s.h <= 2 * (int64_t)cu_count(stream);
         return one_round ? fwd_sw_launch<D, 1, 8, true, 2>(q, k, v, o, lse, s, c, neg_q, stream)
                          : fwd_sw_launch<D, 1, 8, false, 2>(q, k, v, o, lse, s, c, neg_q, stream);
       } else {
@@ -3304,7 +3312,7 @@ int dq_pp_launch_t(const void* q, const void* k, const void* v, const void* dout
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq: grid too large");
   auto kern = o ? attn_dq_pp_kernel<D, W, SLOTS, ZIG, true, KSPLIT> : attn_dq_pp_kernel<D, W, SLOTS, ZIG, false, KSPLIT>;
-  set_lds(kern, F::kLds);
+  if (int rc = set_lds(kern, F::kLds, stream)) return rc;
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
                      delta, static_cast<bf16*>(dq), (int)bh, (int)s.sq, (int)s.sk, (int)s.d, causal, scale,
@@ -3326,7 +3334,7 @@ int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, 
     // 136 -> 122 us). Otherwise 4 waves each take whole tiles (the split
     // measured 10% slower at 8x12x1024x64).
     typedef DqPp<64, 8, 2, 2> F4;
-    const bool one_round = causal && cdiv(s.sq, F4::BQ) * s.b * s.h <= 2 * (int64_t)cu_count();
+    const bool one_round = causal && cdiv(s.sq, F4::BQ) * s.b * s.h <= 2 * (int64_t)cu_count(stream);
     return one_round ? dq_pp_launch_t<D, 8, 2, true, 2>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw)
                      : dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
   } else {
@@ -3344,7 +3352,7 @@ int dq_launch(const void* q, const void* k, const void* v, const void* dout, con
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq: grid too large");
   auto kern = attn_dq_kernel<T, D, AL>;
-  set_lds(kern, F::kLds);
+  if (int rc = set_lds(kern, F::kLds, stream)) return rc;
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(kThreads), F::kLds, stream, static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v), static_cast<const T*>(dout), lse, delta,
                      static_cast<T*>(dq), (int)bh, s.sq, s.sk, (int)s.d, causal, scale, scale * kLog2e, (int)nq);
@@ -3364,7 +3372,7 @@ int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout,
     // Two waves per SIMD with the work of a key block split between them.
     typedef DkvRs R;
     auto kern = vw.q.r == vw.dout.r ? attn_dkv_rs_kernel<true> : attn_dkv_rs_kernel<false>;
-    set_lds(kern, R::kLds);
+    if (int rc = set_lds(kern, R::kLds, stream)) return rc;
     hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(R::kThreads), R::kLds, stream, static_cast<const bf16*>(q),
                        static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
                        delta, static_cast<bf16*>(dk), static_cast<bf16*>(dv), (int)bh, (int)s.sq, (int)s.sk, (int)s.d,
@@ -3372,8 +3380,8 @@ int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout,
     return check_launch("ferrite_flash_attention_bwd_dkv");
   } else {
     auto kern = vw.q.r == vw.dout.r ? attn_dkv_sw_kernel<D, true> : attn_dkv_sw_kernel<D, false>;
-    set_lds(kern, F::kLds);
-    const int zig = causal && F::kMinBlocks == 2 && nk * bh <= 2 * (int64_t)cu_count();
+    if (int rc = set_lds(kern, F::kLds, stream)) return rc;
+    const int zig = causal && F::kMinBlocks == 2 && nk * bh <= 2 * (int64_t)cu_count(stream);
     hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                        static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
                        delta, static_cast<bf16*>(dk), static_cast<bf16*>(dv), (int)bh, (int)s.sq, (int)s.sk, (int)s.d,
@@ -3392,7 +3400,7 @@ int dkv_launch(const void* q, const void* k, const void* v, const void* dout, co
   const int64_t bh = s.b * s.h;
   if (nk * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dkv: grid too large");
   auto kern = attn_dkv_kernel<T, D, AL>;
-  set_lds(kern, F::kLds);
+  if (int rc = set_lds(kern, F::kLds, stream)) return rc;
   hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(kThreads), F::kLds, stream, static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v), static_cast<const T*>(dout), lse, delta,
                      static_cast<T*>(dk), static_cast<T*>(dv), (int)bh, s.sq, s.sk, (int)s.d, causal, scale,
@@ -3411,7 +3419,7 @@ int fwd_wide_launch(const void* q, const void* k, const void* v, void* o, float*
   const int neg_q = c < 0.f;
   c = fmaxf(fabsf(c), 1e-30f);
   auto kern = attn_fwd_wide_kernel<T, AL>;
-  set_lds(kern, F::kFwdLds);
+  if (int rc = set_lds(kern, F::kFwdLds, stream)) return rc;
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh * nc)), dim3(kThreads), F::kFwdLds, stream,
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), static_cast<T*>(o),
                      lse, (int)bh, (int)s.sq, (int)s.sk, (int)s.d, causal, c, neg_q, (int)nq);
@@ -3425,7 +3433,7 @@ int dq_wide_launch(const void* q, const void* k, const void* v, const void* dout
   const int64_t nq = cdiv(s.sq, F::BQ), bh = s.b * s.h, nc = s.d / kSlab;
   if (nq * bh * nc > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq: grid too large");
   auto kern = attn_dq_wide_kernel<T, AL>;
-  set_lds(kern, F::kDqLds);
+  if (int rc = set_lds(kern, F::kDqLds, stream)) return rc;
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh * nc)), dim3(kThreads), F::kDqLds, stream,
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<const T*>(dout), lse, delta, static_cast<T*>(dq), (int)bh, (int)s.sq, (int)s.sk,
@@ -3441,7 +3449,7 @@ int dkv_wide_launch(const void* q, const void* k, const void* v, const void* dou
   const int64_t nk = cdiv(s.sk, F::BKV), bh = s.b * s.h, nc = s.d / kSlab;
   if (nk * bh * nc > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dkv: grid too large");
   auto kern = attn_dkv_wide_kernel<T, AL>;
-  set_lds(kern, F::kDkvLds);
+  if (int rc = set_lds(kern, F::kDkvLds, stream)) return rc;
   hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh * nc)), dim3(kThreads), F::kDkvLds, stream,
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<const T*>(dout), lse, delta, static_cast<T*>(dk), static_cast<T*>(dv), (int)bh,
@@ -3575,7 +3583,7 @@ extern "C" int ferrite_hip_attn_fwd_qkv(const void* qkv, void* o, float* lse, in
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (d == 64) {
     typedef FwdW<64, 1, 8, 2> F4;
-    const bool one_round = cdiv(s, F4::BQ) * b * h <= 2 * (int64_t)cu_count();
+    const bool one_round = cdiv(s, F4::BQ) * b * h <= 2 * (int64_t)cu_count(st);
     return one_round ? fwd_sw_launch<64, 1, 8, true, 2>(q, k, v, o, lse, sh, c, neg_q, st, &vw)
                      : fwd_sw_launch<64, 1, 8, false, 2>(q, k, v, o, lse, sh, c, neg_q, st, &vw);
   }

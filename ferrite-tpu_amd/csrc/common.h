@@ -160,8 +160,29 @@ __device__ __forceinline__ float wave_sum(float x) {
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
-// Compute units of the current device (256 on an MI355X).
-int cu_count();
+// The device a stream's launches run on (the current device for the null and
+// per-thread streams), or -1. Every per-device lookup of an entry point goes
+// through the stream it was given, not through the thread's current device.
+int stream_device(hipStream_t s);
+// Compute units of device `dev` (the current device when dev < 0; 256 on an MI355X).
+int cu_count_of(int dev);
+// Compute units of the stream's device.
+int cu_count(hipStream_t s);
+// Makes `dev` current for its lifetime (no-op when it already is or dev < 0).
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(int dev);
+  ~DeviceGuard();
+  DeviceGuard(const DeviceGuard&) = delete;
+  DeviceGuard& operator=(const DeviceGuard&) = delete;
+
+ private:
+  int prev_;
+};
+// Raises `kernel`'s dynamic-LDS limit to `bytes` on the stream's device, once per
+// (kernel, device); FERRITE_OK, or an error code with the message set (`what`
+// names the entry point).
+int allow_lds(const void* kernel, int bytes, hipStream_t s, const char* what);
 
 inline bool valid_dtype(int dt) { return dt == FERRITE_F32 || dt == FERRITE_BF16; }
 inline const char* dtype_name(int dt) { return dt == FERRITE_F32 ? "f32" : dt == FERRITE_BF16 ? "bf16" : "?"; }

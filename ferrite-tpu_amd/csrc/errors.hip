@@ -3,6 +3,7 @@
 #include <string>
 
 #include "common.h"
+#include "device_select.h"
 
 namespace ferrite {
 
@@ -22,18 +23,48 @@ int check_launch(const char* what) {
   return FERRITE_OK;
 }
 
-// Compute units of the current device, looked up once per device. Racing
-// first calls store the same value.
-int cu_count() {
+int stream_device(hipStream_t s) {
+  return device_of_stream(
+      s, [](const void* st, int* d) { return (int)hipStreamGetDevice(static_cast<hipStream_t>(const_cast<void*>(st)), d); },
+      [](int* d) { return (int)hipGetDevice(d); });
+}
+
+// Compute units of device `dev` (the current device when dev < 0), looked up
+// once per device. Racing first calls store the same value.
+int cu_count_of(int dev) {
   static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (dev < 0 && hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev < 0 || dev >= 64) return 256;
   int n = cache[dev].load(std::memory_order_relaxed);
   if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
     cache[dev].store(n, std::memory_order_relaxed);
   }
   return n;
+}
+
+int cu_count(hipStream_t s) { return cu_count_of(stream_device(s)); }
+
+DeviceGuard::DeviceGuard(int dev) : prev_(-1) {
+  if (dev >= 0 && hipGetDevice(&prev_) == hipSuccess && prev_ != dev && hipSetDevice(dev) == hipSuccess) return;
+  prev_ = -1;
+}
+DeviceGuard::~DeviceGuard() {
+  if (prev_ >= 0) (void)hipSetDevice(prev_);
+}
+
+int allow_lds(const void* kernel, int bytes, hipStream_t s, const char* what) {
+  static OncePerDevice once;
+  const int dev = stream_device(s);
+  if (dev < 0) return fail(FERRITE_ERR_LAUNCH, std::string(what) + ": cannot tell the stream's device");
+  const int rc = once.run(kernel, dev, [&] {
+    DeviceGuard on(dev);
+    return (int)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  });
+  if (rc != (int)hipSuccess)
+    return fail(FERRITE_ERR_LAUNCH, std::string(what) + ": raising the LDS limit to " + std::to_string(bytes) +
+                                        " bytes failed: " + hipGetErrorString(static_cast<hipError_t>(rc)));
+  return FERRITE_OK;
 }
 
 }  // namespace ferrite

@@ -707,7 +707,7 @@ template <typename T, typename TO, int BM, int BN, int BK, int WM, int WN, bool 
 void launch_gemm_kernel(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, int64_t tiles,
                         int64_t tiles_n, size_t lds, hipStream_t stream) {
   auto k = gemm_kernel<T, TO, BM, BN, BK, WM, WN, AL>;
-  (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  (void)allow_lds((const void*)k, (int)lds, stream, "ferrite_matmul");  // a failure resurfaces as the launch's error
   hipLaunchKernelGGL(k, dim3((unsigned)tiles), dim3(WM * WN * 64), lds, stream, static_cast<const T*>(x),
                      static_cast<const T*>(y), static_cast<TO*>(out), M, N, K, (int)tiles_n);
 }
@@ -737,9 +737,9 @@ int launch_gemm(const void* x, const void* y, void* out, int64_t M, int64_t N, i
 struct F32Split {
   int s, g;
 };
-F32Split f32_split(int64_t M, int64_t N, int64_t K) {
+F32Split f32_split(int64_t M, int64_t N, int64_t K, int64_t cus) {
   const int64_t tiles = cdiv(M, (int64_t)64) * cdiv(N, (int64_t)64);
-  const int64_t waves = 8 * (int64_t)cu_count();  // two per SIMD
+  const int64_t waves = 8 * cus;  // two per SIMD
   int s = K >= 512 ? 4 : K >= 256 ? 2 : 1;
   while (s > 1 && tiles * 2 * s > waves) s /= 2;
   int64_t g = 1;
@@ -747,8 +747,8 @@ F32Split f32_split(int64_t M, int64_t N, int64_t K) {
     g = std::min<int64_t>({cdiv(waves, tiles * 2 * s), K / (128 * s), (int64_t)8});
   return {s, (int)std::max<int64_t>(g, 1)};
 }
-int64_t f32_workspace(int64_t M, int64_t N, int64_t K) {
-  const F32Split sp = f32_split(M, N, K);
+int64_t f32_workspace(int64_t M, int64_t N, int64_t K, int64_t cus) {
+  const F32Split sp = f32_split(M, N, K, cus);
   return sp.g > 1 ? (int64_t)sp.g * M * N * (int64_t)sizeof(float) : 0;
 }
 
@@ -763,7 +763,7 @@ void launch_gemm_f32_slices(const float* x, const float* y, TO* out, int64_t M, 
   auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   const bool aligned = K % 4 == 0 && N % 4 == 0 && a16(x) && a16(y) && a16(out);
   auto go = [&](auto kern) {
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    (void)allow_lds((const void*)kern, (int)lds, stream, "ferrite_matmul");  // a failure resurfaces as the launch's error
     hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)groups), dim3(128 * S), lds, stream, x, y, out, M, N, K,
                        (int)tiles_n, kslice);
   };
@@ -792,8 +792,9 @@ int launch_gemm_f32_split(const void* x, const void* y, void* out, int64_t M, in
 template <typename TO>
 int launch_gemm_f32_small(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, void* ws,
                           int64_t ws_bytes, hipStream_t stream) {
-  F32Split sp = f32_split(M, N, K);
-  if (sp.g > 1 && (ws == nullptr || ws_bytes < f32_workspace(M, N, K) || (reinterpret_cast<uintptr_t>(ws) & 15)))
+  const int64_t cus = cu_count(stream);
+  F32Split sp = f32_split(M, N, K, cus);
+  if (sp.g > 1 && (ws == nullptr || ws_bytes < f32_workspace(M, N, K, cus) || (reinterpret_cast<uintptr_t>(ws) & 15)))
     sp.g = 1;
   if (sp.s == 4) return launch_gemm_f32_split<TO, 4>(x, y, out, M, N, K, sp.g, ws, stream);
   if (sp.s == 2) return launch_gemm_f32_split<TO, 2>(x, y, out, M, N, K, sp.g, ws, stream);
@@ -805,9 +806,8 @@ int launch_gemm_f32_small(const void* x, const void* y, void* out, int64_t M, in
 // already fill most CUs or the f32 partials would outweigh the work. A round
 // that spills over by a few workgroups costs a whole second round: 36 tiles in
 // 8 slices (288 workgroups on 256 CUs) take longer than in 7.
-int splitk_slices(int64_t M, int64_t N, int64_t K) {
+int splitk_slices(int64_t M, int64_t N, int64_t K, int64_t cus) {
   const int64_t tiles = cdiv(M, (int64_t)Gemm2::BM) * cdiv(N, (int64_t)Gemm2::BN);
-  const int64_t cus = cu_count();
   // Up to half the CUs busy and a long K (the 8192 x 768 outputs of a 768-wide model): two
   // slices fill 3/4 of the CUs, and the two f32 partial slabs stay in the Infinity Cache.
   if (tiles >= cus / 4) return (2 * tiles <= cus && K >= 2048) ? 2 : 1;
@@ -817,14 +817,14 @@ int splitk_slices(int64_t M, int64_t N, int64_t K) {
   return (int)cdiv(K, kslice);
 }
 
-int64_t splitk_workspace(int64_t M, int64_t N, int64_t K) {
-  const int s = splitk_slices(M, N, K);
+int64_t splitk_workspace(int64_t M, int64_t N, int64_t K, int64_t cus) {
+  const int s = splitk_slices(M, N, K, cus);
   return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
 }
 
 // f32 products too small for 128 x 128 tiles on every CU run 64 x 64 tiles
 // (launch_gemm_f32_small).
-bool f32_small(int64_t M, int64_t N) { return cdiv(M, (int64_t)128) * cdiv(N, (int64_t)128) < cu_count(); }
+bool f32_small(int64_t M, int64_t N, int64_t cus) { return cdiv(M, (int64_t)128) * cdiv(N, (int64_t)128) < cus; }
 
 // Output rows per workgroup. 128-row tiles (k-contiguous x only) halve the work of a
 // tile, so a problem whose 256-row tiles spill into a mostly empty round, or fill
@@ -833,9 +833,8 @@ bool f32_small(int64_t M, int64_t N) { return cdiv(M, (int64_t)128) * cdiv(N, (i
 // the work), and 8192 x 768 one round of 192 tiles instead of 96 tiles or a K split.
 // A 128-row tile moves more bytes per product, costed at 0.55 of a 256-row one.
 // With fewer than a quarter of the CUs' worth of 256-row tiles the K split is used.
-int pick_bm(int64_t M, int64_t N, bool xt) {
+int pick_bm(int64_t M, int64_t N, bool xt, int64_t cus) {
   if (xt) return 256;
-  const int64_t cus = cu_count();
   const int64_t t256 = cdiv(M, (int64_t)256) * cdiv(N, (int64_t)Gemm2::BN);
   const int64_t t128 = cdiv(M, (int64_t)128) * cdiv(N, (int64_t)Gemm2::BN);
   if (t256 < cus / 4) return 256;
@@ -847,9 +846,8 @@ int pick_bm(int64_t M, int64_t N, bool xt) {
 // have no second wave to cover a workgroup's start and end. They pay from four
 // rounds of workgroups on: 8192^3 1244 -> 1372 TFLOP/s, 8192 x 4096 x 4096 level,
 // 4096^3 (one round) 2-5% slower. Both give bitwise the same output.
-bool use_four_waves(int64_t M, int64_t N, int64_t K) {
-  (void)K;
-  return cdiv(M, (int64_t)256) * cdiv(N, (int64_t)256) >= 4 * (int64_t)cu_count();
+bool use_four_waves(int64_t M, int64_t N, int64_t cus) {
+  return cdiv(M, (int64_t)256) * cdiv(N, (int64_t)256) >= 4 * cus;
 }
 
 template <typename TO, bool XT, bool YT, int EPI = kEpiNone>
@@ -857,13 +855,14 @@ int launch_gemm_dma_t(const void* x, const void* y, void* out, int64_t M, int64_
                       int64_t ws_bytes, hipStream_t stream, void* aux = nullptr) {
   typedef Gemm2 G;
   bf16* const ax = static_cast<bf16*>(aux);
+  const int64_t cus = cu_count(stream);
   if constexpr (!XT) {
-    if (pick_bm(M, N, XT) == 128) {
+    if (pick_bm(M, N, XT, cus) == 128) {
       constexpr int kLds128 = 3 * (2 * GemmXTile::kSubBytes + OperandTile<YT>::kBytes);
       static_assert(kLds128 <= 160 * 1024, "three stages of a 128-row tile fit the LDS");
       const int64_t tiles_m = cdiv(M, (int64_t)128), tiles_n = cdiv(N, G::BN);
       auto kern = gemm_dma_kernel<TO, false, YT, 128, 3, EPI>;
-      (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds128);
+      if (int rc = allow_lds((const void*)kern, kLds128, stream, "ferrite_matmul")) return rc;
       hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n)), dim3(G::kThreads), kLds128, stream,
                          static_cast<const bf16*>(x), static_cast<const bf16*>(y), static_cast<TO*>(out), (int)M,
                          (int)N, (int)K, (int)tiles_m, (int)tiles_n, (int)K, ax);
@@ -871,8 +870,8 @@ int launch_gemm_dma_t(const void* x, const void* y, void* out, int64_t M, int64_
     }
   }
   const int64_t tiles_m = cdiv(M, G::BM), tiles_n = cdiv(N, G::BN);
-  int slices = splitk_slices(M, N, K);
-  if (slices > 1 && (ws == nullptr || ws_bytes < splitk_workspace(M, N, K) || (M * N) % 4 != 0 ||
+  int slices = splitk_slices(M, N, K, cus);
+  if (slices > 1 && (ws == nullptr || ws_bytes < splitk_workspace(M, N, K, cus) || (M * N) % 4 != 0 ||
                      (reinterpret_cast<uintptr_t>(ws) & 15) != 0))
     slices = 1;
   const int kslice = slices > 1 ? (int)(cdiv(cdiv(K, slices), (int64_t)G::BK) * G::BK) : (int)K;
@@ -881,17 +880,17 @@ int launch_gemm_dma_t(const void* x, const void* y, void* out, int64_t M, int64_
   if (slices == 1) {
     // The GELU epilogues keep eight waves: with four, the 128 x 128 accumulators of a wave
     // and the epilogue's operands do not fit its registers (12 bytes per lane spilled).
-    const bool w4 = EPI == kEpiNone && use_four_waves(M, N, K);
+    const bool w4 = EPI == kEpiNone && use_four_waves(M, N, cus);
     auto kern = gemm_dma_kernel<TO, XT, YT, 256, 2, EPI, 8>;
     if constexpr (EPI == kEpiNone)
       if (w4) kern = gemm_dma_kernel<TO, XT, YT, 256, 2, EPI, 4>;
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    if (int rc = allow_lds((const void*)kern, kLds, stream, "ferrite_matmul")) return rc;
     hipLaunchKernelGGL(kern, grid, dim3(w4 ? 256 : G::kThreads), kLds, stream, static_cast<const bf16*>(x),
                        static_cast<const bf16*>(y), static_cast<TO*>(out), (int)M, (int)N, (int)K, (int)tiles_m,
                        (int)tiles_n, kslice, ax);
   } else {
     auto kern = gemm_dma_kernel<float, XT, YT>;
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    if (int rc = allow_lds((const void*)kern, kLds, stream, "ferrite_matmul")) return rc;
     hipLaunchKernelGGL(kern, grid, dim3(G::kThreads), kLds, stream, static_cast<const bf16*>(x),
                        static_cast<const bf16*>(y), static_cast<float*>(ws), (int)M, (int)N, (int)K, (int)tiles_m,
                        (int)tiles_n, kslice, nullptr);
@@ -927,8 +926,10 @@ bool dma_ok(const void* x, const void* y, const void* out, int64_t m, int64_t n,
 
 extern "C" int64_t ferrite_hip_matmul_workspace(int64_t m, int64_t n, int64_t k, int in_dtype) {
   if (m < 1 || n < 1 || k < 1) return -1;
-  if (in_dtype == FERRITE_BF16) return ferrite::splitk_workspace(m, n, k);
-  return ferrite::f32_small(m, n) ? ferrite::f32_workspace(m, n, k) : 0;
+  // No stream here: the workspace is sized for the current device's CU count.
+  const int64_t cus = ferrite::cu_count_of(-1);
+  if (in_dtype == FERRITE_BF16) return ferrite::splitk_workspace(m, n, k, cus);
+  return ferrite::f32_small(m, n, cus) ? ferrite::f32_workspace(m, n, k, cus) : 0;
 }
 
 extern "C" int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k,
@@ -958,7 +959,7 @@ extern "C" int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, in
   // f32: 128 x 128 tiles of four waves reach ~80% of the fp32 MFMA peak at 4096^3; a
   // problem with fewer such tiles than CUs (1000^3 has 64) runs 64 x 64 tiles instead,
   // with K split inside the workgroup while SIMDs would stay idle.
-  if (f32_small(m, n)) {
+  if (f32_small(m, n, cu_count(s))) {
     if (out_dtype == FERRITE_BF16) return launch_gemm_f32_small<bf16>(x, y, out, m, n, k, workspace, workspace_bytes, s);
     return launch_gemm_f32_small<float>(x, y, out, m, n, k, workspace, workspace_bytes, s);
   }

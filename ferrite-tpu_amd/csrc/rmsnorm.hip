@@ -584,6 +584,55 @@ __global__ __launch_bounds__(256) void stream_copy2_kernel(const char* __restric
   }
 }
 
+// One-direction streams, the read-only and write-only halves of the ceiling:
+// persistent grids in which wave w takes 4 KB units w, w + waves, ... (four
+// 16-byte non-temporal accesses per lane and unit). The read stream folds every
+// word it loads with XOR so that no load is dead, and each workgroup leaves one
+// word in sink[blockIdx.x]; the fill stream stores `value` in every word.
+constexpr int kStreamUnit = 4096;
+
+__global__ __launch_bounds__(256) void stream_read_kernel(const char* __restrict__ a, uint32_t* __restrict__ sink,
+                                                          int64_t units, int64_t tail_words) {
+  __shared__ uint32_t part[4];
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  u32x4 x = {0u, 0u, 0u, 0u};
+  for (int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); u < units; u += nwaves) {
+    const int64_t o = u * kStreamUnit + lane * 16;
+    const u32x4 a0 = ld16_nt(a + o), a1 = ld16_nt(a + o + 1024), a2 = ld16_nt(a + o + 2048), a3 = ld16_nt(a + o + 3072);
+    x ^= (a0 ^ a1) ^ (a2 ^ a3);
+  }
+  if (blockIdx.x == 0 && threadIdx.x < tail_words) x ^= ld16_nt(a + units * kStreamUnit + (int64_t)threadIdx.x * 16);
+  uint32_t w = (x[0] ^ x[1]) ^ (x[2] ^ x[3]);
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) w ^= (uint32_t)__shfl_xor((int)w, off, kWave);
+  if (lane == 0) part[threadIdx.x >> 6] = w;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = (part[0] ^ part[1]) ^ (part[2] ^ part[3]);
+}
+
+__global__ __launch_bounds__(256) void stream_fill_kernel(char* __restrict__ out, uint32_t value, int64_t units,
+                                                          int64_t tail_words) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  const u32x4 v = {value, value, value, value};
+  for (int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); u < units; u += nwaves) {
+    const int64_t o = u * kStreamUnit + lane * 16;
+    st16_nt(out + o, v);
+    st16_nt(out + o + 1024, v);
+    st16_nt(out + o + 2048, v);
+    st16_nt(out + o + 3072, v);
+  }
+  if (blockIdx.x == 0 && threadIdx.x < tail_words) st16_nt(out + units * kStreamUnit + (int64_t)threadIdx.x * 16, v);
+}
+
+// Workgroups of a stream launch: `blocks` if given (1 .. 65536), else 512 (two per CU), and
+// never more than there are units for.
+int64_t stream_blocks(int blocks, int64_t units) {
+  const int64_t want = blocks > 0 ? blocks : 512;
+  return std::max<int64_t>(1, std::min<int64_t>(want, cdiv(units, 4)));
+}
+
 // ---------------------------------------------------------------------------
 // Scratch of the allocation-free backward (ferrite_hip_rmsnorm_bwd_noalloc):
 // the partial dw rows (and inverse RMS per row) live in this file-scope device
@@ -605,16 +654,18 @@ struct ScratchSlot {
 };
 ScratchSlot g_scratch[kMaxDevices];
 
-// Device address of `scratch` on the current device (looked up on the first
-// call per device), or nullptr with the error message set.
-void* scratch_on_current_device() {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    fail(FERRITE_ERR_LAUNCH, "ferrite_hip_rmsnorm_bwd_noalloc: no current HIP device");
+// Device address of `scratch` on the stream's device (looked up on the first
+// call per device, with that device current), or nullptr with the error message
+// set.
+void* scratch_on_device(hipStream_t stream) {
+  const int dev = stream_device(stream);
+  if (dev < 0 || dev >= kMaxDevices) {
+    fail(FERRITE_ERR_LAUNCH, "ferrite_hip_rmsnorm_bwd_noalloc: cannot tell the stream's HIP device");
     return nullptr;
   }
   ScratchSlot& slot = g_scratch[dev];
-  std::call_once(slot.once, [&slot] {
+  std::call_once(slot.once, [&slot, dev] {
+    DeviceGuard on(dev);
     void* p = nullptr;
     slot.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     slot.ptr = slot.err == hipSuccess ? p : nullptr;
@@ -643,7 +694,7 @@ int bwd_entry(const char* name, const void* h, const void* weight, const void* d
                       std::to_string(plan.bytes) + " bytes of scratch, more than its fixed " +
                       std::to_string((long long)FERRITE_RMSNORM_BWD_SCRATCH_BYTES) +
                       " (use ferrite_hip_rmsnorm_bwd with a workspace)");
-    workspace = scratch_on_current_device();
+    workspace = scratch_on_device(static_cast<hipStream_t>(stream));
     if (!workspace) return FERRITE_ERR_LAUNCH;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -707,4 +758,35 @@ extern "C" int ferrite_hip_stream_copy2(const void* a, const void* b, void* a_ou
                      static_cast<const char*>(a), static_cast<const char*>(b), static_cast<char*>(a_out),
                      static_cast<char*>(b_out), units, tail);
   return check_launch("ferrite_hip_stream_copy2");
+}
+
+extern "C" int ferrite_hip_stream_read(const void* a, int64_t bytes, void* sink, int blocks, void* stream) {
+  using namespace ferrite;
+  if (bytes < 0 || bytes % 16 != 0)
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_stream_read: bytes must be a multiple of 16");
+  if (blocks < 0 || blocks > 65536)
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_stream_read: blocks must be 0 (default) or 1 .. 65536");
+  if (bytes == 0) return FERRITE_OK;
+  if (!a || !sink || (reinterpret_cast<uintptr_t>(a) & 15) || (reinterpret_cast<uintptr_t>(sink) & 3))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_stream_read: null or unaligned pointer");
+  const int64_t units = bytes / kStreamUnit, tail = (bytes % kStreamUnit) / 16;
+  hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)stream_blocks(blocks, units)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const char*>(a), static_cast<uint32_t*>(sink), units,
+                     tail);
+  return check_launch("ferrite_hip_stream_read");
+}
+
+extern "C" int ferrite_hip_stream_fill(void* out, int64_t bytes, uint32_t value, int blocks, void* stream) {
+  using namespace ferrite;
+  if (bytes < 0 || bytes % 16 != 0)
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_stream_fill: bytes must be a multiple of 16");
+  if (blocks < 0 || blocks > 65536)
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_stream_fill: blocks must be 0 (default) or 1 .. 65536");
+  if (bytes == 0) return FERRITE_OK;
+  if (!out || (reinterpret_cast<uintptr_t>(out) & 15))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_stream_fill: null or unaligned pointer");
+  const int64_t units = bytes / kStreamUnit, tail = (bytes % kStreamUnit) / 16;
+  hipLaunchKernelGGL(stream_fill_kernel, dim3((unsigned)stream_blocks(blocks, units)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<char*>(out), value, units, tail);
+  return check_launch("ferrite_hip_stream_fill");
 }

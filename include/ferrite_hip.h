@@ -132,6 +132,20 @@ int ferrite_hip_rmsnorm_bwd_noalloc(const void* h, const void* weight, const voi
 int ferrite_hip_stream_copy2(const void* a, const void* b, void* a_out, void* b_out, int64_t bytes, void* stream);
 
 /*
+ * The two one-direction halves of that ceiling, with no counterpart in the
+ * reference either. ferrite_hip_stream_read loads every byte of `a` once
+ * (16-byte non-temporal loads) and folds the words with XOR, leaving one 32-bit
+ * word per workgroup in sink[0 .. blocks); ferrite_hip_stream_fill stores
+ * `value` in every 32-bit word of `out` (16-byte non-temporal stores).
+ * `blocks` is the number of 256-thread workgroups of the persistent grid
+ * (0: 512, two per CU; at most 65536); sink holds at least that many words
+ * (512 when blocks is 0). bytes % 16 == 0; a and out 16-byte aligned, sink
+ * 4-byte aligned.
+ */
+int ferrite_hip_stream_read(const void* a, int64_t bytes, void* sink, int blocks, void* stream);
+int ferrite_hip_stream_fill(void* out, int64_t bytes, uint32_t value, int blocks, void* stream);
+
+/*
  * out[M, N] = x[M, K] @ y[K, N] with f32 accumulation (matmul.py:27-38, :52-86).
  * in_dtype FERRITE_BF16 uses bf16 MFMA; FERRITE_F32 uses fp32 MFMA (true fp32
  * products, the reference's Precision.HIGHEST, _compat.py:17-25). Ragged shapes

@@ -25,7 +25,7 @@ def _declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     declared = _declared_symbols()
-    assert len(declared) == 27
+    assert len(declared) == 29
     out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH], capture_output=True, text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s(\w+)", out))
     missing = [s for s in declared if s not in exported]
@@ -171,3 +171,15 @@ def test_platform_peaks():
     assert BlockSizes.for_device() == BlockSizes(128, 128, 128, 128)
     with platform.interpret_mode() as on:
         assert on is False
+
+
+def test_stream_kernels_argument_checks():
+    """Bad sizes, grids and pointers are refused before any launch (runs on the CPU path too)."""
+    lib = _hip.lib()
+    assert lib.ferrite_hip_stream_read(None, 15, None, 0, None) == 1
+    assert "multiple of 16" in _hip.last_error()
+    assert lib.ferrite_hip_stream_read(None, 16, None, 70000, None) == 1
+    assert "blocks" in _hip.last_error()
+    assert lib.ferrite_hip_stream_fill(None, 32, 1, 0, None) == 1
+    assert "null" in _hip.last_error()
+    assert lib.ferrite_hip_stream_fill(None, 0, 1, 0, None) == 0

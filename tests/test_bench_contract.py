@@ -38,8 +38,12 @@ def test_traffic_table_feeds_the_roofline():
     roof = bench._roofline("attn_fwd", flops, alg, flops / 900e12, traffic=bench._traffic("attn_fwd"))
     assert roof["bound"] == "mfma" and abs(roof["frac"] - 900.0 / 2516.6) < 1e-3
     assert roof["unit"] == "TFLOP/s" and abs(roof["achieved"] - 900.0) < 0.01 and roof["traffic"] > alg
+    # a traffic figure read from the committed profile says where it came from
+    assert "profiles/hbm_traffic.md" in roof["traffic_source"] and "not measured in this run" in roof["traffic_source"]
     norm = bench._roofline("add_rmsnorm", 5 * 4096 * 1024, 33556480, 33556480 / 5000e9)
     assert norm["bound"] == "hbm" and norm["unit"] == "GB/s" and abs(norm["frac"] - 5000 / 8000) < 1e-4
+    # without a traffic figure the field is left out rather than reported as null
+    assert "traffic" not in norm and "traffic_source" not in norm
     json.dumps(roof)
 
 

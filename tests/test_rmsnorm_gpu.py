@@ -233,3 +233,33 @@ def test_stream_copy2_is_exact(dev, nbytes):
     torch.cuda.synchronize()
     assert torch.equal(ao[:n], a) and torch.equal(bo[:n], b)
     assert bool((ao[n:] == 7).all()) and bool((bo[n:] == 7).all())
+
+
+@pytest.mark.parametrize("blocks", [0, 1, 7, 1024])
+@pytest.mark.parametrize("nbytes", [16, 4096, 4096 * 37 + 48, 3 << 20])
+def test_stream_read_and_fill_are_exact(dev, nbytes, blocks):
+    """The one-direction streams bench.py measures as HBM ceilings: ferrite_hip_stream_read leaves
+    one word per workgroup whose XOR over the workgroups is the XOR of every word of the buffer
+    (every byte read, partial 4 KB units included), and ferrite_hip_stream_fill writes `value` into
+    every word and nothing past them."""
+    from ferrite import _hip
+
+    lib = _hip.lib()
+    n = nbytes // 4
+    g = torch.Generator(device=dev).manual_seed(11)
+    a = torch.randint(-2**31, 2**31 - 1, (n,), generator=g, device=dev, dtype=torch.int32)
+    units = nbytes // 4096
+    used = max(1, min(blocks or 512, -(-units // 4)))  # the launch's workgroup count
+    sink = torch.zeros(1024, device=dev, dtype=torch.int32)
+    _hip.check(lib.ferrite_hip_stream_read(a.data_ptr(), nbytes, sink.data_ptr(), blocks, _hip.stream_of(a)),
+               "stream_read")
+    torch.cuda.synchronize()
+    words = a.cpu().numpy().view(np.uint32)
+    folded = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)[:used])
+    assert int(folded) == int(np.bitwise_xor.reduce(words))
+    out = torch.full((n + 64,), 7, device=dev, dtype=torch.int32)
+    _hip.check(lib.ferrite_hip_stream_fill(out.data_ptr(), nbytes, 0x3F803F80, blocks, _hip.stream_of(a)), "fill")
+    torch.cuda.synchronize()
+    o = out.cpu().numpy().view(np.uint32)
+    assert np.all(o[:n] == 0x3F803F80) and np.all(o[n:] == 7)
+
