@@ -40,9 +40,9 @@ class ServeConfig:
     batch: int = 1
     max_len: int = 512
     buckets: tuple[int, ...] = (64, 128, 256)
-    prefill_kernels: str = "pallas"  # "pallas" | "xla": attention + norms in prefill
-    decode_kernels: str = "pallas"  # "pallas" (HIP decode attention + norms) | "xla" (torch math, as the reference)
-    graphs: bool = True  # replay prefill and decode from captured HIP graphs
+    prefill_kernels: str = "pallas"  # prefill's attention and norms: HIP kernels ("pallas") or torch ("xla")
+    decode_kernels: str = "pallas"  # decode: HIP decode attention and norms ("pallas"), or torch math ("xla")
+    graphs: bool = True  # capture prefill and decode as HIP graphs and replay them
 
 
 def bucket_for(length: int, buckets: tuple[int, ...]) -> int:
@@ -50,14 +50,16 @@ def bucket_for(length: int, buckets: tuple[int, ...]) -> int:
     for b in buckets:
         if length <= b:
             return b
-    raise ValueError(f"prompt length {length} exceeds largest bucket {buckets[-1]}")
+    raise ValueError(f"no bucket holds a {length}-token prompt (buckets go up to {buckets[-1]})")
 
 
-# ---------------------------------------------------------------- model pieces
+# The model, split into the prefill and decode passes.
 
 
 def _block_prefill(layer, h, pending, cfg: GPTConfig):
-    """One transformer block over a full sequence, returning (h, pending, k, v) (engine.py:53-66)."""
+    """Runs a block on a whole padded prompt. Returns the residual stream, the MLP output still to
+    be added by the next norm, and the block's keys and values [B, H, S, hd] for the cache
+    (engine.py:53-66)."""
     if pending is None:
         y = _norm(h, layer["ln1"], None, cfg)
     else:
@@ -71,10 +73,11 @@ def _block_prefill(layer, h, pending, cfg: GPTConfig):
 
 @torch.no_grad()
 def prefill(params, tokens, lengths, cfg: GPTConfig, max_len: int, k_cache=None, v_cache=None):
-    """tokens [B, L] (right-padded), lengths [B] -> (next-token logits [B, V], k_cache, v_cache)
-    (engine.py:69-86). Caches are [layers, B, H, max_len, hd]; the prompt's keys and values
-    fill positions 0..L-1 (padding positions hold values decode never attends to and
-    overwrites in order). Given caches are written in place."""
+    """Runs the model over right-padded prompts ``tokens`` [B, L] whose true lengths are
+    ``lengths`` [B], and returns the logits of each prompt's last real token [B, V] with the
+    two caches [layers, B, H, max_len, hd] (engine.py:69-86). Cache rows 0..L-1 receive the
+    prompt's keys and values; rows past a prompt's length hold padding that decode masks out
+    and overwrites as it goes. Caches passed in are filled in place."""
     b, s = tokens.shape
     if k_cache is None:
         shape = (cfg.n_layer, b, cfg.n_head, max_len, cfg.head_dim)
@@ -94,8 +97,8 @@ def prefill(params, tokens, lengths, cfg: GPTConfig, max_len: int, k_cache=None,
 
 
 def _cache_attention(q, k_cache, v_cache, pos, scale):
-    """q [B, H, hd]; caches [B, H, max_len, hd]; pos [B]: f32 scores over keys <= pos
-    (engine.py:89-95)."""
+    """Attention of one new query per sequence (q [B, H, hd]) over the cache rows up to and
+    including its position pos [B], with f32 scores (engine.py:89-95)."""
     s = torch.einsum("bhd,bhkd->bhk", q.float(), k_cache.float()) * scale
     keys = torch.arange(k_cache.shape[2], device=q.device)[None, :]
     s = torch.where((keys <= pos.long()[:, None])[:, None, :], s, torch.full_like(s, -1e30))
@@ -104,16 +107,18 @@ def _cache_attention(q, k_cache, v_cache, pos, scale):
 
 
 def _write_cache(cache, new, pos):
-    """cache [B, H, max_len, hd] <- new [B, H, hd] at row pos[b] (engine.py:98-104), in place."""
+    """Stores each sequence's new row (new [B, H, hd]) at its own position pos[b] of the cache
+    [B, H, max_len, hd], in place (engine.py:98-104)."""
     idx = torch.arange(cache.shape[0], device=cache.device)
     cache[idx, :, pos.long()] = new.to(cache.dtype)
 
 
 @torch.no_grad()
 def decode_step(params, token, pos, k_cache, v_cache, cfg: GPTConfig):
-    """One greedy decode step (engine.py:107-131): token [B] at position pos [B] -> logits
-    [B, V]; the caches are updated in place. ``cfg.attention == "pallas"`` runs the HIP
-    decode-attention kernel; otherwise the torch restatement of the reference's XLA math."""
+    """Advances every sequence by one token: feeds ``token`` [B] at positions ``pos`` [B],
+    writes their keys and values into the caches and returns the next logits [B, V]
+    (engine.py:107-131). With ``cfg.attention == "pallas"`` the HIP decode-attention kernel does
+    the cache write and the attention; otherwise torch restates the reference's XLA math."""
     b = token.shape[0]
     h = (params["tok_emb"][token] + params["pos_emb"][pos.long()]).to(cfg.dtype)  # [B, d]
     scale = 1.0 / math.sqrt(cfg.head_dim)
@@ -140,7 +145,7 @@ def decode_step(params, token, pos, k_cache, v_cache, cfg: GPTConfig):
     return _dot_f32(y, params["tok_emb"].to(cfg.dtype).t())
 
 
-# ---------------------------------------------------------------- engine
+# The serving engine: captured prefill per bucket, one captured decode step.
 
 
 class _Captured:
@@ -177,12 +182,14 @@ class _Captured:
 
 
 class Engine:
-    """Prefill per bucket and one decode step, each captured as a HIP graph; greedy generation
-    (engine.py:137-203)."""
+    """Serves greedy generation from captured HIP graphs: one prefill graph per prompt bucket
+    and one decode-step graph, all built when the engine is constructed (engine.py:137-203).
+    Usable as a context manager; ``close()`` releases the graphs and ends the engine's use."""
 
     def __init__(self, params, model_cfg: GPTConfig, serve_cfg: ServeConfig, device=None):
         if max(serve_cfg.buckets) > model_cfg.seq_len or serve_cfg.max_len > model_cfg.seq_len:
-            raise ValueError("buckets and max_len must fit within the model's trained seq_len (positional table)")
+            raise ValueError(f"the model's positional table has {model_cfg.seq_len} rows: buckets and max_len "
+                             "cannot exceed it")
         if max(serve_cfg.buckets) > serve_cfg.max_len:
             raise ValueError("buckets must fit within max_len")
         self.params = params
@@ -206,6 +213,7 @@ class Engine:
         self.token = torch.zeros((b,), dtype=torch.long, device=dev)
         self.pos = torch.zeros((b,), dtype=torch.int32, device=dev)
         self.compile_seconds: dict[str, float] = {}
+        self._closed = False
         self._prefill: dict[int, Any] = {}
         self._tokens: dict[int, torch.Tensor] = {}
         # The captured functions hold the tensors they use, not the engine: no reference cycle,
@@ -232,15 +240,21 @@ class Engine:
         self.k_cache.zero_()
         self.v_cache.zero_()
 
-    # -- lifetime -----------------------------------------------------------
+    # Lifetime.
 
     def close(self) -> None:
-        """Release every captured graph now (prefill buckets and decode). The engine cannot
-        serve afterwards. Also called on leaving a ``with Engine(...) as eng:`` block."""
+        """Releases the captured graphs (every prefill bucket and the decode step) at once; leaving
+        a ``with`` block does the same. A closed engine refuses further prefill, decode and
+        generate calls. Closing twice is harmless."""
         for cap in self._prefill.values():
             cap.close()
         self._decode.close()
         self._prefill.clear()
+        self._closed = True
+
+    def _check_open(self) -> None:
+        if self._closed:
+            raise RuntimeError("engine closed: its graphs were released by close(); build a new Engine to serve")
 
     def __enter__(self) -> "Engine":
         return self
@@ -248,16 +262,19 @@ class Engine:
     def __exit__(self, *exc) -> None:
         self.close()
 
-    # -- public API ---------------------------------------------------------
+    # Serving.
 
     def prefill(self, prompts: list[list[int]]):
-        """Returns (first token [B], pos [B], caches). Prompts are right-padded to a bucket."""
+        """Pads the prompts on the right to the smallest bucket that holds them, replays that
+        bucket's prefill graph and returns the greedy first token of each [B], the positions
+        decode continues from (the prompt lengths) [B], and the two caches."""
+        self._check_open()
         b = self.serve.batch
         if len(prompts) != b:
-            raise ValueError(f"engine built for batch {b}, got {len(prompts)} prompts")
+            raise ValueError(f"this engine serves {b} prompt(s) at a time; {len(prompts)} given")
         lengths = np.array([len(p) for p in prompts], np.int32)
         if lengths.min() < 1:
-            raise ValueError("empty prompt")
+            raise ValueError("every prompt needs at least one token")
         bucket = bucket_for(int(lengths.max()), self.serve.buckets)
         tokens = np.zeros((b, bucket), np.int64)
         for i, p in enumerate(prompts):
@@ -268,16 +285,23 @@ class Engine:
         return torch.argmax(logits, dim=-1), self.lengths.clone(), self.k_cache, self.v_cache
 
     def decode(self, token, pos, kc=None, vc=None):
-        """One step from ``token`` at ``pos``; returns (next token, caches)."""
+        """Replays the decode graph for ``token`` [B] at positions ``pos`` [B] and returns the
+        greedy next token [B] and the two caches (``kc`` / ``vc`` are accepted for the
+        reference's signature; the engine always uses its own caches)."""
+        self._check_open()
         self.token.copy_(token)
         self.pos.copy_(pos)
         logits = self._decode()
         return torch.argmax(logits, dim=-1), self.k_cache, self.v_cache
 
     def generate(self, prompts: list[list[int]], max_new_tokens: int) -> tuple[np.ndarray, dict]:
-        """Greedy generation; returns generated tokens [B, max_new_tokens] and timing stats."""
+        """Generates ``max_new_tokens`` tokens per prompt greedily. Returns them as an array
+        [B, max_new_tokens] and a dict of timings: time to first token, median and p99
+        inter-token latency, tokens per second, total seconds and the number of captures."""
+        self._check_open()
         if max(len(p) for p in prompts) + max_new_tokens > self.serve.max_len:
-            raise ValueError("prompt + new tokens exceed max_len")
+            raise ValueError(f"the longest prompt plus {max_new_tokens} new tokens does not fit the "
+                             f"{self.serve.max_len}-row cache")
         sync = torch.cuda.synchronize if self.device.type == "cuda" else (lambda: None)
         t0 = time.perf_counter()
         token, pos, _, _ = self.prefill(prompts)
@@ -305,7 +329,8 @@ class Engine:
 
 @torch.no_grad()
 def reference_greedy(params, cfg: GPTConfig, prompt: list[int], max_new_tokens: int) -> np.ndarray:
-    """Slow but obviously correct greedy decoding: the full model re-run each step (engine.py:231-242)."""
+    """Greedy decoding without a cache, as a check on the engine: every step runs the whole
+    model over the prompt and the tokens so far (engine.py:231-242)."""
     from ferrite.model.gpt import forward
 
     dev = params["tok_emb"].device

@@ -5,7 +5,11 @@
  * enqueues its kernels on `stream` (a hipStream_t passed as void*, NULL = the
  * default stream), never synchronises, never allocates, and returns 0 on
  * success. A non-zero return is one of the FERRITE_ERR_* codes; the message
- * for the calling thread's last failure is ferrite_hip_last_error().
+ * for the calling thread's last failure is ferrite_hip_last_error(). Work runs
+ * on the stream's device: per-device state (the CU count that shapes a grid, a
+ * kernel's LDS limit, the no-alloc scratch array) is looked up for that device,
+ * whichever device is current on the calling thread, and set up once per
+ * device. Entry points are reentrant and may be called from several threads.
  *
  * All tensors are dense and row-major (last dimension contiguous). Outputs are
  * preallocated by the caller, exactly as XLA preallocates the out_shape buffers
@@ -265,7 +269,9 @@ int ferrite_hip_adamw(int64_t n_tensors, void* const* params, const void* const*
  * (those the reference's _validate accepts, flash_attention.py:341-343): any
  * D <= 128 (zero-padded inside the kernel to 64 or 128) and any multiple of 128
  * (D > 256 runs slab-wise: 128 output columns per workgroup, the scores
- * recomputed per slab). The same holds for every backward entry point below.
+ * recomputed per slab). The same holds for the backward entry points below on
+ * [B, H, S, D] tensors; the packed-QKV entry points (ferrite_hip_attn_fwd_qkv,
+ * ferrite_hip_attn_bwd_qkv) are the exception and take head_dim 64 or 128 only.
  * Sq, Sk >= 1; Sq and Sk need not be multiples of any tile size.
  */
 int ferrite_hip_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t b, int64_t h,

@@ -44,6 +44,20 @@ def test_engine_validation():
         eng.prefill([[1], [2]])
 
 
+def test_closed_engine_refuses_to_serve():
+    """close() ends an engine's use: prefill, decode and generate raise instead of failing deep
+    inside (a missing bucket) or quietly capturing a new graph."""
+    cfg = CFG.replace(**XLA)
+    params = init_params(0, cfg)
+    with Engine(params, cfg, ServeConfig(batch=1, max_len=64, buckets=(32,), prefill_kernels="xla",
+                                         decode_kernels="xla", graphs=False)) as eng:
+        tok, pos, _, _ = eng.prefill([[1, 2, 3]])
+    for call in (lambda: eng.prefill([[1, 2, 3]]), lambda: eng.decode(tok, pos), lambda: eng.generate([[1, 2]], 2)):
+        with pytest.raises(RuntimeError, match="engine closed"):
+            call()
+    eng.close()  # closing again is harmless
+
+
 def test_capture_window_holds_off_the_cycle_collector():
     """ferrite.graphs.capture_window: no cyclic collection inside a capture, the collector's
     previous state restored afterwards (also when the capture raises)."""

@@ -60,8 +60,9 @@ def test_noalloc_matches_workspace_entry(dev, first, second, xd, wd, od, direct)
 
 
 def test_noalloc_refuses_shapes_beyond_its_scratch(dev):
-    """4112 rows of dim 8192 take 257 partial rows of 8192 floats (8.4 MB > 8 MiB): refused before
-    any launch, outputs untouched."""
+    """dim 8192 is past the one-pass kernel's 4096, so 4112 rows take the general path: 512 partial
+    rows of 8192 floats plus one float per row, (512 * 8192 + 4112) * 4 = 16.8 MB > 8 MiB. Refused
+    before any launch, outputs untouched."""
     rows, dim = 4112, 8192
     h, dy, w, _ = _inputs(dev, rows, dim, "bf16", "f32", False, seed=230)
     dh = torch.full((rows, dim), float("nan"), dtype=torch.bfloat16, device=dev)
@@ -73,3 +74,27 @@ def test_noalloc_refuses_shapes_beyond_its_scratch(dev):
     torch.cuda.synchronize()
     assert torch.isnan(dw).all() and torch.isnan(dh.float()).all()
     np.testing.assert_equal(_hip.RMSNORM_BWD_SCRATCH_BYTES, 8 << 20)
+
+
+def test_noalloc_scratch_edge_on_the_general_path(dev):
+    """The refusal edge of the general path (dim % 8 != 0): nparts = min(rows, 512) partial rows of
+    dim floats plus one float per row. dim 4095 with 512 rows needs (512 * 4095 + 512) * 4 bytes,
+    exactly the 8 MiB array: accepted and bitwise equal to the workspace entry. 513 rows need four
+    bytes more: refused, outputs untouched."""
+    dim = 4095
+    rows = 512
+    assert (rows * dim + rows) * 4 == _hip.RMSNORM_BWD_SCRATCH_BYTES
+    h, dy, w, _ = _inputs(dev, rows, dim, "bf16", "f32", False, seed=240)
+    ref_dh, ref_dw = _run(dev, h, dy, w, None, rows, dim, "bf16", "f32", "bf16", noalloc=False)
+    got_dh, got_dw = _run(dev, h, dy, w, None, rows, dim, "bf16", "f32", "bf16", noalloc=True)
+    assert torch.equal(got_dh, ref_dh) and torch.equal(got_dw, ref_dw)
+    rows = 513
+    h, dy, w, _ = _inputs(dev, rows, dim, "bf16", "f32", False, seed=250)
+    dh = torch.full((rows, dim), float("nan"), dtype=torch.bfloat16, device=dev)
+    dw = torch.full((dim,), float("nan"), dtype=torch.float32, device=dev)
+    rc = _hip.lib().ferrite_hip_rmsnorm_bwd_noalloc(h.data_ptr(), w.data_ptr(), dy.data_ptr(), None, dh.data_ptr(),
+                                                    dw.data_ptr(), rows, dim, _hip.BF16, _hip.F32, _hip.BF16, 1e-6,
+                                                    _hip.stream_of(h))
+    assert rc == 1 and "scratch" in _hip.last_error() and str((512 * dim + rows) * 4) in _hip.last_error()
+    torch.cuda.synchronize()
+    assert torch.isnan(dw).all() and torch.isnan(dh.float()).all()
