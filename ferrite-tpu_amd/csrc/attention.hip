@@ -36,6 +36,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "attn_sched.h"
 
 namespace ferrite {
 namespace {
@@ -963,10 +964,20 @@ struct FwdW {
   static_assert(KT::kBlocks == VT::kBlocks && kDma >= 1, "K and V tiles split evenly over the waves");
 };
 
-template <int D, int RB, int W, bool ZIG, int KSPLIT = 1>
+// SPLIT (a resident grid, ZIG pairing, 128-row tiles, an even number of them): the
+// long tile L = n_qtiles - 1 - p and the short tile p of pair p have
+// 2 (L + 1) + 2 (p + 1) = 2 (n_qtiles + 1) key tiles between them, and a whole
+// long tile keeps its workgroup busy long after its partner is done. Instead
+// blocks A and B of the pair cut that sequence of key tiles at `cut`
+// (sched::split_segments): the tile the cut falls in is shared, and A and B
+// leave their states of it (unnormalised O, row max, row sum) in the
+// workspace `ws`; the second to get there (an atomic count per pair, kept even
+// between launches) merges the two in a fixed order and writes O and lse.
+template <int D, int RB, int W, bool ZIG, int KSPLIT = 1, bool SPLIT = false>
 __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4 : W == 4 ? 2 : 1)) void attn_fwd_sw_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, bf16* __restrict__ o,
-    float* __restrict__ lse, int bh_count, int S, int d, float scale_log2, int neg_q, int n_qtiles, AttnViews vw) {
+    float* __restrict__ lse, int bh_count, int S, int d, float scale_log2, int neg_q, int n_qtiles, AttnViews vw,
+    char* __restrict__ ws, int cut) {
   typedef FwdW<D, RB, W, KSPLIT> F;
   typedef typename F::KT KT;
   typedef typename F::VT VT;
@@ -982,7 +993,6 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   const int bh = blockIdx.x % bh_count;
   const int blk = (int)(blockIdx.x / bh_count);
   const int half_q = n_qtiles / 2;
-  const int qt = !ZIG ? n_qtiles - 1 - blk : blk < n_qtiles - half_q ? n_qtiles - 1 - blk : blk - (n_qtiles - half_q);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
@@ -991,19 +1001,44 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   constexpr int WR = W / KSPLIT, NKT = 2 / KSPLIT;
   const int wr = wave % WR;
   const int kh = KSPLIT == 1 ? 0 : wave / WR;
-  const int q0 = qt * F::BQ;
-  const int q0w = q0 + 32 * RB * wr;
-  // Tiles of 64 keys: n for the workgroup, n_w for this wave, whose last
-  // tile (keys from 64 (n_w - 1)) is its diagonal. The upper key half of the
-  // first 32 rows sees no key at all: that wave computes nothing.
-  const int n = (min(q0 + F::BQ, S) - 1) / F::BK + 1;
-  const int n_w = q0w < S && !(kh == 1 && q0w == 0) ? (q0w + 32 * RB - 1) / F::BK + 1 : 0;
 
   // Row pitches (elements): d for dense [B, H, S, d] tensors.
   const int ldq = (int)vw.q.r, ldk = (int)vw.k.r, ldv = (int)vw.v.r;
   const bf16* qb = q + vw.q.at(bh, vw.heads);
+
+  // The workgroup's segments: key tiles [t0, t1) of query tile qt. One whole
+  // tile without SPLIT; with it, block A's share of the long tile L (role 0),
+  // or block B's share of L (role 1) and then the whole short tile.
+  static_assert(!SPLIT || (ZIG && KSPLIT == 2 && RB == 1 && F::BQ == 2 * F::BK), "the split pairs 128-row tiles");
+  // One segment, inlined once per call below (a loop over the segments left
+  // the register allocation of the key-split kernel with spills).
+  auto segment = [&](const int qt, const int t0, const int t1, const int role) __attribute__((always_inline)) {
+  const int q0 = qt * F::BQ;
+  const int q0w = q0 + 32 * RB * wr;
+  // Tiles of 64 keys: n for the workgroup, n_w for this wave, whose last
+  // tile (keys from 64 (nwf - 1)) is its diagonal, both counted from t0. The
+  // upper key half of 32 rows starting a key tile sees no key of that tile:
+  // that wave computes nothing in a segment that begins with its diagonal tile
+  // (the first 32 rows of the sequence, and with SPLIT the start of B's share).
+  int n, n_w, nwf, tt1, nkv;
   const bf16* kb = k + vw.k.at(bh, vw.heads);
   const bf16* vb = v + vw.v.at(bh, vw.heads);
+  if constexpr (SPLIT) {
+    tt1 = min(t1, (min(q0 + F::BQ, S) - 1) / F::BK + 1);
+    n = tt1 - t0;
+    nwf = q0w < S ? (q0w + 32 * RB - 1) / F::BK + 1 : 0;
+    n_w = kh == 1 && q0w % F::BK == 0 && t0 == nwf - 1 ? 0 : max(min(nwf, tt1) - t0, 0);
+    // K and V rows of the segment; the DMA reads nothing past them.
+    kb += (int64_t)t0 * F::BK * ldk;
+    vb += (int64_t)t0 * F::BK * ldv;
+    nkv = n * F::BK;
+  } else {
+    (void)t0, (void)t1, (void)role;
+    n = (min(q0 + F::BQ, S) - 1) / F::BK + 1;
+    n_w = q0w < S && !(kh == 1 && q0w == 0) ? (q0w + 32 * RB - 1) / F::BK + 1 : 0;
+    nwf = tt1 = 0;
+    nkv = S;
+  }
 
   // K_0 and K_1 go out first; stage j then loads K_{j+3} and V_{j+1}.
   const PpDma<KT, true, F::kWaves> kdma(wave, ldk);
@@ -1017,12 +1052,12 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   static_assert(2 * KT::kBytes + F::kWaves * 32 * RB * kQRow <= F::kLds, "the Q rows fit the idle ring slots");
   const bool q_lds = d == D;
   char* const qst = smem + 2 * KT::kBytes + wave * (32 * RB * kQRow);
-  kdma.issue(kb, 0, S, ldk, kring);
+  kdma.issue(kb, 0, nkv, ldk, kring);
   if (q_lds) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) dma_rows32<D>(qb, q0w + 32 * rb, S, ldq, qst + rb * 32 * kQRow);
   }
-  kdma.issue(kb, F::BK, S, ldk, kring + KT::kBytes);
+  kdma.issue(kb, F::BK, nkv, ldk, kring + KT::kBytes);
 
   bf16x8 qf[RB][KS];
   if (!q_lds) {
@@ -1044,6 +1079,11 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) lim[rb][kt] = q0w % F::BK + rb * 32 + l32 - kt * 32 - g * 16;
+  if (SPLIT && nwf > tt1) {  // (SPLIT only: nwf and tt1 are 0 otherwise)
+    // This wave's last tile of the segment lies below its diagonal: all of it is visible.
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) lim[rb][0] = lim[rb][1] = 1 << 20;
+  }
 
   f32x16 acc[RB][DT];  // O^T per row block: register r of tile u = dim u*32 + (r/4)*8 + g*4 + r%4
 #pragma unroll
@@ -1068,11 +1108,13 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   // share. Issued unconditionally: a tile past the end has an empty buffer
   // range, so its instructions read nothing and write zeros into a slot nobody
   // reads again.
+  static_assert(F::kSlots == sched::kFwdSlots, "the ring of the schedule");
   auto dma_part = [&](int j, int qd) {
+    const int tk = sched::fwd_k_loaded(j), tv = sched::fwd_v_loaded(j);
     if (qd < F::kDma)
-      kdma.issue_one(kb, (j + 3) * F::BK, S, ldk, kring + ((j + 3) % F::kSlots) * KT::kBytes, qd);
+      kdma.issue_one(kb, tk * F::BK, nkv, ldk, kring + (tk % F::kSlots) * KT::kBytes, qd);
     else
-      vdma.issue_one(vb, (j + 1) * F::BK, S, ldv, vring + ((j + 1) % F::kSlots) * VT::kBytes, qd - F::kDma);
+      vdma.issue_one(vb, tv * F::BK, nkv, ldv, vring + (tv % F::kSlots) * VT::kBytes, qd - F::kDma);
   };
   auto dma = [&](int j) {
 #pragma unroll
@@ -1094,8 +1136,8 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
     // out of the stage loop (the reads' 16-bit offsets cannot reach past 64 KB
     // of ring), and those addresses spill: the D = 64 key-split kernel wrote
     // 12 bytes of scratch per lane without this.
-    int koff = ((j + 1) % F::kSlots) * KT::kBytes;
-    int voff = ((j - 1 + F::kSlots) % F::kSlots) * VT::kBytes;
+    int koff = (sched::fwd_k_read(j) % F::kSlots) * KT::kBytes;
+    int voff = ((sched::fwd_v_read(j) + F::kSlots) % F::kSlots) * VT::kBytes;
     asm volatile("" : "+s"(koff), "+s"(voff));
     const char* kp = kring + koff + kbase;
     const char* vp = vring + voff + vbase;
@@ -1235,9 +1277,9 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
     // This wave's parts of K_{j+1} and V_{j-1} have landed; the loads issued
     // by stage j - 1 (or K_1 of the prologue) may still be in flight.
     if (j >= 0)
-      wait_vmem<2 * F::kDma>();
+      wait_vmem<sched::fwd_in_flight(0, F::kDma)>();
     else
-      wait_vmem<F::kDma>();
+      wait_vmem<sched::fwd_in_flight(-1, F::kDma)>();
     // Every wave's parts have landed and every wave has left stage j - 1.
     lds_barrier();
   };
@@ -1332,7 +1374,8 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
       const float m1 = xs[16 * DT * 64 + lane];
       const float l1 = xs[16 * DT * 64 + 64 + lane];
       const float mm = fmaxf(m[0], m1);
-      const float a0 = __builtin_amdgcn_exp2f(m[0] - mm), a1 = __builtin_amdgcn_exp2f(m1 - mm);
+      float a0 = __builtin_amdgcn_exp2f(m[0] - mm), a1 = __builtin_amdgcn_exp2f(m1 - mm);
+      if (SPLIT && mm == -INFINITY) a0 = a1 = 0.f;  // neither half saw a key of the segment
 #pragma unroll
       for (int u = 0; u < DT; ++u)
 #pragma unroll
@@ -1346,14 +1389,88 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
     }
   }
   // The lower key half of each row block writes (every wave without KSPLIT).
-  const bool writer = kh == 0 && n_w > 0;
+  const bool writer = kh == 0 && q0w < S;
+  float lrow[RB];  // the rows' sums of p (the lane's and its partner's 32 lanes away)
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) lrow[rb] = lane32_sum(lsum[rb]);
+
+  if constexpr (SPLIT) {
+    if (role >= 0) {
+      // This share of the long tile: the writers' (O, m, l) into the pair's
+      // slot, role-major, then one count per workgroup.
+      const int slot = bh * half_q + blk % half_q;
+      constexpr int kAccFloats = WR * DT * 16 * 64;
+      constexpr int kPartBytes = (kAccFloats + 2 * F::BQ) * 4;
+      float* const part = reinterpret_cast<float*>(ws + (int64_t)(2 * slot + role) * kPartBytes);
+      float* const other = reinterpret_cast<float*>(ws + (int64_t)(2 * slot + 1 - role) * kPartBytes);
+      int* const count = reinterpret_cast<int*>(ws + (int64_t)2 * bh_count * half_q * kPartBytes) + slot;
+      // The shares cross between workgroups through device memory with
+      // agent-scope accesses (each store and load goes past the caches a CU
+      // does not share), not through agent-scope fences: a fence writes back
+      // or invalidates the whole L2 of its XCD, which every other workgroup
+      // there then refills (the split ran 2.5x slower with them).
+      // Pairs of floats, lane-contiguous: register pair (u, r / 2) of the 64
+      // lanes fills 512 consecutive bytes, whole cache lines.
+      auto put2 = [](float* p, float x, float y) {
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, f32x2{x, y}), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      };
+      auto get2 = [](const float* p) {
+        return __builtin_bit_cast(f32x2, __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)),
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      };
+      auto at = [&](int u, int r2) { return ((wr * DT + u) * 8 + r2) * 128 + 2 * lane; };
+      if (writer) {
+#pragma unroll
+        for (int u = 0; u < DT; ++u)
+#pragma unroll
+          for (int r2 = 0; r2 < 8; ++r2) put2(part + at(u, r2), acc[0][u][2 * r2], acc[0][u][2 * r2 + 1]);
+        if (g == 0) put2(part + kAccFloats + 2 * (32 * wr + l32), m[0], lrow[0]);
+      }
+      __shared__ int arrival;
+      wait_vmem<0>();  // this wave's share has reached memory before the workgroup's count
+      lds_barrier();
+      if (threadIdx.x == 0) arrival = atomicAdd(count, 1);
+      lds_barrier();
+      // The first of A and B to arrive is done with the long tile (the count is
+      // even before a launch and each launch adds two per pair).
+      if ((arrival & 1) == 0) return;
+      if (writer) {
+        // Merge in role order whichever block runs it: A (keys before the
+        // split), then B.
+        const f32x2 st = get2(other + kAccFloats + 2 * (32 * wr + l32));
+        const float mo = st[0], lo = st[1];
+        const float ma = role == 0 ? m[0] : mo, mb = role == 0 ? mo : m[0];
+        const float la = role == 0 ? lrow[0] : lo, lb = role == 0 ? lo : lrow[0];
+        const float mm = fmaxf(ma, mb);  // A's rows all see key 0: finite
+        const float ca = __builtin_amdgcn_exp2f(ma - mm), cb = __builtin_amdgcn_exp2f(mb - mm);
+#pragma unroll
+        for (int u = 0; u < DT; ++u)
+#pragma unroll
+          for (int r2 = 0; r2 < 8; ++r2) {
+            const f32x2 oo = get2(other + at(u, r2));
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const float mine = acc[0][u][2 * r2 + e];
+              const float xa = role == 0 ? mine : oo[e], xb = role == 0 ? oo[e] : mine;
+              // Spelled out: A and B inline this merge separately, and left to
+              // itself the compiler contracts it into an fma on different sides
+              // in the two copies (results that differ in the last bit).
+              acc[0][u][2 * r2 + e] = __builtin_fmaf(xa, ca, xb * cb);
+            }
+          }
+        lrow[0] = __builtin_fmaf(la, ca, lb * cb);
+        m[0] = mm;
+      }
+    }
+  }
 
   if (d < D) {
     if (!writer) return;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const int row = q0w + 32 * rb + l32;
-      const float l = lane32_sum(lsum[rb]);
+      const float l = lrow[rb];
       store_acc_rows<bf16, D, true>(acc[rb], o + vw.o.at(bh, vw.heads), row, S, d, 1.0f / l, vw.o.r);
       if (g == 0 && row < S) lse[(int64_t)bh * S + row] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
     }
@@ -1370,10 +1487,25 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int row = q0w + 32 * rb + l32;
-    const float l = lane32_sum(lsum[rb]);
+    const float l = lrow[rb];
     if (g == 0 && row < S) lse[(int64_t)bh * S + row] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
     store_acc_rows_lds<D>(acc[rb], ot + rb * 32 * 2 * D, o + vw.o.at(bh, vw.heads), q0w + 32 * rb, S, 1.0f / l,
                           vw.o.r);
+  }
+  };  // segment
+
+  if constexpr (!SPLIT) {
+    segment(sched::query_tile(blk, n_qtiles, ZIG), 0, 0, -1);
+  } else {
+    sched::Segment seg[2];
+    const int nseg = sched::split_segments(blk, n_qtiles, cut, seg);
+    segment(seg[0].qt, seg[0].t0, seg[0].t1, seg[0].role);
+    if (nseg > 1) {
+      // Every wave has left the first segment's LDS (its O rows may have gone
+      // out through the rings) before the second one's DMA writes them.
+      lds_barrier();
+      segment(seg[1].qt, seg[1].t0, seg[1].t1, seg[1].role);
+    }
   }
 }
 
@@ -2271,8 +2403,8 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
   // long and a short causal sweep.
   const int bh = blockIdx.x % bh_count;
   const int blk = (int)(blockIdx.x / bh_count);
-  const int first_half = n_ktiles - n_ktiles / 2;
-  const int kt = !zig || blk < first_half ? blk : n_ktiles - 1 - (blk - first_half);
+  static_assert(F::kSlots == sched::kDkvSwSlots, "the ring of the schedule");
+  const int kt = sched::key_block(blk, n_ktiles, zig);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
@@ -2433,7 +2565,7 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
     };
     // DMA share: odd half-steps the first half of tile (h + 5) / 2's
     // instructions, even half-steps the rest.
-    const int tdma = (h + 5) >> 1;
+    const int tdma = sched::dkv_sw_loaded(h);
     constexpr int QD0 = P ? 0 : kTileDma / 2;
     constexpr int NQ = P ? kTileDma / 2 : kTileDma - kTileDma / 2;
 
@@ -2573,8 +2705,8 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
   // Heaviest (first) key blocks first; zig as in attn_dkv_sw_kernel.
   const int bh = blockIdx.x % bh_count;
   const int blk = (int)(blockIdx.x / bh_count);
-  const int first_half = n_ktiles - n_ktiles / 2;
-  const int kt = !zig || blk < first_half ? blk : n_ktiles - 1 - (blk - first_half);
+  static_assert(F::kSlots == sched::kDkvRsSlots, "the ring of the schedule");
+  const int kt = sched::key_block(blk, n_ktiles, zig);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int pair = wave & 3, role = wave >> 2;
   const int lane = threadIdx.x & 63;
@@ -2632,7 +2764,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
   // The DMA of tile (h + 3) / 2 in odd half-steps: instruction f of the
   // wave's share in the f-th product slot of the DMA's place in the stage.
   auto dma_at = [&](int h, int f) {
-    if ((h & 1) && f < kTileDma) dma_part((h + 3) >> 1, f);
+    if ((h & 1) && f < kTileDma) dma_part(sched::dkv_rs_loaded(h), f);
   };
 
   // Full-width K (role A) or V (role B) rows come by row-coalesced DMA
@@ -2953,7 +3085,8 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
   const int bh = blockIdx.x % bh_count;
   const int blk = (int)(blockIdx.x / bh_count);
   const int half_q = n_qtiles / 2;
-  const int qt = !ZIG ? n_qtiles - 1 - blk : blk < n_qtiles - half_q ? n_qtiles - 1 - blk : blk - (n_qtiles - half_q);
+  const int qt = sched::query_tile(blk, n_qtiles, ZIG);
+  (void)half_q;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
@@ -3103,12 +3236,12 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
     static_assert(D == 64, "the split path ends in the direct stores");
     // This wave's half of every tile: S and dP, dS, then its dQ products.
     for (int t = 0; t < n; ++t) {
-      if (SLOTS == 3 && t + 1 < n)
+      if (sched::dq_in_flight(t, n, SLOTS, 1))
         wait_vmem<2 * F::kDma>();
       else
         wait_vmem<0>();
       lds_barrier();
-      if (t + SLOTS - 1 < n) issue_tile(t + SLOTS - 1);
+      if (sched::dq_loaded(t, SLOTS) < n) issue_tile(sched::dq_loaded(t, SLOTS));
       if (t >= n_w) continue;
       const char* sl = slot(t);
       const int kv0 = t * F::BK + 32 * kh;
@@ -3147,12 +3280,12 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
       // Tile t complete for this wave (with three slots tile t + 1 may be in
       // flight); after the barrier every wave has left tile t - 1's slot, which
       // tile t + SLOTS - 1 takes.
-      if (SLOTS == 3 && t + 1 < n)
+      if (sched::dq_in_flight(t, n, SLOTS, 1))
         wait_vmem<2 * F::kDma>();
       else
         wait_vmem<0>();
       lds_barrier();
-      if (t + SLOTS - 1 < n) issue_tile(t + SLOTS - 1);
+      if (sched::dq_loaded(t, SLOTS) < n) issue_tile(sched::dq_loaded(t, SLOTS));
       if (t >= n_w) continue;
       const char* sl = slot(t);
       const int kv0 = t * F::BK;
@@ -3229,18 +3362,39 @@ AttnViews dense_views(const Shape& s) {
   return AttnViews{vq, vk, vk, vq, vq, vq, vk, vk, (int)s.h};
 }
 
-template <int D, int RB = 1, int W = 8, bool ZIG = false, int KSPLIT = 1>
+// The split long-context forward (attn_fwd_sw_kernel with SPLIT): where it
+// applies and where the cut falls are sched::fwd_split_applies and
+// sched::fwd_split_cut, for bf16 causal self-attention with head dims <= 64
+// (the key-split kernel).
+bool fwd_split_applies(const Shape& s, int dtype, int causal, int cus) {
+  if (dtype != FERRITE_BF16 || !causal || s.sq != s.sk || s.d > 64 || s.d % 8 != 0) return false;
+  return sched::fwd_split_applies(s.b * s.h, s.sq, cus);
+}
+int fwd_split_cut(const Shape& s, int cus) { return sched::fwd_split_cut(s.b * s.h, s.sq, cus); }
+// Workspace bytes of the split forward, 0 where it does not apply: two partial
+// states per pair of tiles (128 x 64 f32 O, row max and row sum) and one count
+// per pair.
+int64_t fwd_split_bytes(const Shape& s, int dtype, int causal, int cus) {
+  typedef FwdW<64, 1, 8, 2> F;
+  if (!fwd_split_applies(s, dtype, causal, cus)) return 0;
+  const int64_t pairs = s.b * s.h * (s.sq / F::BQ / 2);
+  constexpr int64_t kPart = (4 * 2 * 16 * 64 + 2 * F::BQ) * 4;
+  return pairs * (2 * kPart + 4);
+}
+
+template <int D, int RB = 1, int W = 8, bool ZIG = false, int KSPLIT = 1, bool SPLIT = false>
 int fwd_sw_launch(const void* q, const void* k, const void* v, void* o, float* lse, const Shape& s, float c, int neg_q,
-                  hipStream_t stream, const AttnViews* views = nullptr) {
+                  hipStream_t stream, const AttnViews* views = nullptr, void* ws = nullptr) {
   typedef FwdW<D, RB, W, KSPLIT> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: grid too large");
-  auto kern = attn_fwd_sw_kernel<D, RB, W, ZIG, KSPLIT>;
+  auto kern = attn_fwd_sw_kernel<D, RB, W, ZIG, KSPLIT, SPLIT>;
   if (int rc = set_lds(kern, F::kLds, stream)) return rc;
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<bf16*>(o), lse, (int)bh,
-                     (int)s.sq, (int)s.d, c, neg_q, (int)nq, views ? *views : dense_views(s));
+                     (int)s.sq, (int)s.d, c, neg_q, (int)nq, views ? *views : dense_views(s), static_cast<char*>(ws),
+                     fwd_split_cut(s, cu_count(stream)));
   return check_launch("ferrite_flash_attention_fwd");
 }
 
@@ -3259,9 +3413,11 @@ int fwd_pp_launch(const void* q, const void* k, const void* v, void* o, float* l
   return check_launch("ferrite_flash_attention_fwd");
 }
 
+// ws / ws_bytes: the caller's workspace for the split long-context forward
+// (fwd_split_bytes), or nullptr.
 template <typename T, int D, bool AL>
 int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse, const Shape& s, int causal,
-               float scale, hipStream_t stream) {
+               float scale, hipStream_t stream, void* ws = nullptr, int64_t ws_bytes = 0) {
   typedef Fwd<T, D, AL> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
@@ -3286,8 +3442,15 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
         // (128 VGPRs, four waves per SIMD): the long tile that outlasts its
         // partner still runs two waves per SIMD (93.7 -> 84.7 us; 8x12x1024x64
         // 24.4 -> 23.5 us).
+        // With a workspace, a resident grid of an even number of 128-row tiles
+        // splits its long tiles between the two workgroups of a CU (the SPLIT
+        // kernel above): every workgroup then sweeps the same number of key tiles.
         typedef FwdW<64, 1, 8, 2> F4;
-        const bool one_round = cdiv(s.sq, F4::BQ) * s.b * s.h <= 2 * (int64_t)cu_count(stream);
+        const int cus = cu_count(stream);
+        const int64_t split = fwd_split_bytes(s, FERRITE_BF16, causal, cus);
+        if (split > 0 && ws && ws_bytes >= split && (reinterpret_cast<uintptr_t>(ws) & 255) == 0)
+          return fwd_sw_launch<D, 1, 8, true, 2, true>(q, k, v, o, lse, s, c, neg_q, stream, nullptr, ws);
+        const bool one_round = sched::resident(cdiv(s.sq, F4::BQ) * s.b * s.h, 2, cus);
         return one_round ? fwd_sw_launch<D, 1, 8, true, 2>(q, k, v, o, lse, s, c, neg_q, stream)
                          : fwd_sw_launch<D, 1, 8, false, 2>(q, k, v, o, lse, s, c, neg_q, stream);
       } else {
@@ -3334,7 +3497,7 @@ int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, 
     // 136 -> 122 us). Otherwise 4 waves each take whole tiles (the split
     // measured 10% slower at 8x12x1024x64).
     typedef DqPp<64, 8, 2, 2> F4;
-    const bool one_round = causal && cdiv(s.sq, F4::BQ) * s.b * s.h <= 2 * (int64_t)cu_count(stream);
+    const bool one_round = causal && sched::resident(cdiv(s.sq, F4::BQ) * s.b * s.h, 2, cu_count(stream));
     return one_round ? dq_pp_launch_t<D, 8, 2, true, 2>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw)
                      : dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
   } else {
@@ -3381,7 +3544,7 @@ int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout,
   } else {
     auto kern = vw.q.r == vw.dout.r ? attn_dkv_sw_kernel<D, true> : attn_dkv_sw_kernel<D, false>;
     if (int rc = set_lds(kern, F::kLds, stream)) return rc;
-    const int zig = causal && F::kMinBlocks == 2 && nk * bh <= 2 * (int64_t)cu_count(stream);
+    const int zig = causal && F::kMinBlocks == 2 && sched::resident(nk * bh, 2, cu_count(stream));
     hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                        static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
                        delta, static_cast<bf16*>(dk), static_cast<bf16*>(dv), (int)bh, (int)s.sq, (int)s.sk, (int)s.d,
@@ -3487,20 +3650,35 @@ int dkv_wide_launch(const void* q, const void* k, const void* v, const void* dou
 
 using namespace ferrite;
 
-extern "C" int ferrite_hip_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t b,
-                                    int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype, int causal, float scale,
-                                    void* stream) {
+extern "C" int64_t ferrite_hip_attn_fwd_workspace(int64_t b, int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype,
+                                                  int causal) {
+  if (b < 1 || h < 1 || sq < 1 || sk < 1 || d < 1) return -1;
+  // No stream here: sized for the current device's CU count.
+  return fwd_split_bytes(Shape{b, h, sq, sk, d}, dtype, causal, cu_count_of(-1));
+}
+
+extern "C" int ferrite_hip_attn_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse, int64_t b,
+                                       int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype, int causal,
+                                       float scale, void* workspace, int64_t workspace_bytes, void* stream) {
   const Shape s{b, h, sq, sk, d};
   if (int rc = check_shape("ferrite_hip_attn_fwd", s, dtype, causal, false)) return rc;
   if (!q || !k || !v || !o || !lse) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: null pointer");
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_fwd: workspace_bytes > 0 needs a workspace");
   const bool al = d % (dtype == FERRITE_BF16 ? 8 : 4) == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
                   aligned16(o);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (d > 256) FERRITE_WIDE(fwd_wide_launch, dtype, al, q, k, v, o, lse, s, causal, scale, st);
 #define FERRITE_DISPATCH_256(LAUNCH, T, aligned, ...) \
   return (aligned) ? LAUNCH<T, 256, true>(__VA_ARGS__) : LAUNCH<T, 256, false>(__VA_ARGS__)
-  FERRITE_DISPATCH(fwd_launch, s, dtype, al, q, k, v, o, lse, s, causal, scale, st);
+  FERRITE_DISPATCH(fwd_launch, s, dtype, al, q, k, v, o, lse, s, causal, scale, st, workspace, workspace_bytes);
 #undef FERRITE_DISPATCH_256
+}
+
+extern "C" int ferrite_hip_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t b,
+                                    int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype, int causal, float scale,
+                                    void* stream) {
+  return ferrite_hip_attn_fwd_ex(q, k, v, o, lse, b, h, sq, sk, d, dtype, causal, scale, nullptr, 0, stream);
 }
 
 extern "C" int ferrite_hip_attn_bwd_delta(const void* o, const void* dout, float* delta, int64_t b, int64_t h,
@@ -3583,7 +3761,7 @@ extern "C" int ferrite_hip_attn_fwd_qkv(const void* qkv, void* o, float* lse, in
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (d == 64) {
     typedef FwdW<64, 1, 8, 2> F4;
-    const bool one_round = cdiv(s, F4::BQ) * b * h <= 2 * (int64_t)cu_count(st);
+    const bool one_round = sched::resident(cdiv(s, F4::BQ) * b * h, 2, cu_count(st));
     return one_round ? fwd_sw_launch<64, 1, 8, true, 2>(q, k, v, o, lse, sh, c, neg_q, st, &vw)
                      : fwd_sw_launch<64, 1, 8, false, 2>(q, k, v, o, lse, sh, c, neg_q, st, &vw);
   }

@@ -1,0 +1,143 @@
+// Work decomposition and LDS ring schedules of the causal attention kernels.
+//
+// The kernels in attention.hip take every block -> tile mapping, every split of a
+// sweep and every "which tile goes into which ring slot at which step" decision
+// from here, and so does the host-side schedule checker
+// (tests/cpp/attn_schedule_test.cpp), which replays the launches over a sweep of
+// shapes on the CPU: every output row written exactly once, no ring slot
+// refilled while a wave may still read it, every tile landed (by the waits the
+// kernels issue) before its first read. Plain integer functions, usable from
+// host and device code.
+#pragma once
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#define FERRITE_SCHED __host__ __device__ constexpr
+#else
+#define FERRITE_SCHED constexpr
+#endif
+
+namespace ferrite {
+namespace sched {
+
+// ---- grids -----------------------------------------------------------------
+// A causal query-tile grid runs its heaviest (last) tiles first. zig (a grid
+// resident all at once, two workgroups per CU): the second half of the grid
+// takes the light tiles in rising order, so that block b and block b + grid / 2,
+// which the dispatcher places on one CU, pair a long and a short sweep.
+// blk = blockIdx / (B H); n = query tiles per head.
+FERRITE_SCHED int query_tile(int blk, int n, bool zig) {
+  return !zig || blk < n - n / 2 ? n - 1 - blk : blk - (n - n / 2);
+}
+
+// A causal key-block grid (dK/dV) runs its heaviest (first) blocks first; zig
+// as above, the second half in falling order from the last block.
+FERRITE_SCHED int key_block(int blk, int n, bool zig) {
+  return !zig || blk < n - n / 2 ? blk : n - 1 - (blk - (n - n / 2));
+}
+
+// ---- the split long-context forward ---------------------------------------
+// Key tiles [t0, t1) of query tile qt; role 0 / 1: block A's / B's share of a
+// split tile (partial state, merged by the later of the two), -1: a whole tile.
+struct Segment {
+  int qt, t0, t1, role;
+};
+constexpr int kWholeTile = 0x7fffffff;  // t1 of a segment that runs to the tile's diagonal
+
+// With 128-row query tiles (two 64-key tiles per query tile) and an even n,
+// the tiles L = n - 1 - p and p of pair p hold 2 (L + 1) + 2 (p + 1) = 2 (n + 1)
+// key tiles. Laid end to end (L's key tiles, then p's), they are cut after
+// `cut` key tiles (0 < cut < 2 (n + 1)): block A of the pair (blk < n / 2) takes
+// the tiles before the cut, block B (blk = p + n / 2) those after it. The tile
+// the cut falls in (L if cut < 2 (L + 1), else p) is shared: its lower keys
+// are A's (role 0), its upper keys B's (role 1). A cut at L's end shares none.
+// Returns the number of segments (1 or 2) written to seg.
+FERRITE_SCHED int split_segments(int blk, int n, int cut, Segment* seg) {
+  const int half = n / 2, pair = blk % half, L = n - 1 - pair, nl = 2 * (L + 1);
+  if (blk < half) {
+    if (cut < nl) {
+      seg[0] = Segment{L, 0, cut, 0};
+      return 1;
+    }
+    seg[0] = Segment{L, 0, kWholeTile, -1};
+    if (cut == nl) return 1;
+    seg[1] = Segment{pair, 0, cut - nl, 0};
+    return 2;
+  }
+  if (cut < nl) {
+    seg[0] = Segment{L, cut, kWholeTile, 1};
+    seg[1] = Segment{pair, 0, kWholeTile, -1};
+    return 2;
+  }
+  seg[0] = Segment{pair, cut - nl, kWholeTile, cut == nl ? -1 : 1};
+  return 1;
+}
+
+// Launch choices of the key-split forward (D <= 64, 128-row query tiles) for
+// B H = bh heads of S rows on a device of `cus` CUs. The split applies to a grid
+// resident all at once (bh nq <= 2 CUs) with an even number nq of tiles, where
+// it pays: with one workgroup per CU (bh nq <= CUs) from nq = 16 on, with two
+// from nq = 64 on (a shorter sweep gains less than the exchange of the shared
+// tile costs; the causal, bf16, S % 128 == 0 and head-dim conditions are the
+// caller's). With one workgroup per CU, A and B run at the same pace: equal
+// halves. Two workgroups on a CU do not share it evenly: the older one (A,
+// dispatched in the grid's first half) wins the issue ties and runs about 2.5
+// stages for each of the younger one's, so A takes 70% of the pair's key tiles.
+constexpr int kSplitRows = 128, kSplitMinTiles1 = 16, kSplitMinTiles2 = 64, kSplitOlderShare = 70;
+FERRITE_SCHED bool fwd_split_applies(long long bh, long long S, int cus) {
+  const long long nq = S / kSplitRows, grid = nq * bh;
+  return S % kSplitRows == 0 && nq % 2 == 0 && grid <= 2LL * cus &&
+         nq >= (grid <= cus ? kSplitMinTiles1 : kSplitMinTiles2);
+}
+FERRITE_SCHED int fwd_split_cut(long long bh, long long S, int cus) {
+  const long long nq = S / kSplitRows;
+  return nq * bh <= cus ? (int)nq + 1 : (int)((2 * (nq + 1) * kSplitOlderShare + 50) / 100);
+}
+// ZIG (query_tile, key_block) for a grid of `grid` workgroups that admits
+// `per_cu` workgroups per CU: when all of them are resident at once.
+FERRITE_SCHED bool resident(long long grid, int per_cu, int cus) { return grid <= (long long)per_cu * cus; }
+
+// ---- rings -------------------------------------------------------------------
+// Forward (attn_fwd_sw_kernel), three slots, tile t in slot t % 3. The prologue
+// loads K_0 and K_1; stage j (-1 .. n) loads K_{j+3} and V_{j+1} after its
+// barrier and reads K_{j+1} (S products) and V_{j-1} (P V products). Before
+// the barrier of stage j >= 0 a wave lets its previous stage's loads (2 kDma
+// instructions) stay in flight, before stage -1 its K_1 (kDma).
+constexpr int kFwdSlots = 3;
+FERRITE_SCHED int fwd_k_loaded(int j) { return j + 3; }
+FERRITE_SCHED int fwd_v_loaded(int j) { return j + 1; }
+FERRITE_SCHED int fwd_k_read(int j) { return j + 1; }
+FERRITE_SCHED int fwd_v_read(int j) { return j - 1; }
+FERRITE_SCHED int fwd_in_flight(int j, int kdma) { return j >= 0 ? 2 * kdma : kdma; }
+
+// dQ (attn_dq_pp_kernel), SLOTS = 2 or 3, tile t in slot t % SLOTS. The
+// prologue loads tiles 0 .. SLOTS - 2; after the barrier of step t the wave
+// loads tile t + SLOTS - 1 (if any) and reads tile t. Before that barrier a
+// wave lets tile t + 1 stay in flight (three slots) or nothing.
+FERRITE_SCHED int dq_loaded(int t, int slots) { return t + slots - 1; }
+FERRITE_SCHED int dq_in_flight(int t, int n, int slots, int ops_per_tile) {
+  return slots == 3 && t + 1 < n ? ops_per_tile : 0;
+}
+
+// dK/dV at D = 64 (attn_dkv_sw_kernel), four slots, query tile t in slot t % 4,
+// half-steps h = -1 .. 2 nt (two per 64-query tile). The prologue loads tiles 0
+// and 1; half-step h loads half of tile (h + 5) / 2's instructions (the first
+// half in odd half-steps) and reads tiles (h - 1) / 2 .. (h + 1) / 2
+// (arithmetic shifts). A barrier opens every odd half-step; before it a wave
+// lets one tile's instructions stay in flight.
+constexpr int kDkvSwSlots = 4;
+FERRITE_SCHED int dkv_sw_loaded(int h) { return (h + 5) >> 1; }
+FERRITE_SCHED int dkv_sw_first_read(int h) { return (h - 1) >> 1; }
+FERRITE_SCHED int dkv_sw_last_read(int h) { return (h + 1) >> 1; }
+
+// dK/dV at D = 128 (attn_dkv_rs_kernel), three slots, query tile t in slot
+// t % 3, half-steps h = -1 .. 2 nt. The prologue loads tile 0; odd half-step h
+// loads tile (h + 3) / 2, and tile t is read in half-steps 2 t - 1 .. 2 t + 2.
+// A barrier opens every half-step; before an odd one a wave waits for all its
+// loads.
+constexpr int kDkvRsSlots = 3;
+FERRITE_SCHED int dkv_rs_loaded(int h) { return (h & 1) ? (h + 3) >> 1 : -1; }
+FERRITE_SCHED int dkv_rs_first_read(int t) { return 2 * t - 1; }
+FERRITE_SCHED int dkv_rs_last_read(int t) { return 2 * t + 2; }
+
+}  // namespace sched
+}  // namespace ferrite

@@ -59,6 +59,26 @@ def _on_or_below_diag(qi: int, bq: int, ki: int, bk: int) -> bool:
 # --------------------------------------------------------------------------
 
 
+# Forward workspaces (the long-context split's partial states and per-pair counts), one per
+# (device, stream, size), zero-filled once: the kernel leaves the counts even, as it found them.
+# A workspace first needed inside a graph capture is allocated there (its zero fill is then part
+# of the graph) and not kept.
+_FWD_WORKSPACES: dict[tuple, torch.Tensor] = {}
+
+
+def _fwd_workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
+    if nbytes <= 0:
+        return None
+    stream = torch.cuda.current_stream(device)
+    key = (device, stream.cuda_stream, nbytes)
+    ws = _FWD_WORKSPACES.get(key)
+    if ws is None:
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        if not torch.cuda.is_current_stream_capturing():
+            _FWD_WORKSPACES[key] = ws
+    return ws
+
+
 def _flash_forward(q, k, v, *, causal: bool, scale: float, bs: BlockSizes | None = None):
     """O and the compact logsumexp. Reference: _flash_forward, flash_attention.py:130-175."""
     _hip.require_gpu(q, k, v)
@@ -67,9 +87,12 @@ def _flash_forward(q, k, v, *, causal: bool, scale: float, bs: BlockSizes | None
     sk = k.shape[2]
     out = torch.empty_like(q)
     lse = torch.empty((b, h, sq), dtype=torch.float32, device=q.device)
-    rc = _hip.lib().ferrite_hip_attn_fwd(
+    lib, dt = _hip.lib(), _hip.dtype_code(q.dtype)
+    ws = _fwd_workspace(lib.ferrite_hip_attn_fwd_workspace(b, h, sq, sk, d, dt, int(causal)), q.device)
+    rc = lib.ferrite_hip_attn_fwd_ex(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
-        b, h, sq, sk, d, _hip.dtype_code(q.dtype), int(causal), float(scale), _hip.stream_of(q),
+        b, h, sq, sk, d, dt, int(causal), float(scale),
+        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _hip.stream_of(q),
     )
     _hip.check(rc, "ferrite_flash_attention_fwd")
     return out, lse

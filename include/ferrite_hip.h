@@ -277,6 +277,31 @@ int ferrite_hip_adamw(int64_t n_tensors, void* const* params, const void* const*
 int ferrite_hip_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t b, int64_t h,
                          int64_t sq, int64_t sk, int64_t d, int dtype, int causal, float scale, void* stream);
 
+/*
+ * ferrite_hip_attn_fwd with a workspace (the same kernels and arguments, plus
+ * `workspace` of `workspace_bytes` device bytes, 256-byte aligned). Where
+ * ferrite_hip_attn_fwd_workspace returns a size above 0 and the workspace holds
+ * it (bf16 causal self-attention with head dim <= 64, S a multiple of 128 with
+ * an even number of 128-row tiles, B H S / 128 <= 2 x CUs: the long-context
+ * shapes whose grid is resident all at once, such as 1 x 8 x 8192 x 64), the
+ * longest query tiles' key sweeps are split between the two workgroups of a
+ * CU and their partial softmax states merged in a fixed order: lse agrees
+ * with the unsplit kernel to f32 rounding, O to the bf16 rounding of the
+ * probabilities (each share rounds p against its own running max), and a
+ * rerun gives the same bits. Otherwise (NULL workspace, too small, other
+ * shapes) it is
+ * ferrite_hip_attn_fwd. The workspace must be zero-filled before its first
+ * use; a call leaves it ready for the next one (per-pair counts stay even).
+ * Calls sharing one workspace must not overlap in time. The reference's
+ * pallas_call has no scratch (flash_attention.py:146-174); XLA FFI would hand
+ * this buffer over as the handler's scratch allocation.
+ */
+int64_t ferrite_hip_attn_fwd_workspace(int64_t b, int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype,
+                                       int causal);
+int ferrite_hip_attn_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse, int64_t b, int64_t h,
+                            int64_t sq, int64_t sk, int64_t d, int dtype, int causal, float scale, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
 /* delta[B, H, S] = sum_d f32(dO) * f32(O) (flash_attention.py:328). */
 int ferrite_hip_attn_bwd_delta(const void* o, const void* dout, float* delta, int64_t b, int64_t h, int64_t s,
                                int64_t d, int dtype, void* stream);

@@ -25,7 +25,7 @@ def _declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     declared = _declared_symbols()
-    assert len(declared) == 29
+    assert len(declared) == 31
     out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH], capture_output=True, text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s(\w+)", out))
     missing = [s for s in declared if s not in exported]
@@ -183,3 +183,28 @@ def test_stream_kernels_argument_checks():
     assert lib.ferrite_hip_stream_fill(None, 32, 1, 0, None) == 1
     assert "null" in _hip.last_error()
     assert lib.ferrite_hip_stream_fill(None, 0, 1, 0, None) == 0
+
+
+def test_forward_workspace_query():
+    """ferrite_hip_attn_fwd_workspace: the split long-context forward's workspace for the shapes it
+    takes (bf16, causal, d <= 64, an even number of 128-row tiles, a grid resident at once, at
+    least 16 tiles with one workgroup per CU or 64 with two), 0 for every other shape, -1 for
+    invalid ones; a positive size with no workspace is refused. (256 CUs: no device here.)"""
+    lib = _hip.lib()
+    bf, f32 = _hip.BF16, _hip.F32
+    per_pair = 2 * (8192 + 256) * 4 + 4
+    assert lib.ferrite_hip_attn_fwd_workspace(1, 8, 8192, 8192, 64, bf, 1) == 256 * per_pair
+    assert lib.ferrite_hip_attn_fwd_workspace(1, 1, 2048, 2048, 48, bf, 1) == 8 * per_pair
+    for args in [(1, 8, 8192, 8192, 128, bf, 1),   # the D = 128 kernel is not split
+                 (1, 1, 1792, 1792, 64, bf, 1),    # one workgroup per CU, fewer than 16 query tiles
+                 (4, 8, 4096, 4096, 64, bf, 1),    # two per CU, fewer than 64 query tiles
+                 (1, 8, 8192, 8192, 64, bf, 0),    # non-causal
+                 (1, 8, 8192, 8192, 64, f32, 1),   # f32
+                 (1, 8, 8192 - 64, 8192 - 64, 64, bf, 1),  # S not a multiple of 128
+                 (1, 1, 1152, 1152, 64, bf, 1),    # an odd number of tiles (9)
+                 (8, 12, 1024, 1024, 64, bf, 1),   # more tiles than resident workgroups (the GPT shape)
+                 (1, 8, 8192, 4096, 64, bf, 1)]:   # sq != sk
+        assert lib.ferrite_hip_attn_fwd_workspace(*args) == 0, args
+    assert lib.ferrite_hip_attn_fwd_workspace(0, 8, 8192, 8192, 64, bf, 1) == -1
+    rc = lib.ferrite_hip_attn_fwd_ex(1, 1, 1, 1, 1, 1, 8, 8192, 8192, 64, bf, 1, 0.125, None, 1024, None)
+    assert rc == 1 and "workspace" in _hip.last_error()

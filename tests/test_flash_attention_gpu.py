@@ -155,6 +155,61 @@ def test_long_context_config(dev):
     _check_config(dev, 1, 8, 8192, 64, seed=27)
 
 
+@pytest.mark.parametrize("b,h,s,d", [
+    (1, 2, 2048, 64),   # 32 workgroups, one per CU: the pair's key tiles cut in equal halves
+    (2, 2, 4096, 48),   # d < 64 (O leaves from registers), one workgroup per CU
+    (1, 6, 8192, 64),   # 384 workgroups, two on most CUs: the older block takes 70% of the pair's key
+                        # tiles, so the cut falls in the long tile for pairs 0-18 and in the short one
+                        # after that
+])
+def test_split_long_context_forward(dev, b, h, s, d):
+    """The split forward (ferrite_hip_attn_fwd_ex with its workspace: the key tiles of each pair of
+    query tiles cut between the pair's two workgroups, the tile the cut falls in merged by the later
+    one) on resident grids: O and lse against the oracle at the BASELINE bars (on the first head),
+    lse against the unsplit kernel to f32 rounding and O no less accurate than it; every output
+    written (NaN prefill); a second call on the same workspace gives the same bits, and the
+    per-pair counts are even after each call."""
+    lib = _hip.lib()
+    nbytes = lib.ferrite_hip_attn_fwd_workspace(b, h, s, s, d, _hip.BF16, 1)
+    pairs = b * h * (s // 128) // 2
+    assert nbytes == pairs * (2 * (8192 + 256) * 4 + 4)
+    q, k, v = _qkv(70 + d, (b, h, s, d), "bf16")
+    qt, kt, vt = (to_dev(a, "bf16", dev) for a in (q, k, v))
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    scale, st = d ** -0.5, _hip.stream_of(qt)
+    runs = []
+    for call in range(2):
+        o = torch.full_like(qt, float("nan"))
+        lse = torch.full((b, h, s), float("nan"), device=dev)
+        _hip.check(lib.ferrite_hip_attn_fwd_ex(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), o.data_ptr(),
+                                               lse.data_ptr(), b, h, s, s, d, _hip.BF16, 1, scale, ws.data_ptr(),
+                                               nbytes, st), "fwd_ex")
+        torch.cuda.synchronize()
+        counts = ws[-4 * pairs:].view(torch.int32).cpu().numpy()
+        assert np.all(counts == 2 * (call + 1)), counts[:8]
+        runs.append((to_np(o), to_np(lse)))
+    np.testing.assert_array_equal(runs[0][0], runs[1][0])
+    np.testing.assert_array_equal(runs[0][1], runs[1][1])
+    o_split, lse_split = runs[0]
+    assert not np.isnan(o_split).any() and not np.isnan(lse_split).any()
+    o_ref, lse_ref = oatt.forward(q[:1, :1], k[:1, :1], v[:1, :1], causal=True, dtype=np.float32)
+    assert max_abs(o_split[:1, :1], o_ref) <= 2e-2
+    assert max_abs(lse_split[:1, :1], lse_ref) <= 1e-3
+    o1 = torch.empty_like(qt)
+    lse1 = torch.empty((b, h, s), device=dev)
+    _hip.check(lib.ferrite_hip_attn_fwd(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), o1.data_ptr(), lse1.data_ptr(),
+                                        b, h, s, s, d, _hip.BF16, 1, scale, st), "fwd")
+    torch.cuda.synchronize()
+    # Against the unsplit kernel: the row sums are f32 sums of the same terms in another order, so
+    # lse agrees to f32 rounding. O does not agree bit for bit and cannot: each share rounds its p
+    # to bf16 for the P V product relative to its own running max (as the reference's blocked
+    # recipe does relative to its block order), so the two O differ by that rounding noise
+    # (~1e-4 here, against the 2e-2 bar). The split must not be less accurate: on the first head
+    # its error against the f32 oracle stays within 10% of the unsplit kernel's.
+    assert max_abs(lse_split, to_np(lse1)) <= 1e-5
+    assert rel_fro(o_split[:1, :1], o_ref) <= 1.1 * rel_fro(to_np(o1)[:1, :1], o_ref) + 1e-5
+
+
 @pytest.mark.parametrize("fused", [True, False], ids=["delta_in_dq", "delta_pass"])
 def test_gpt_attention_shape(dev, fused):
     """The GPT step's attention, B=8, H=12, T=1024, d=64: 768 dQ workgroups, more than fit at
