@@ -1854,17 +1854,10 @@ struct Wide {
   static constexpr int kDkvLds = 2 * kRowBytes + 2 * kTrBytes + 2 * BS * 4;
 };
 
-// Workgroup -> (head, tile, output slab): heads fastest, then tiles (the
-// heaviest causal tiles first where `heavy_last`), then slabs.
-struct WideCoord {
-  int bh, tile, slab;
-  __device__ WideCoord(int bh_count, int n_tiles, bool heavy_last) {
-    bh = blockIdx.x % bh_count;
-    const int rest = blockIdx.x / bh_count;
-    const int t = rest % n_tiles;
-    tile = heavy_last ? n_tiles - 1 - t : t;
-    slab = rest / n_tiles;
-  }
+// Workgroup -> (head, tile, output slab): sched::wide_coord.
+struct WideCoord : sched::WideCoord {
+  __device__ WideCoord(int bh_count, int n_tiles, bool heavy_last)
+      : sched::WideCoord(sched::wide_coord((int)blockIdx.x, bh_count, n_tiles, heavy_last)) {}
 };
 
 template <typename T, bool ALIGNED>

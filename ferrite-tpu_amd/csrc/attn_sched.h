@@ -35,6 +35,18 @@ FERRITE_SCHED int key_block(int blk, int n, bool zig) {
   return !zig || blk < n - n / 2 ? blk : n - 1 - (blk - (n - n / 2));
 }
 
+// Wide head dims (D a multiple of 128 above 128 or 256): grid = heads x tiles x
+// 128-column output slabs; block -> (head, tile, slab) with heads fastest, then
+// tiles (heaviest causal tiles first where heavy_last: the query tiles of the
+// forward and dQ; dK/dV's first key tiles are its heaviest), then slabs.
+struct WideCoord {
+  int bh, tile, slab;
+};
+FERRITE_SCHED WideCoord wide_coord(int block, int bh_count, int n_tiles, bool heavy_last) {
+  const int rest = block / bh_count, t = rest % n_tiles;
+  return WideCoord{block % bh_count, heavy_last ? n_tiles - 1 - t : t, rest / n_tiles};
+}
+
 // ---- the split long-context forward ---------------------------------------
 // Key tiles [t0, t1) of query tile qt; role 0 / 1: block A's / B's share of a
 // split tile (partial state, merged by the later of the two), -1: a whole tile.
