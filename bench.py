@@ -129,22 +129,34 @@ def bench_attention(b, h, t, d, steps, warmup, seed=7):
     lib, st, bf = _hip.lib(), _hip.stream_of(q), _hip.BF16
     P = [x.data_ptr() for x in (q, k, v, o, lse, delta, do, dq, dk, dv)]
     qp, kp, vp, op, lp, dp, dop, dqp, dkp, dvp = P
+    # The split kernels' exchange buffers (zero bytes where the long-context split does not
+    # apply), zero-filled once, as flash_attention() keeps them: one for the forward, one that
+    # the backward's dQ and dK/dV take turns with.
+    ws_bytes = int(lib.ferrite_hip_attn_fwd_workspace(b, h, t, t, d, bf, 1))
+    ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    wsp = ws.data_ptr() if ws_bytes > 0 else None
+    bws_bytes = int(lib.ferrite_hip_attn_bwd_workspace(b, h, t, t, d, bf, 1))
+    bws = torch.zeros(max(bws_bytes, 1), dtype=torch.uint8, device=dev)
+    bwa = (bws.data_ptr(), bws_bytes) if bws_bytes > 0 else (None, 0)
 
     def fwd():
-        _hip.check(lib.ferrite_hip_attn_fwd(qp, kp, vp, op, lp, b, h, t, t, d, bf, 1, scale, st), "fwd")
+        _hip.check(lib.ferrite_hip_attn_fwd_ex(qp, kp, vp, op, lp, b, h, t, t, d, bf, 1, scale, wsp, ws_bytes, st),
+                   "fwd")
 
     def dlt():
         _hip.check(lib.ferrite_hip_attn_bwd_delta(op, dop, dp, b, h, t, d, bf, st), "delta")
 
     def dkv():
-        _hip.check(lib.ferrite_hip_attn_bwd_dkv(qp, kp, vp, dop, lp, dp, dkp, dvp, b, h, t, t, d, bf, 1, scale, st), "dkv")
+        _hip.check(lib.ferrite_hip_attn_bwd_dkv_ex(qp, kp, vp, dop, lp, dp, dkp, dvp, b, h, t, t, d, bf, 1, scale,
+                                                   *bwa, st), "dkv")
 
     def dqk():
-        _hip.check(lib.ferrite_hip_attn_bwd_dq(qp, kp, vp, dop, lp, dp, dqp, b, h, t, t, d, bf, 1, scale, st), "dq")
+        _hip.check(lib.ferrite_hip_attn_bwd_dq_ex(qp, kp, vp, dop, lp, dp, dqp, b, h, t, t, d, bf, 1, scale, *bwa, st),
+                   "dq")
 
     def dq_delta():
-        _hip.check(lib.ferrite_hip_attn_bwd_dq_delta(qp, kp, vp, op, dop, lp, dp, dqp, b, h, t, t, d, bf, 1, scale, st),
-                   "dq_delta")
+        _hip.check(lib.ferrite_hip_attn_bwd_dq_delta_ex(qp, kp, vp, op, dop, lp, dp, dqp, b, h, t, t, d, bf, 1, scale,
+                                                        *bwa, st), "dq_delta")
 
     def bwd():  # the backward flash_attention runs: dQ computing delta, then dK/dV reading it
         dq_delta()
@@ -166,7 +178,7 @@ def bench_attention(b, h, t, d, steps, warmup, seed=7):
     f_fwd = attention_flops(b, h, t, t, d, causal=True)
     f_bwd = attention_flops(b, h, t, t, d, causal=True, backward=True)
     return {
-        "shape": [b, h, t, d],
+        "shape": [b, h, t, d], "fwd_key_split": ws_bytes > 0, "bwd_key_split": bws_bytes > 0,
         "fwd_us": t_fwd * 1e6, "fwd_tflops": f_fwd / t_fwd / 1e12,
         "delta_us": t_delta * 1e6, "dkv_us": t_dkv * 1e6, "dq_us": t_dq * 1e6, "dq_with_delta_us": t_dq_delta * 1e6,
         "bwd_split_us": t_bwd_split * 1e6,
@@ -176,6 +188,45 @@ def bench_attention(b, h, t, d, steps, warmup, seed=7):
         "bwd_frac_bf16_peak": f_bwd / t_bwd / 1e12 / PEAK_BF16_TFLOPS,
         "flops_fwd": f_fwd, "flops_bwd": f_bwd, "bytes_fwd": 4 * b * h * t * d * 2 + 4 * b * h * t,
     }
+
+
+def bench_attention_fwd_parts(steps, warmup, seed=11):
+    """The headline forward (causal 4x16x2048x128: 512 workgroups of 256 query rows, two rounds on
+    256 CUs) beside two workloads that take away one of its costs each, so the gap to peak splits
+    into parts measured by this file:
+      noncausal:  the same shape without the mask (the non-causal kernel, 128-row tiles, two
+                  workgroups per CU): every query tile sweeps all 32 key tiles, so there are no
+                  diagonal stages and all tiles are equally long (no tail of short sweeps);
+      one_round:  causal 2x16x2048x128: 256 workgroups, one per CU, all resident at once: no second
+                  round of workgroups, and the longest tile (32 key tiles) sets the time."""
+    import torch
+
+    from ferrite import _hip
+    from ferrite.kernels import attention_flops
+
+    dev = torch.device("cuda:0")
+    lib, bf = _hip.lib(), _hip.BF16
+    rows = {}
+    for name, (b, h, t, d, causal) in {"causal": (4, 16, 2048, 128, 1), "noncausal": (4, 16, 2048, 128, 0),
+                                       "one_round": (2, 16, 2048, 128, 1)}.items():
+        g = torch.Generator(device=dev).manual_seed(seed)
+        q, k, v = (torch.randn(b, h, t, d, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+        o, lse = torch.empty_like(q), torch.empty(b, h, t, device=dev)
+        st = _hip.stream_of(q)
+
+        def fwd(q=q, k=k, v=v, o=o, lse=lse, b=b, h=h, t=t, d=d, causal=causal, st=st):
+            _hip.check(lib.ferrite_hip_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                                lse.data_ptr(), b, h, t, t, d, bf, causal, d**-0.5, st), "fwd")
+
+        _settle(fwd, 0.1)
+        sec = _events_time(fwd, steps, warmup)
+        fl = attention_flops(b, h, t, t, d, causal=bool(causal))
+        rows[name] = {"shape": [b, h, t, d], "causal": bool(causal), "kernel": "attn_fwd_sw_kernel<128>" if causal
+                      else "attn_fwd_pp_kernel<128> (the non-causal forward)",
+                      "workgroups": b * h * (t // (256 if causal else 128)),
+                      "us": sec * 1e6, "tflops": fl / sec / 1e12, "frac_bf16_peak": fl / sec / 1e12 / PEAK_BF16_TFLOPS}
+        del q, k, v, o, lse
+    return rows
 
 
 def _rmsnorm_sets(rows, dim, sets, seed=0):
@@ -556,6 +607,7 @@ def main(argv=None):
     if a.only in ("attn", "all"):
         kernels["attention"] = bench_attention(4, 16, 2048, 128, a.steps, a.warmup)
         kernels["attention_long_context"] = bench_attention(1, 8, 8192, 64, max(a.steps // 2, 3), 2, seed=27)
+        kernels["attention_fwd_parts"] = bench_attention_fwd_parts(max(a.steps // 2, 5), 2)
     if a.only in ("rmsnorm", "all"):
         kernels["add_rmsnorm"] = bench_rmsnorm(4096, 1024, a.steps, a.warmup)
         ceil = bench_stream_ceilings()

@@ -947,6 +947,43 @@ __device__ __forceinline__ void pin(bf16x8& f) {
   f = __builtin_bit_cast(bf16x8, w);
 }
 
+// ---- the pair exchange of the split causal kernels --------------------------
+// Blocks A and B of a pair each leave their share of a shared tile in the
+// workspace; the second to arrive merges the two. The shares cross between
+// workgroups through device memory with agent-scope accesses (each store and
+// load goes past the caches a CU does not share), not through agent-scope
+// fences: a fence writes back or invalidates the whole L2 of its XCD, which
+// every other workgroup there then refills (a split forward ran 2.5x slower
+// with them). Pairs of floats, lane-contiguous: register pair r / 2 of a
+// wave's 64 lanes fills 512 consecutive bytes, whole cache lines.
+__device__ __forceinline__ void xput2(float* p, float x, float y) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, f32x2{x, y}), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x2 xget2(const float* p) {
+  return __builtin_bit_cast(f32x2, __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)),
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+// Offset (floats) of register pair r2 of accumulator tile `tile` (a wave's
+// f32x16 tiles numbered by the caller) in a share laid out as above.
+__device__ __forceinline__ int xat(int tile, int r2) { return (tile * 8 + r2) * 128 + 2 * (threadIdx.x & 63); }
+// Every wave's stores of its share have reached memory; then one count per
+// workgroup (the pair's count is even before a launch and each launch adds
+// two). True for the second of the pair to arrive, which merges; called by
+// every wave of the workgroup.
+__device__ __forceinline__ bool pair_arrive_second(int* count) {
+  __shared__ int arrival;
+  wait_vmem<0>();
+  lds_barrier();
+  if (threadIdx.x == 0) arrival = atomicAdd(count, 1);
+  lds_barrier();
+  return (arrival & 1) != 0;
+}
+
+// Workspace of the split backward kernels: one count per pair, rounded up to
+// 256 bytes, then the pairs' shares.
+__host__ __device__ constexpr int64_t split_counts_bytes(int64_t pairs) { return (pairs * 4 + 255) / 256 * 256; }
+
 // KSPLIT = 2: the waves form pairs on one SIMD (waves w and w + W / 2) that
 // take the same rows and split every 64-key tile, keys 0-31 and 32-63; the
 // pair merges its softmax states at the end.
@@ -1404,41 +1441,19 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
       float* const part = reinterpret_cast<float*>(ws + (int64_t)(2 * slot + role) * kPartBytes);
       float* const other = reinterpret_cast<float*>(ws + (int64_t)(2 * slot + 1 - role) * kPartBytes);
       int* const count = reinterpret_cast<int*>(ws + (int64_t)2 * bh_count * half_q * kPartBytes) + slot;
-      // The shares cross between workgroups through device memory with
-      // agent-scope accesses (each store and load goes past the caches a CU
-      // does not share), not through agent-scope fences: a fence writes back
-      // or invalidates the whole L2 of its XCD, which every other workgroup
-      // there then refills (the split ran 2.5x slower with them).
-      // Pairs of floats, lane-contiguous: register pair (u, r / 2) of the 64
-      // lanes fills 512 consecutive bytes, whole cache lines.
-      auto put2 = [](float* p, float x, float y) {
-        __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, f32x2{x, y}), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      };
-      auto get2 = [](const float* p) {
-        return __builtin_bit_cast(f32x2, __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)),
-                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      };
-      auto at = [&](int u, int r2) { return ((wr * DT + u) * 8 + r2) * 128 + 2 * lane; };
       if (writer) {
 #pragma unroll
         for (int u = 0; u < DT; ++u)
 #pragma unroll
-          for (int r2 = 0; r2 < 8; ++r2) put2(part + at(u, r2), acc[0][u][2 * r2], acc[0][u][2 * r2 + 1]);
-        if (g == 0) put2(part + kAccFloats + 2 * (32 * wr + l32), m[0], lrow[0]);
+          for (int r2 = 0; r2 < 8; ++r2) xput2(part + xat(wr * DT + u, r2), acc[0][u][2 * r2], acc[0][u][2 * r2 + 1]);
+        if (g == 0) xput2(part + kAccFloats + 2 * (32 * wr + l32), m[0], lrow[0]);
       }
-      __shared__ int arrival;
-      wait_vmem<0>();  // this wave's share has reached memory before the workgroup's count
-      lds_barrier();
-      if (threadIdx.x == 0) arrival = atomicAdd(count, 1);
-      lds_barrier();
-      // The first of A and B to arrive is done with the long tile (the count is
-      // even before a launch and each launch adds two per pair).
-      if ((arrival & 1) == 0) return;
+      // The first of A and B to arrive is done with the long tile.
+      if (!pair_arrive_second(count)) return;
       if (writer) {
         // Merge in role order whichever block runs it: A (keys before the
         // split), then B.
-        const f32x2 st = get2(other + kAccFloats + 2 * (32 * wr + l32));
+        const f32x2 st = xget2(other + kAccFloats + 2 * (32 * wr + l32));
         const float mo = st[0], lo = st[1];
         const float ma = role == 0 ? m[0] : mo, mb = role == 0 ? mo : m[0];
         const float la = role == 0 ? lrow[0] : lo, lb = role == 0 ? lo : lrow[0];
@@ -1448,7 +1463,7 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
         for (int u = 0; u < DT; ++u)
 #pragma unroll
           for (int r2 = 0; r2 < 8; ++r2) {
-            const f32x2 oo = get2(other + at(u, r2));
+            const f32x2 oo = xget2(other + xat(wr * DT + u, r2));
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
               const float mine = acc[0][u][2 * r2 + e];
@@ -2373,14 +2388,15 @@ __device__ __forceinline__ void stat_dma(const float* base, int r0, int nrows, c
 // t + 3 goes out during the two half-steps after the barrier that frees its
 // slot.
 // SAMEP: Q and dO share a row pitch (dense tensors), so one DMA descriptor serves both.
-template <int D, bool SAMEP = true>
+template <int D, bool SAMEP = true, bool SPLIT = false>
 __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                             const bf16* __restrict__ v, const bf16* __restrict__ dout,
                                                             const float* __restrict__ lse,
                                                             const float* __restrict__ delta, bf16* __restrict__ dk,
                                                             bf16* __restrict__ dv, int bh_count, int Sq, int Sk, int d,
                                                             int causal, float scale, float scale_log2, AttnViews vw,
-                                                            int n_ktiles, int zig) {
+                                                            int n_ktiles, int zig, char* __restrict__ ws,
+                                                            int cut) {
   typedef DkvPp<D> F;
   typedef typename F::Tile Tile;
   constexpr int KS = F::KS, DT = F::DT;
@@ -2397,13 +2413,9 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
   const int bh = blockIdx.x % bh_count;
   const int blk = (int)(blockIdx.x / bh_count);
   static_assert(F::kSlots == sched::kDkvSwSlots, "the ring of the schedule");
-  const int kt = sched::key_block(blk, n_ktiles, zig);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
-  const int k0 = kt * F::BKV;
-  const int k0w = k0 + 32 * wave;
-  const int kvrow = k0w + l32;
 
   // Row pitches (elements; d for dense tensors).
   const int ldq = (int)vw.q.r, lddo = (int)vw.dout.r;
@@ -2423,8 +2435,24 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
   // allocation of the pipeline from splitting over short cases (38 spilled
   // registers at D = 128 with separate short paths; at D = 64 the single path
   // is what fits two waves per SIMD).
-  const int first = causal ? k0 / F::BQ : 0;
-  const int nt = max((Sq + F::BQ - 1) / F::BQ - first, 3);
+  // Key block kt over query tiles t0 .. t1 - 1 of its causal sweep (t1 =
+  // sched::kWholeTile: to the end of the queries); role as in
+  // sched::Segment. Without SPLIT every block is one whole sweep.
+  auto segment = [&](int kt, int t0, int t1, int role) __attribute__((always_inline)) {
+  const int k0 = kt * F::BKV;
+  const int k0w = k0 + 32 * wave;
+  const int kvrow = k0w + l32;
+  int first, qlim;
+  if constexpr (SPLIT) {
+    // Causal self-attention with S % BKV == 0 (the host's conditions): rows
+    // at or past qlim, the segment's end, arrive as zeros like rows past Sq.
+    first = k0 / F::BQ + t0;
+    qlim = t1 == sched::kWholeTile ? Sq : (k0 / F::BQ + t1) * F::BQ;
+  } else {
+    first = causal ? k0 / F::BQ : 0;
+    qlim = Sq;
+  }
+  const int nt = max((qlim + F::BQ - 1) / F::BQ - first, 3);
   const int nh = 2 * nt;
 
   bf16x8 kf[KS], vf[KS];
@@ -2444,13 +2472,13 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
     char* sl = slot(t);
     const int r0 = (first + t) * F::BQ;
     if (qd < F::kDma)
-      dma.issue_one(qb, r0, Sq, ldq, sl, qd);
+      dma.issue_one(qb, r0, qlim, ldq, sl, qd);
     else if (qd < 2 * F::kDma)
-      (SAMEP ? dma : dma_do).issue_one(dob, r0, Sq, SAMEP ? ldq : lddo, sl + Tile::kBytes, qd - F::kDma);
+      (SAMEP ? dma : dma_do).issue_one(dob, r0, qlim, SAMEP ? ldq : lddo, sl + Tile::kBytes, qd - F::kDma);
     else if (qd == 2 * F::kDma)
-      stat_dma(lseb, r0, Sq, sl + 2 * Tile::kBytes);
+      stat_dma(lseb, r0, qlim, sl + 2 * Tile::kBytes);
     else
-      stat_dma(db, r0, Sq, sl + 2 * Tile::kBytes + 1024);
+      stat_dma(db, r0, qlim, sl + 2 * Tile::kBytes + 1024);
   };
   // Tiles 0 and 1 first; the two half-steps after barrier t load tile t + 3.
 #pragma unroll
@@ -2634,6 +2662,40 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
   stage(P0(), F_(), F_(), F_(), T_(), nh);
   wait_vmem<0>();
 
+  if constexpr (SPLIT) {
+    if (role >= 0) {
+      // This share of the long block: every wave's dK and dV partial sums into
+      // the pair's slot (counts first, then two shares per pair), then one
+      // count per workgroup; the second to arrive adds the other share (a
+      // sum, the same bits in either order) and stores.
+      const int half = n_ktiles / 2, slot_id = bh * half + blk % half;
+      constexpr int kShareFloats = F::kWaves * 2 * DT * 16 * 64;
+      float* const part = reinterpret_cast<float*>(ws + split_counts_bytes(bh_count * half)) +
+                          (int64_t)(2 * slot_id + role) * kShareFloats;
+      float* const other = part + (role == 0 ? kShareFloats : -kShareFloats);
+#pragma unroll
+      for (int u = 0; u < DT; ++u)
+#pragma unroll
+        for (int r2 = 0; r2 < 8; ++r2) {
+          xput2(part + xat((wave * 2 + 0) * DT + u, r2), dka[u][2 * r2], dka[u][2 * r2 + 1]);
+          xput2(part + xat((wave * 2 + 1) * DT + u, r2), dva[u][2 * r2], dva[u][2 * r2 + 1]);
+        }
+      if (!pair_arrive_second(reinterpret_cast<int*>(ws) + slot_id)) return;
+#pragma unroll
+      for (int u = 0; u < DT; ++u)
+#pragma unroll
+        for (int r2 = 0; r2 < 8; ++r2) {
+          const f32x2 ok = xget2(other + xat((wave * 2 + 0) * DT + u, r2));
+          const f32x2 ov = xget2(other + xat((wave * 2 + 1) * DT + u, r2));
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            dka[u][2 * r2 + e] += ok[e];
+            dva[u][2 * r2 + e] += ov[e];
+          }
+        }
+    }
+  }
+
   if (d == D) {
     // Whole-row stores through LDS (store_acc_rows_lds); the barrier keeps the
     // other waves' last reads and DMA off this wave's region of the ring.
@@ -2648,6 +2710,24 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
   if (k0w >= Sk) return;
   store_acc_rows<bf16, D, true>(dka, dk + vw.dk.at(bh, vw.heads), kvrow, Sk, d, scale, vw.dk.r);
   store_acc_rows<bf16, D, true>(dva, dv + vw.dv.at(bh, vw.heads), kvrow, Sk, d, 1.0f, vw.dv.r);
+  };
+
+  if constexpr (!SPLIT) {
+    segment(sched::key_block(blk, n_ktiles, zig), 0, sched::kWholeTile, -1);
+  } else {
+    // The pair's sequence of query tiles (sched::split_segments, in the
+    // forward's terms: its "long tile" n - 1 - p is key block p here, the
+    // block with the longer causal sweep).
+    sched::Segment seg[2];
+    const int nseg = sched::split_segments(blk, n_ktiles, cut, seg);
+    segment(n_ktiles - 1 - seg[0].qt, seg[0].t0, seg[0].t1, seg[0].role);
+    if (nseg > 1) {
+      // The first segment's stores went through LDS (a barrier before them,
+      // none after): every wave is past them before the ring refills.
+      lds_barrier();
+      segment(n_ktiles - 1 - seg[1].qt, seg[1].t0, seg[1].t1, seg[1].role);
+    }
+  }
 }
 
 // dK, dV at D = 128 with the work of each 32-key block split over the two
@@ -3060,7 +3140,7 @@ struct DqPp {
 // FUSED: delta is not read but computed here from O and dO (the rows' dO
 // fragments are loaded anyway) and written out for the dK/dV kernel, which
 // then runs after this one: the separate delta pass over O and dO goes away.
-template <int D, int W, int SLOTS, bool ZIG, bool FUSED = false, int KSPLIT = 1>
+template <int D, int W, int SLOTS, bool ZIG, bool FUSED = false, int KSPLIT = 1, bool SPLIT = false>
 __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                                 const bf16* __restrict__ v,
                                                                 const bf16* __restrict__ dout,
@@ -3069,7 +3149,7 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
                                                                 bf16* __restrict__ dq, int bh_count, int Sq, int Sk,
                                                                 int d, int causal, float scale, float scale_log2,
                                                                 int n_qtiles, const bf16* __restrict__ o,
-                                                                AttnViews vw) {
+                                                                AttnViews vw, char* __restrict__ ws, int cut) {
   typedef DqPp<D, W, SLOTS, KSPLIT> F;
   typedef typename F::Tile Tile;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -3077,12 +3157,14 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
   // Heaviest (last) query tiles first.
   const int bh = blockIdx.x % bh_count;
   const int blk = (int)(blockIdx.x / bh_count);
-  const int half_q = n_qtiles / 2;
-  const int qt = sched::query_tile(blk, n_qtiles, ZIG);
-  (void)half_q;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
+  static_assert(!SPLIT || (KSPLIT == 2 && D == 64), "the split runs the key-split kernel at D = 64");
+  // Query tile qt over key tiles t0 .. t1 - 1 of its causal sweep (t1 =
+  // sched::kWholeTile: to the diagonal); role as in sched::Segment. Without
+  // SPLIT every block is one whole sweep.
+  auto segment = [&](int qt, int t0, int t1, int role) __attribute__((always_inline)) {
   // 8 waves: SIMD w % 4 holds row blocks 2 (w % 4) and 2 (w % 4) + 1.
   const int q0 = qt * F::BQ;
   // With KSPLIT = 2, kh is the wave's half of every key tile.
@@ -3099,16 +3181,26 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
   const bf16* vb = v + vw.v.at(bh, vw.heads);
 
   const int q_last = min(q0 + F::BQ, Sq) - 1;
-  const int n = causal ? min(q_last, Sk - 1) / F::BK + 1 : (Sk + F::BK - 1) / F::BK;
   const bool wave_active = q0w < Sq;
-  const int n_w = !wave_active ? 0 : causal ? min(min(q0w + 31, Sq - 1), Sk - 1) / F::BK + 1 : n;
+  // n tiles in this sweep (or segment), the wave's first n_w of them up to
+  // its rows' diagonal; tile t of the sweep is key tile t0 + t.
+  int n, n_w;
+  if constexpr (SPLIT) {
+    // Causal self-attention with S % 128 == 0 (the host's conditions).
+    const int n_all = q_last / F::BK + 1;
+    n = (t1 == sched::kWholeTile ? n_all : t1) - t0;
+    n_w = min(max(min(q0w + 31, Sq - 1) / F::BK + 1 - t0, 0), n);
+  } else {
+    n = causal ? min(q_last, Sk - 1) / F::BK + 1 : (Sk + F::BK - 1) / F::BK;
+    n_w = !wave_active ? 0 : causal ? min(min(q0w + 31, Sq - 1), Sk - 1) / F::BK + 1 : n;
+  }
 
   const PpDma<Tile, true, W> dma(wave, ldk);
   auto slot = [&](int t) { return smem + (t % F::kSlots) * F::kSlotBytes; };
   auto issue_tile = [&](int t) {
     char* sl = slot(t);
-    dma.issue(kb, t * F::BK, Sk, ldk, sl);
-    dma.issue(vb, t * F::BK, Sk, ldk, sl + Tile::kBytes);
+    dma.issue(kb, (t0 + t) * F::BK, Sk, ldk, sl);
+    dma.issue(vb, (t0 + t) * F::BK, Sk, ldk, sl + Tile::kBytes);
   };
 
   bf16x8 qf[F::KS], dof[F::KS];
@@ -3128,7 +3220,8 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
 #pragma unroll
       for (int e = 0; e < 8; ++e) part = __builtin_fmaf((float)dof[kk][e], (float)of[kk][e], part);
     dl = lane32_sum(part);
-    if (qok && g == 0 && kh == 0) delta[(int64_t)bh * Sq + qrow] = dl;
+    // (Of a split tile, block A's share writes it; both compute the same.)
+    if (qok && g == 0 && kh == 0 && role != 1) delta[(int64_t)bh * Sq + qrow] = dl;
   } else {
     dl = qok ? delta[(int64_t)bh * Sq + qrow] : 0.f;
   }
@@ -3237,7 +3330,7 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
       if (sched::dq_loaded(t, SLOTS) < n) issue_tile(sched::dq_loaded(t, SLOTS));
       if (t >= n_w) continue;
       const char* sl = slot(t);
-      const int kv0 = t * F::BK + 32 * kh;
+      const int kv0 = (t0 + t) * F::BK + 32 * kh;
       sdp(sl, kh, s0, dp0, nop);
       if (causal && kv0 + 31 > q0w)
         grad_s(kv0, s0, dp0, dsf, std::true_type{});
@@ -3259,15 +3352,51 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
               f32x4{acc[u][4 * r4], acc[u][4 * r4 + 1], acc[u][4 * r4 + 2], acc[u][4 * r4 + 3]};
     }
     lds_barrier();
-    if (kh == 1) return;
+    if constexpr (!SPLIT) {
+      if (kh == 1) return;
+    }
+    if (kh == 0) {
 #pragma unroll
-    for (int u = 0; u < F::DT; ++u)
+      for (int u = 0; u < F::DT; ++u)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const f32x4 o1 = *reinterpret_cast<const f32x4*>(xs + ((u * 4 + r4) * 64 + lane) * 4);
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x4 o1 = *reinterpret_cast<const f32x4*>(xs + ((u * 4 + r4) * 64 + lane) * 4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[u][4 * r4 + e] += o1[e];
+          for (int e = 0; e < 4; ++e) acc[u][4 * r4 + e] += o1[e];
+        }
+    }
+    if constexpr (SPLIT) {
+      if (role >= 0) {
+        // This share of the long tile: the lower waves' dQ partial sums into
+        // the pair's slot (counts first, then two shares per pair), then one
+        // count per workgroup (every wave takes part); the second to arrive
+        // adds the other share (a sum, the same bits in either order).
+        const int half = n_qtiles / 2, slot_id = bh * half + blk % half;
+        constexpr int kShareFloats = (W / KSPLIT) * F::DT * 16 * 64;
+        float* const part = reinterpret_cast<float*>(ws + split_counts_bytes(bh_count * half)) +
+                            (int64_t)(2 * slot_id + role) * kShareFloats;
+        float* const other = part + (role == 0 ? kShareFloats : -kShareFloats);
+        const int wr = wave % (W / KSPLIT);
+        if (kh == 0) {
+#pragma unroll
+          for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+            for (int r2 = 0; r2 < 8; ++r2) xput2(part + xat(wr * F::DT + u, r2), acc[u][2 * r2], acc[u][2 * r2 + 1]);
+        }
+        if (!pair_arrive_second(reinterpret_cast<int*>(ws) + slot_id)) return;
+        if (kh == 0) {
+#pragma unroll
+          for (int u = 0; u < F::DT; ++u)
+#pragma unroll
+            for (int r2 = 0; r2 < 8; ++r2) {
+              const f32x2 oo = xget2(other + xat(wr * F::DT + u, r2));
+              acc[u][2 * r2] += oo[0];
+              acc[u][2 * r2 + 1] += oo[1];
+            }
+        }
       }
+      if (kh == 1) return;
+    }
   } else {
     for (int t = 0; t < n; ++t) {
       // Tile t complete for this wave (with three slots tile t + 1 may be in
@@ -3281,7 +3410,7 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
       if (sched::dq_loaded(t, SLOTS) < n) issue_tile(sched::dq_loaded(t, SLOTS));
       if (t >= n_w) continue;
       const char* sl = slot(t);
-      const int kv0 = t * F::BK;
+      const int kv0 = (t0 + t) * F::BK;
       const bool mask0 = causal && kv0 + 31 > q0w;
       const bool mask1 = causal && kv0 + 63 > q0w;
       sdp(sl, 0, s0, dp0, nop);
@@ -3311,6 +3440,21 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
   }
   if (!wave_active) return;
   store_acc_rows<bf16, D, true>(acc, dq + vw.dq.at(bh, vw.heads), qrow, Sq, d, scale, vw.dq.r);
+  };
+
+  if constexpr (!SPLIT) {
+    segment(sched::query_tile(blk, n_qtiles, ZIG), 0, sched::kWholeTile, -1);
+  } else {
+    sched::Segment seg[2];
+    const int nseg = sched::split_segments(blk, n_qtiles, cut, seg);
+    segment(seg[0].qt, seg[0].t0, seg[0].t1, seg[0].role);
+    if (nseg > 1) {
+      // The first segment's last LDS reads (the partials' merge through the
+      // ring) are done on every wave before the ring refills.
+      lds_barrier();
+      segment(seg[1].qt, seg[1].t0, seg[1].t1, seg[1].role);
+    }
+  }
 }
 
 // ===========================================================================
@@ -3373,6 +3517,35 @@ int64_t fwd_split_bytes(const Shape& s, int dtype, int causal, int cus) {
   const int64_t pairs = s.b * s.h * (s.sq / F::BQ / 2);
   constexpr int64_t kPart = (4 * 2 * 16 * 64 + 2 * F::BQ) * 4;
   return pairs * (2 * kPart + 4);
+}
+
+// Where the split dK/dV and dQ apply (sched::kDkvSplit, sched::kDqSplit): bf16
+// causal self-attention with head dims <= 64, the shapes of the key-split
+// long-context kernels.
+bool bwd_split_shape(const Shape& s, int dtype, int causal) {
+  return dtype == FERRITE_BF16 && causal && s.sq == s.sk && s.d <= 64 && s.d % 8 == 0;
+}
+bool dkv_split_applies(const Shape& s, int dtype, int causal, int cus) {
+  return bwd_split_shape(s, dtype, causal) && sched::split_applies(s.b * s.h, s.sq, cus, sched::kDkvSplit);
+}
+bool dq_split_applies(const Shape& s, int dtype, int causal, int cus) {
+  return bwd_split_shape(s, dtype, causal) && sched::split_applies(s.b * s.h, s.sq, cus, sched::kDqSplit);
+}
+// Workspace bytes of the split backward, 0 where neither kernel splits: one
+// count per pair of tiles (split_counts_bytes), then two shares per pair, each
+// a 128 x 64 f32 dK and dV (dK/dV) or a 128 x 64 f32 dQ (dQ). The two kernels
+// run one after the other on a stream and take turns with one workspace.
+int64_t bwd_split_bytes(const Shape& s, int dtype, int causal, int cus) {
+  const int64_t share = dkv_split_applies(s, dtype, causal, cus)  ? 2 * 128 * 64 * 4
+                        : dq_split_applies(s, dtype, causal, cus) ? 128 * 64 * 4
+                                                                  : 0;
+  if (share == 0) return 0;
+  const int64_t pairs = s.b * s.h * (s.sq / sched::kSplitRows / 2);
+  return split_counts_bytes(pairs) + 2 * pairs * share;
+}
+// A caller's workspace that holds `need` > 0 bytes at a 256-byte boundary.
+bool split_ws_ok(const void* ws, int64_t ws_bytes, int64_t need) {
+  return need > 0 && ws && ws_bytes >= need && (reinterpret_cast<uintptr_t>(ws) & 255) == 0;
 }
 
 template <int D, int RB = 1, int W = 8, bool ZIG = false, int KSPLIT = 1, bool SPLIT = false>
@@ -3459,27 +3632,31 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
 }
 
 // o == nullptr: read delta; otherwise compute it from o and dout and write it.
-template <int D, int W, int SLOTS, bool ZIG, int KSPLIT = 1>
+// SPLIT: the split kernel, with the workspace ws and the pairs' cut.
+template <int D, int W, int SLOTS, bool ZIG, int KSPLIT = 1, bool SPLIT = false>
 int dq_pp_launch_t(const void* q, const void* k, const void* v, const void* dout, const float* lse, float* delta,
                    void* dq, const Shape& s, int causal, float scale, hipStream_t stream, const void* o,
-                   const AttnViews& vw) {
+                   const AttnViews& vw, void* ws = nullptr, int cut = 0) {
   typedef DqPp<D, W, SLOTS, KSPLIT> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
   if (nq * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq: grid too large");
-  auto kern = o ? attn_dq_pp_kernel<D, W, SLOTS, ZIG, true, KSPLIT> : attn_dq_pp_kernel<D, W, SLOTS, ZIG, false, KSPLIT>;
+  auto kern = o ? attn_dq_pp_kernel<D, W, SLOTS, ZIG, true, KSPLIT, SPLIT>
+                : attn_dq_pp_kernel<D, W, SLOTS, ZIG, false, KSPLIT, SPLIT>;
   if (int rc = set_lds(kern, F::kLds, stream)) return rc;
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
                      delta, static_cast<bf16*>(dq), (int)bh, (int)s.sq, (int)s.sk, (int)s.d, causal, scale,
-                     scale * kLog2e, (int)nq, static_cast<const bf16*>(o), vw);
+                     scale * kLog2e, (int)nq, static_cast<const bf16*>(o), vw, static_cast<char*>(ws), cut);
   return check_launch("ferrite_flash_attention_bwd_dq");
 }
 
+// ws / ws_bytes: the caller's workspace for the split long-context dQ
+// (bwd_split_bytes), or nullptr.
 template <int D>
 int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, float* delta,
                  void* dq, const Shape& s, int causal, float scale, hipStream_t stream, const void* o = nullptr,
-                 const AttnViews* views = nullptr) {
+                 const AttnViews* views = nullptr, void* ws = nullptr, int64_t ws_bytes = 0) {
   const AttnViews vw = views ? *views : dense_views(s);
   if constexpr (D == 64) {
     // 128-query workgroups with two LDS slots (67 KB): two share a CU. A grid
@@ -3489,8 +3666,15 @@ int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, 
     // outlasts its partner still runs two waves per SIMD (1x8x8192x64:
     // 136 -> 122 us). Otherwise 4 waves each take whole tiles (the split
     // measured 10% slower at 8x12x1024x64).
+    // With a workspace, a resident grid of an even number of 128-row tiles
+    // splits its long tiles between the two workgroups of a CU, as the forward.
     typedef DqPp<64, 8, 2, 2> F4;
-    const bool one_round = causal && sched::resident(cdiv(s.sq, F4::BQ) * s.b * s.h, 2, cu_count(stream));
+    const int cus = cu_count(stream);
+    if (dq_split_applies(s, FERRITE_BF16, causal, cus) &&
+        split_ws_ok(ws, ws_bytes, bwd_split_bytes(s, FERRITE_BF16, causal, cus)))
+      return dq_pp_launch_t<D, 8, 2, true, 2, true>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw, ws,
+                                                    sched::split_cut(s.b * s.h, s.sq, cus, sched::kDqSplit));
+    const bool one_round = causal && sched::resident(cdiv(s.sq, F4::BQ) * s.b * s.h, 2, cus);
     return one_round ? dq_pp_launch_t<D, 8, 2, true, 2>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw)
                      : dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
   } else {
@@ -3500,9 +3684,11 @@ int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, 
 
 template <typename T, int D, bool AL>
 int dq_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
-              void* dq, const Shape& s, int causal, float scale, hipStream_t stream) {
+              void* dq, const Shape& s, int causal, float scale, hipStream_t stream, void* ws = nullptr,
+              int64_t ws_bytes = 0) {
   if constexpr (sizeof(T) == 2 && AL && D <= 128)
-    return dq_pp_launch<D>(q, k, v, dout, lse, const_cast<float*>(delta), dq, s, causal, scale, stream);
+    return dq_pp_launch<D>(q, k, v, dout, lse, const_cast<float*>(delta), dq, s, causal, scale, stream, nullptr,
+                           nullptr, ws, ws_bytes);
   typedef Dq<T, D, AL> F;
   const int64_t nq = cdiv(s.sq, F::BQ);
   const int64_t bh = s.b * s.h;
@@ -3518,7 +3704,7 @@ int dq_launch(const void* q, const void* k, const void* v, const void* dout, con
 template <int D>
 int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
                   void* dk, void* dv, const Shape& s, int causal, float scale, hipStream_t stream,
-                  const AttnViews* views = nullptr) {
+                  const AttnViews* views = nullptr, void* ws = nullptr, int64_t ws_bytes = 0) {
   typedef DkvPp<D> F;
   const int64_t nk = cdiv(s.sk, F::BKV);
   const int64_t bh = s.b * s.h;
@@ -3535,22 +3721,31 @@ int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout,
                        causal, scale, scale * kLog2e, vw, (int)nk, 0);
     return check_launch("ferrite_flash_attention_bwd_dkv");
   } else {
-    auto kern = vw.q.r == vw.dout.r ? attn_dkv_sw_kernel<D, true> : attn_dkv_sw_kernel<D, false>;
+    // With a workspace, a resident grid of an even number of 128-key blocks
+    // splits the long causal sweeps between the two workgroups of a CU, as the
+    // forward splits its long query tiles.
+    const int cus = cu_count(stream);
+    const bool split = dkv_split_applies(s, FERRITE_BF16, causal, cus) &&
+                       split_ws_ok(ws, ws_bytes, bwd_split_bytes(s, FERRITE_BF16, causal, cus));
+    auto kern = split ? (vw.q.r == vw.dout.r ? attn_dkv_sw_kernel<D, true, true> : attn_dkv_sw_kernel<D, false, true>)
+                      : (vw.q.r == vw.dout.r ? attn_dkv_sw_kernel<D, true> : attn_dkv_sw_kernel<D, false>);
     if (int rc = set_lds(kern, F::kLds, stream)) return rc;
-    const int zig = causal && F::kMinBlocks == 2 && sched::resident(nk * bh, 2, cu_count(stream));
+    const int zig = causal && F::kMinBlocks == 2 && sched::resident(nk * bh, 2, cus);
+    const int cut = split ? sched::split_cut(bh, s.sq, cus, sched::kDkvSplit) : 0;
     hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(F::kThreads), F::kLds, stream, static_cast<const bf16*>(q),
                        static_cast<const bf16*>(k), static_cast<const bf16*>(v), static_cast<const bf16*>(dout), lse,
                        delta, static_cast<bf16*>(dk), static_cast<bf16*>(dv), (int)bh, (int)s.sq, (int)s.sk, (int)s.d,
-                       causal, scale, scale * kLog2e, vw, (int)nk, zig);
+                       causal, scale, scale * kLog2e, vw, (int)nk, zig, split ? static_cast<char*>(ws) : nullptr, cut);
     return check_launch("ferrite_flash_attention_bwd_dkv");
   }
 }
 
 template <typename T, int D, bool AL>
 int dkv_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
-               void* dk, void* dv, const Shape& s, int causal, float scale, hipStream_t stream) {
+               void* dk, void* dv, const Shape& s, int causal, float scale, hipStream_t stream, void* ws = nullptr,
+               int64_t ws_bytes = 0) {
   if constexpr (sizeof(T) == 2 && AL && D <= 128)
-    return dkv_pp_launch<D>(q, k, v, dout, lse, delta, dk, dv, s, causal, scale, stream);
+    return dkv_pp_launch<D>(q, k, v, dout, lse, delta, dk, dv, s, causal, scale, stream, nullptr, ws, ws_bytes);
   typedef Dkv<T, D, AL> F;
   const int64_t nk = cdiv(s.sk, F::BKV);
   const int64_t bh = s.b * s.h;
@@ -3697,22 +3892,40 @@ extern "C" int ferrite_hip_attn_bwd_delta(const void* o, const void* dout, float
   return check_launch("ferrite_flash_attention_bwd_delta");
 }
 
-extern "C" int ferrite_hip_attn_bwd_dkv(const void* q, const void* k, const void* v, const void* dout,
-                                        const float* lse, const float* delta, void* dk, void* dv, int64_t b,
-                                        int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype, int causal,
-                                        float scale, void* stream) {
+extern "C" int64_t ferrite_hip_attn_bwd_workspace(int64_t b, int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype,
+                                                  int causal) {
+  if (b < 1 || h < 1 || sq < 1 || sk < 1 || d < 1) return -1;
+  // No stream here: sized for the current device's CU count.
+  return bwd_split_bytes(Shape{b, h, sq, sk, d}, dtype, causal, cu_count_of(-1));
+}
+
+extern "C" int ferrite_hip_attn_bwd_dkv_ex(const void* q, const void* k, const void* v, const void* dout,
+                                           const float* lse, const float* delta, void* dk, void* dv, int64_t b,
+                                           int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype, int causal,
+                                           float scale, void* workspace, int64_t workspace_bytes, void* stream) {
   const Shape s{b, h, sq, sk, d};
   if (int rc = check_shape("ferrite_hip_attn_bwd_dkv", s, dtype, causal, true)) return rc;
   if (!q || !k || !v || !dout || !lse || !delta || !dk || !dv)
     return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dkv: null pointer");
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dkv: workspace_bytes > 0 needs a workspace");
   const bool al = d % (dtype == FERRITE_BF16 ? 8 : 4) == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
                   aligned16(dout) && aligned16(dk) && aligned16(dv);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (d > 128) FERRITE_WIDE(dkv_wide_launch, dtype, al, q, k, v, dout, lse, delta, dk, dv, s, causal, scale, st);
 #define FERRITE_DISPATCH_256(LAUNCH, T, aligned, ...) \
   return fail(FERRITE_ERR_INVALID_ARGUMENT, "unreachable head_dim")
-  FERRITE_DISPATCH(dkv_launch, s, dtype, al, q, k, v, dout, lse, delta, dk, dv, s, causal, scale, st);
+  FERRITE_DISPATCH(dkv_launch, s, dtype, al, q, k, v, dout, lse, delta, dk, dv, s, causal, scale, st, workspace,
+                   workspace_bytes);
 #undef FERRITE_DISPATCH_256
+}
+
+extern "C" int ferrite_hip_attn_bwd_dkv(const void* q, const void* k, const void* v, const void* dout,
+                                        const float* lse, const float* delta, void* dk, void* dv, int64_t b,
+                                        int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype, int causal,
+                                        float scale, void* stream) {
+  return ferrite_hip_attn_bwd_dkv_ex(q, k, v, dout, lse, delta, dk, dv, b, h, sq, sk, d, dtype, causal, scale, nullptr,
+                                     0, stream);
 }
 
 namespace ferrite {
@@ -3785,41 +3998,70 @@ extern "C" int ferrite_hip_attn_bwd_qkv(const void* qkv, const void* o, const vo
                  : dkv_pp_launch<128>(q, k, v, dout, lse, delta, dk, dv, sh, 1, scale, st, &vw);
 }
 
-extern "C" int ferrite_hip_attn_bwd_dq_delta(const void* q, const void* k, const void* v, const void* o,
-                                             const void* dout, const float* lse, float* delta, void* dq, int64_t b,
-                                             int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype, int causal,
-                                             float scale, void* stream) {
+extern "C" int ferrite_hip_attn_bwd_dq_ex(const void* q, const void* k, const void* v, const void* dout,
+                                          const float* lse, const float* delta, void* dq, int64_t b, int64_t h,
+                                          int64_t sq, int64_t sk, int64_t d, int dtype, int causal, float scale,
+                                          void* workspace, int64_t workspace_bytes, void* stream);
+
+extern "C" int ferrite_hip_attn_bwd_dq_delta_ex(const void* q, const void* k, const void* v, const void* o,
+                                                const void* dout, const float* lse, float* delta, void* dq, int64_t b,
+                                                int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype, int causal,
+                                                float scale, void* workspace, int64_t workspace_bytes, void* stream) {
   const Shape s{b, h, sq, sk, d};
   if (int rc = check_shape("ferrite_hip_attn_bwd_dq_delta", s, dtype, causal, true)) return rc;
   if (!q || !k || !v || !o || !dout || !lse || !delta || !dq)
     return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq_delta: null pointer");
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq_delta: workspace_bytes > 0 needs a workspace");
   const bool al = d % (dtype == FERRITE_BF16 ? 8 : 4) == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
                   aligned16(o) && aligned16(dout) && aligned16(dq);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int dp = pad_dim(d);
   if (dtype == FERRITE_BF16 && al && dp <= 128) {
-    if (dp == 64) return dq_pp_launch<64>(q, k, v, dout, lse, delta, dq, s, causal, scale, st, o);
+    if (dp == 64)
+      return dq_pp_launch<64>(q, k, v, dout, lse, delta, dq, s, causal, scale, st, o, nullptr, workspace,
+                              workspace_bytes);
     return dq_pp_launch<128>(q, k, v, dout, lse, delta, dq, s, causal, scale, st, o);
   }
   // Other dtypes and head dims: the delta kernel, then dQ reading it.
   if (int rc = ferrite_hip_attn_bwd_delta(o, dout, delta, b, h, sq, d, dtype, stream)) return rc;
-  return ferrite_hip_attn_bwd_dq(q, k, v, dout, lse, delta, dq, b, h, sq, sk, d, dtype, causal, scale, stream);
+  return ferrite_hip_attn_bwd_dq_ex(q, k, v, dout, lse, delta, dq, b, h, sq, sk, d, dtype, causal, scale, workspace,
+                                    workspace_bytes, stream);
 }
 
-extern "C" int ferrite_hip_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout,
-                                       const float* lse, const float* delta, void* dq, int64_t b, int64_t h,
-                                       int64_t sq, int64_t sk, int64_t d, int dtype, int causal, float scale,
-                                       void* stream) {
+extern "C" int ferrite_hip_attn_bwd_dq_delta(const void* q, const void* k, const void* v, const void* o,
+                                             const void* dout, const float* lse, float* delta, void* dq, int64_t b,
+                                             int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype, int causal,
+                                             float scale, void* stream) {
+  return ferrite_hip_attn_bwd_dq_delta_ex(q, k, v, o, dout, lse, delta, dq, b, h, sq, sk, d, dtype, causal, scale,
+                                          nullptr, 0, stream);
+}
+
+extern "C" int ferrite_hip_attn_bwd_dq_ex(const void* q, const void* k, const void* v, const void* dout,
+                                          const float* lse, const float* delta, void* dq, int64_t b, int64_t h,
+                                          int64_t sq, int64_t sk, int64_t d, int dtype, int causal, float scale,
+                                          void* workspace, int64_t workspace_bytes, void* stream) {
   const Shape s{b, h, sq, sk, d};
   if (int rc = check_shape("ferrite_hip_attn_bwd_dq", s, dtype, causal, true)) return rc;
   if (!q || !k || !v || !dout || !lse || !delta || !dq)
     return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq: null pointer");
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dq: workspace_bytes > 0 needs a workspace");
   const bool al = d % (dtype == FERRITE_BF16 ? 8 : 4) == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
                   aligned16(dout) && aligned16(dq);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (d > 128) FERRITE_WIDE(dq_wide_launch, dtype, al, q, k, v, dout, lse, delta, dq, s, causal, scale, st);
 #define FERRITE_DISPATCH_256(LAUNCH, T, aligned, ...) \
   return fail(FERRITE_ERR_INVALID_ARGUMENT, "unreachable head_dim")
-  FERRITE_DISPATCH(dq_launch, s, dtype, al, q, k, v, dout, lse, delta, dq, s, causal, scale, st);
+  FERRITE_DISPATCH(dq_launch, s, dtype, al, q, k, v, dout, lse, delta, dq, s, causal, scale, st, workspace,
+                   workspace_bytes);
 #undef FERRITE_DISPATCH_256
+}
+
+extern "C" int ferrite_hip_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout,
+                                       const float* lse, const float* delta, void* dq, int64_t b, int64_t h,
+                                       int64_t sq, int64_t sk, int64_t d, int dtype, int causal, float scale,
+                                       void* stream) {
+  return ferrite_hip_attn_bwd_dq_ex(q, k, v, dout, lse, delta, dq, b, h, sq, sk, d, dtype, causal, scale, nullptr, 0,
+                                    stream);
 }

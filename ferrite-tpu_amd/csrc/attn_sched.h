@@ -16,6 +16,20 @@
 #define FERRITE_SCHED constexpr
 #endif
 
+// Share (percent) of a pair's tiles that the older workgroup takes in the split
+// dK/dV and dQ kernels when two share a CU, and the fewest 128-row tiles for
+// which they split then; compile-time settings so that other values can be
+// built and timed.
+#ifndef FERRITE_DKV_OLDER_SHARE
+#define FERRITE_DKV_OLDER_SHARE 62
+#endif
+#ifndef FERRITE_DQ_OLDER_SHARE
+#define FERRITE_DQ_OLDER_SHARE 62
+#endif
+#ifndef FERRITE_BWD_SPLIT_MIN_TWO
+#define FERRITE_BWD_SPLIT_MIN_TWO 64
+#endif
+
 namespace ferrite {
 namespace sched {
 
@@ -84,26 +98,38 @@ FERRITE_SCHED int split_segments(int blk, int n, int cut, Segment* seg) {
   return 1;
 }
 
-// Launch choices of the key-split forward (D <= 64, 128-row query tiles) for
-// B H = bh heads of S rows on a device of `cus` CUs. The split applies to a grid
-// resident all at once (bh nq <= 2 CUs) with an even number nq of tiles, where
-// it pays: with one workgroup per CU (bh nq <= CUs) from nq = 16 on, with two
-// from nq = 64 on (a shorter sweep gains less than the exchange of the shared
-// tile costs; the causal, bf16, S % 128 == 0 and head-dim conditions are the
+// Launch choices of the split kernels (128-row tiles) for B H = bh heads of S
+// rows on a device of `cus` CUs. A split applies to a grid resident all at
+// once (bh nq <= 2 CUs) with an even number nq of tiles, where it pays: with
+// one workgroup per CU (bh nq <= CUs) from min_one tiles on, with two from
+// min_two on (a shorter sweep gains less than the exchange of the shared tile
+// costs; the causal, bf16, S % 128 == 0 and head-dim conditions are the
 // caller's). With one workgroup per CU, A and B run at the same pace: equal
 // halves. Two workgroups on a CU do not share it evenly: the older one (A,
-// dispatched in the grid's first half) wins the issue ties and runs about 2.5
-// stages for each of the younger one's, so A takes 70% of the pair's key tiles.
-constexpr int kSplitRows = 128, kSplitMinTiles1 = 16, kSplitMinTiles2 = 64, kSplitOlderShare = 70;
-FERRITE_SCHED bool fwd_split_applies(long long bh, long long S, int cus) {
+// dispatched in the grid's first half) wins the issue ties, so A takes
+// older_share percent of the pair's tiles.
+struct SplitRule {
+  int min_one, min_two, older_share;
+};
+constexpr int kSplitRows = 128;
+// The forward: A runs about 2.5 stages for each of B's.
+constexpr SplitRule kFwdSplit{16, 64, 70};
+// dK/dV (key blocks sweeping query tiles) and dQ (query tiles sweeping key
+// tiles) at head dims <= 64: A takes 62% (1x8x8192x64 on MI355X, shares 55 /
+// 62 / 70 / 78: dK/dV 133.3 / 131.4 / 136.1 / 140.2 us against 157.1 unsplit,
+// dQ with delta 105.9 / 105.2 / 105.8 / 107.6 against 116.1).
+constexpr SplitRule kDkvSplit{16, FERRITE_BWD_SPLIT_MIN_TWO, FERRITE_DKV_OLDER_SHARE};
+constexpr SplitRule kDqSplit{16, FERRITE_BWD_SPLIT_MIN_TWO, FERRITE_DQ_OLDER_SHARE};
+FERRITE_SCHED bool split_applies(long long bh, long long S, int cus, SplitRule r) {
   const long long nq = S / kSplitRows, grid = nq * bh;
-  return S % kSplitRows == 0 && nq % 2 == 0 && grid <= 2LL * cus &&
-         nq >= (grid <= cus ? kSplitMinTiles1 : kSplitMinTiles2);
+  return S % kSplitRows == 0 && nq % 2 == 0 && grid <= 2LL * cus && nq >= (grid <= cus ? r.min_one : r.min_two);
 }
-FERRITE_SCHED int fwd_split_cut(long long bh, long long S, int cus) {
+FERRITE_SCHED int split_cut(long long bh, long long S, int cus, SplitRule r) {
   const long long nq = S / kSplitRows;
-  return nq * bh <= cus ? (int)nq + 1 : (int)((2 * (nq + 1) * kSplitOlderShare + 50) / 100);
+  return nq * bh <= cus ? (int)nq + 1 : (int)((2 * (nq + 1) * r.older_share + 50) / 100);
 }
+FERRITE_SCHED bool fwd_split_applies(long long bh, long long S, int cus) { return split_applies(bh, S, cus, kFwdSplit); }
+FERRITE_SCHED int fwd_split_cut(long long bh, long long S, int cus) { return split_cut(bh, S, cus, kFwdSplit); }
 // ZIG (query_tile, key_block) for a grid of `grid` workgroups that admits
 // `per_cu` workgroups per CU: when all of them are resident at once.
 FERRITE_SCHED bool resident(long long grid, int per_cu, int cus) { return grid <= (long long)per_cu * cus; }

@@ -78,6 +78,22 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f32, _vp, _c_i64, _vp],
     ),
     "ferrite_hip_attn_bwd_delta": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _vp]),
+    "ferrite_hip_attn_bwd_workspace": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int]),
+    "ferrite_hip_attn_bwd_dkv_ex": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f32, _vp,
+         _c_i64, _vp],
+    ),
+    "ferrite_hip_attn_bwd_dq_ex": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f32, _vp, _c_i64,
+         _vp],
+    ),
+    "ferrite_hip_attn_bwd_dq_delta_ex": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f32, _vp,
+         _c_i64, _vp],
+    ),
     "ferrite_hip_attn_bwd_dkv": (
         _c_int,
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_f32, _vp],

@@ -7,10 +7,13 @@ defaults and ValueError conditions; the custom VJP wiring of the reference
 flash_attention.py:315-333) is a torch.autograd.Function here.
 
 Kernels (csrc/attention.hip, through include/ferrite_hip.h):
-  forward   ferrite_hip_attn_fwd        -> O [B,H,S,D], lse f32 [B,H,S]
-  delta     ferrite_hip_attn_bwd_delta  -> rowsum(f32 dO * f32 O)
-  dK, dV    ferrite_hip_attn_bwd_dkv
-  dQ        ferrite_hip_attn_bwd_dq
+  forward   ferrite_hip_attn_fwd_ex       -> O [B,H,S,D], lse f32 [B,H,S]
+  delta     ferrite_hip_attn_bwd_delta    -> rowsum(f32 dO * f32 O)
+  dK, dV    ferrite_hip_attn_bwd_dkv_ex
+  dQ        ferrite_hip_attn_bwd_dq_ex (or _dq_delta_ex, computing delta)
+The _ex entry points take a workspace (sized by ferrite_hip_attn_fwd_workspace /
+_bwd_workspace, zero bytes where it is not used) in which the long-context kernels
+split their longest tiles between the two workgroups of a CU.
 lse and delta are compact [B,H,S] f32 rather than the reference's
 lane-replicated [B,H,S,128] (flash_attention.py:156-160, :329).
 
@@ -59,24 +62,29 @@ def _on_or_below_diag(qi: int, bq: int, ki: int, bk: int) -> bool:
 # --------------------------------------------------------------------------
 
 
-# Forward workspaces (the long-context split's partial states and per-pair counts), one per
-# (device, stream, size), zero-filled once: the kernel leaves the counts even, as it found them.
-# A workspace first needed inside a graph capture is allocated there (its zero fill is then part
-# of the graph) and not kept.
-_FWD_WORKSPACES: dict[tuple, torch.Tensor] = {}
+# Workspaces of the long-context split kernels (partial states and per-pair counts), one per
+# (pass, device, stream, size), zero-filled once: the kernels leave the counts even, as they found
+# them. The forward ("fwd") and the backward's dQ and dK/dV ("bwd", which take turns with one
+# buffer) keep separate ones. A workspace first needed inside a graph capture is allocated there
+# (its zero fill is then part of the graph) and not kept.
+_WORKSPACES: dict[tuple, torch.Tensor] = {}
 
 
-def _fwd_workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
+def _workspace(kind: str, nbytes: int, device: torch.device) -> torch.Tensor | None:
     if nbytes <= 0:
         return None
     stream = torch.cuda.current_stream(device)
-    key = (device, stream.cuda_stream, nbytes)
-    ws = _FWD_WORKSPACES.get(key)
+    key = (kind, device, stream.cuda_stream, nbytes)
+    ws = _WORKSPACES.get(key)
     if ws is None:
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
         if not torch.cuda.is_current_stream_capturing():
-            _FWD_WORKSPACES[key] = ws
+            _WORKSPACES[key] = ws
     return ws
+
+
+def _ws_args(ws: torch.Tensor | None) -> tuple:
+    return (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
 
 
 def _flash_forward(q, k, v, *, causal: bool, scale: float, bs: BlockSizes | None = None):
@@ -88,11 +96,10 @@ def _flash_forward(q, k, v, *, causal: bool, scale: float, bs: BlockSizes | None
     out = torch.empty_like(q)
     lse = torch.empty((b, h, sq), dtype=torch.float32, device=q.device)
     lib, dt = _hip.lib(), _hip.dtype_code(q.dtype)
-    ws = _fwd_workspace(lib.ferrite_hip_attn_fwd_workspace(b, h, sq, sk, d, dt, int(causal)), q.device)
+    ws = _workspace("fwd", lib.ferrite_hip_attn_fwd_workspace(b, h, sq, sk, d, dt, int(causal)), q.device)
     rc = lib.ferrite_hip_attn_fwd_ex(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
-        b, h, sq, sk, d, dt, int(causal), float(scale),
-        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _hip.stream_of(q),
+        b, h, sq, sk, d, dt, int(causal), float(scale), *_ws_args(ws), _hip.stream_of(q),
     )
     _hip.check(rc, "ferrite_flash_attention_fwd")
     return out, lse
@@ -124,14 +131,15 @@ def _flash_backward_fused(q, k, v, out, do, lse, *, causal: bool, scale: float):
     dv = torch.empty_like(v)
     delta = torch.empty((b, h, sq), dtype=torch.float32, device=q.device)
     lib = _hip.lib()
-    rc = lib.ferrite_hip_attn_bwd_dq_delta(
+    wsa = _ws_args(_workspace("bwd", lib.ferrite_hip_attn_bwd_workspace(b, h, sq, sk, d, dt, int(causal)), q.device))
+    rc = lib.ferrite_hip_attn_bwd_dq_delta_ex(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), do.data_ptr(), lse.data_ptr(), delta.data_ptr(),
-        dq.data_ptr(), b, h, sq, sk, d, dt, int(causal), float(scale), stream,
+        dq.data_ptr(), b, h, sq, sk, d, dt, int(causal), float(scale), *wsa, stream,
     )
     _hip.check(rc, "ferrite_flash_attention_bwd_dq")
-    rc = lib.ferrite_hip_attn_bwd_dkv(
+    rc = lib.ferrite_hip_attn_bwd_dkv_ex(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(), delta.data_ptr(),
-        dk.data_ptr(), dv.data_ptr(), b, h, sq, sk, d, dt, int(causal), float(scale), stream,
+        dk.data_ptr(), dv.data_ptr(), b, h, sq, sk, d, dt, int(causal), float(scale), *wsa, stream,
     )
     _hip.check(rc, "ferrite_flash_attention_bwd_dkv")
     return dq, dk, dv
@@ -150,14 +158,15 @@ def _flash_backward(q, k, v, do, lse, delta, *, causal: bool, scale: float, bs: 
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     lib = _hip.lib()
-    rc = lib.ferrite_hip_attn_bwd_dkv(
+    wsa = _ws_args(_workspace("bwd", lib.ferrite_hip_attn_bwd_workspace(b, h, sq, sk, d, dt, int(causal)), q.device))
+    rc = lib.ferrite_hip_attn_bwd_dkv_ex(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(), delta.data_ptr(),
-        dk.data_ptr(), dv.data_ptr(), b, h, sq, sk, d, dt, int(causal), float(scale), stream,
+        dk.data_ptr(), dv.data_ptr(), b, h, sq, sk, d, dt, int(causal), float(scale), *wsa, stream,
     )
     _hip.check(rc, "ferrite_flash_attention_bwd_dkv")
-    rc = lib.ferrite_hip_attn_bwd_dq(
+    rc = lib.ferrite_hip_attn_bwd_dq_ex(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(), delta.data_ptr(),
-        dq.data_ptr(), b, h, sq, sk, d, dt, int(causal), float(scale), stream,
+        dq.data_ptr(), b, h, sq, sk, d, dt, int(causal), float(scale), *wsa, stream,
     )
     _hip.check(rc, "ferrite_flash_attention_bwd_dq")
     return dq, dk, dv

@@ -26,6 +26,9 @@
  *   ferrite_hip_attn_bwd_dq   flash_attention.py:224-243, :281-306 ("ferrite_flash_attention_bwd_dq")
  *   ferrite_hip_attn_bwd_dq_delta  the same dQ with delta (flash_attention.py:328-329)
  *                                  computed inside it and written out for dK/dV
+ *   ferrite_hip_attn_fwd_ex, _bwd_dkv_ex, _bwd_dq_ex, _bwd_dq_delta_ex  the same with a
+ *                                  workspace, in which long-context grids split their
+ *                                  longest tiles between two workgroups
  *   ferrite_hip_attn_fwd_qkv / _bwd_qkv  the causal forward and backward read and
  *                                  written in the model's token-major layouts, with the
  *                                  head transposes of model/gpt.py:137-138 folded in
@@ -331,6 +334,39 @@ int ferrite_hip_attn_bwd_dq(const void* q, const void* k, const void* v, const v
 int ferrite_hip_attn_bwd_dq_delta(const void* q, const void* k, const void* v, const void* o, const void* dout,
                                   const float* lse, float* delta, void* dq, int64_t b, int64_t h, int64_t sq,
                                   int64_t sk, int64_t d, int dtype, int causal, float scale, void* stream);
+
+/*
+ * ferrite_hip_attn_bwd_dkv, _bwd_dq and _bwd_dq_delta with a workspace (the same
+ * kernels and arguments, plus `workspace` of `workspace_bytes` device bytes,
+ * 256-byte aligned; flash_attention.py:246-307 runs the reference's two backward
+ * kernels with no scratch). Where ferrite_hip_attn_bwd_workspace returns a size
+ * above 0 and the workspace holds it (the long-context shapes of
+ * ferrite_hip_attn_fwd_ex: bf16 causal self-attention, head dim <= 64, S a
+ * multiple of 128 with an even number of 128-row tiles, B H S / 128 <= 2 x CUs),
+ * each kernel splits its longest causal sweeps between the two workgroups of a
+ * CU: the dK/dV of a long key block, or the dQ of a long query tile, is summed
+ * from two partial sums (the same bits in either order, and on a rerun); it
+ * agrees with the unsplit kernel to the f32 rounding of the summation order.
+ * Otherwise (NULL workspace, too small, other shapes) each is the call without
+ * _ex. One workspace serves both backward kernels of a step, one after the
+ * other on a stream. It must be zero-filled before its first use; a call leaves
+ * it ready for the next one (per-pair counts stay even). Calls sharing one
+ * workspace must not overlap in time.
+ */
+int64_t ferrite_hip_attn_bwd_workspace(int64_t b, int64_t h, int64_t sq, int64_t sk, int64_t d, int dtype,
+                                       int causal);
+int ferrite_hip_attn_bwd_dkv_ex(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                                const float* delta, void* dk, void* dv, int64_t b, int64_t h, int64_t sq, int64_t sk,
+                                int64_t d, int dtype, int causal, float scale, void* workspace, int64_t workspace_bytes,
+                                void* stream);
+int ferrite_hip_attn_bwd_dq_ex(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                               const float* delta, void* dq, int64_t b, int64_t h, int64_t sq, int64_t sk, int64_t d,
+                               int dtype, int causal, float scale, void* workspace, int64_t workspace_bytes,
+                               void* stream);
+int ferrite_hip_attn_bwd_dq_delta_ex(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                                     const float* lse, float* delta, void* dq, int64_t b, int64_t h, int64_t sq,
+                                     int64_t sk, int64_t d, int dtype, int causal, float scale, void* workspace,
+                                     int64_t workspace_bytes, void* stream);
 
 /*
  * Causal flash attention on the model's token-major layouts (model/gpt.py:136-138:

@@ -9,16 +9,18 @@
 //                        long-context grid)
 //   attn_dq_pp_kernel    dQ (D = 128: 8 waves, 3 slots; D = 64: 4 waves and 2
 //                        slots, or 8 waves splitting every key tile on a
-//                        resident grid)
-//   attn_dkv_sw_kernel   dK/dV at D = 64 (4 waves, 4 slots, half-steps)
+//                        resident grid; the split long-context grid)
+//   attn_dkv_sw_kernel   dK/dV at D = 64 (4 waves, 4 slots, half-steps; the
+//                        split long-context grid)
 //   attn_dkv_rs_kernel   dK/dV at D = 128 (8 waves in two roles, 3 slots)
 //   attn_*_wide_kernel   head dims above 128 / 256 (the grid only: their LDS
 //                        staging is synchronous, between two barriers)
 //
 // and checked:
 //   * every output row (query rows for O and dQ, key rows for dK and dV) is
-//     written exactly once; with the split, every key tile of every query
-//     tile is swept exactly once, by shares that one merge combines;
+//     written exactly once; with a split, every key tile of every query tile
+//     (every query tile of every key block) is swept exactly once, by shares
+//     that one merge combines;
 //   * every LDS ring read finds the tile it expects, loaded at an earlier step
 //     and guaranteed complete by the wait counts each wave issues before the
 //     barrier of the reading step;
@@ -180,6 +182,33 @@ static void fwd_counts(const FwdCfg& c, int S, const Segment& sg, int wave, int&
   n_w = (kh == 1 && q0w % BK == 0 && sg.t0 == nwf - 1) ? 0 : std::max(std::min(nwf, tt1) - sg.t0, 0);
 }
 
+// The split's bookkeeping, per tile that a block sweeps (a query tile over key
+// tiles, or a key block over query tiles): the ranges [t0, t1) its segments
+// swept must cover [0, nfull(tile)) exactly once, and a shared tile must have
+// exactly one share of each role.
+typedef std::map<std::pair<int, int>, std::vector<std::pair<int, int>>> Swept;
+typedef std::map<std::pair<int, int>, int> Roles;
+template <typename NFull>
+static void check_sweeps(const std::string& name, const Swept& swept, const Roles& roles, NFull nfull_of) {
+  for (auto& kv : swept) {
+    const int tile = kv.first.second;
+    const int nfull = nfull_of(tile);
+    std::vector<int> hits(nfull, 0);
+    for (auto& r : kv.second)
+      for (int t = r.first; t < r.second; ++t)
+        if (t >= 0 && t < nfull) ++hits[t];
+    for (int t = 0; t < nfull; ++t)
+      if (hits[t] != 1) fail(name + ": tile " + std::to_string(tile) + " sub-tile " + std::to_string(t) + " swept " +
+                             std::to_string(hits[t]) + " times");
+  }
+  for (auto& kv : roles)
+    if (kv.second != 1) fail(name + ": more than one share of one role for tile " + std::to_string(kv.first.first));
+  std::map<int, int> shared;
+  for (auto& kv : roles) shared[kv.first.first] |= 1 << kv.first.second;
+  for (auto& kv : shared)
+    if (kv.second != 3) fail(name + ": tile " + std::to_string(kv.first) + " shared by one block only");
+}
+
 static void check_fwd(const FwdCfg& c, int bh, int S) {
   const int WR = c.W / c.ksplit, BQ = 32 * WR;
   const int nq = (S + BQ - 1) / BQ;
@@ -192,8 +221,8 @@ static void check_fwd(const FwdCfg& c, int bh, int S) {
   // With the split: every (head, query tile) gets its key tiles from shares
   // that together sweep [0, nfull) once, and exactly one share per shared tile
   // of each role.
-  std::map<std::pair<int, int>, std::vector<std::pair<int, int>>> swept;
-  std::map<std::pair<int, int>, int> roles;
+  Swept swept;
+  Roles roles;
   for (int blk = 0; blk < nq; ++blk) {
     Segment seg[2];
     int nseg = 1;
@@ -252,22 +281,7 @@ static void check_fwd(const FwdCfg& c, int bh, int S) {
     }
   }
   rows.expect_once(name + " O rows");
-  for (auto& kv : swept) {
-    const int qt = kv.first.second;
-    const int nfull = (std::min(qt * BQ + BQ, S) - 1) / BK + 1;
-    std::vector<int> hits(nfull, 0);
-    for (auto& r : kv.second)
-      for (int t = r.first; t < r.second; ++t) ++hits[t];
-    for (int t = 0; t < nfull; ++t)
-      if (hits[t] != 1) fail(name + ": query tile " + std::to_string(qt) + " key tile " + std::to_string(t) + " swept " +
-                             std::to_string(hits[t]) + " times");
-  }
-  for (auto& kv : roles)
-    if (kv.second != 1) fail(name + ": more than one share of one role for query tile " + std::to_string(kv.first.first));
-  std::map<int, int> shared;
-  for (auto& kv : roles) shared[kv.first.first] |= 1 << kv.first.second;
-  for (auto& kv : shared)
-    if (kv.second != 3) fail(name + ": query tile " + std::to_string(kv.first) + " shared by one block only");
+  check_sweeps(name, swept, roles, [&](int qt) { return (std::min(qt * BQ + BQ, S) - 1) / BK + 1; });
 }
 
 // ---------------------------------------------------------------------------
@@ -275,45 +289,66 @@ static void check_fwd(const FwdCfg& c, int bh, int S) {
 // ---------------------------------------------------------------------------
 struct DqCfg {
   int D, W, slots, ksplit;
-  bool zig;
+  bool zig, split;
 };
+
+// The dQ rows a segment writes: a whole tile's, or a shared tile's once (by the
+// second of its two blocks to arrive; counted here with role 0's share).
+static bool dq_writes(int kh, int role) { return g_mutation == 7 ? (kh == 0) : (kh == 0 && role <= 0); }
 
 static void check_dq(const DqCfg& c, int bh, int S) {
   const int BQ = 32 * c.W / c.ksplit;
   const int nq = (S + BQ - 1) / BQ;
   const int kdma = 16 / c.W;  // BwdTile: 16 blocks per tile, split over the waves
-  const std::string name = "dq D" + std::to_string(c.D) + " W" + std::to_string(c.W) + " bh" + std::to_string(bh) +
-                           " S" + std::to_string(S);
+  const int cut = c.split ? split_cut(bh, S, kCus, kDqSplit) : 0;
+  const std::string name = "dq D" + std::to_string(c.D) + " W" + std::to_string(c.W) + (c.split ? " split" : "") +
+                           " bh" + std::to_string(bh) + " S" + std::to_string(S);
   Coverage rows((long)bh * S);
+  Swept swept;
+  Roles roles;
   for (int blk = 0; blk < nq; ++blk) {
-    const int qt = query_tile(blk, nq, c.zig);
-    const int q0 = qt * BQ;
-    const int n = (std::min(q0 + BQ, S) - 1) / BK + 1;
-    {
-      Workgroup wg(c.W, name + " blk" + std::to_string(blk));
+    Segment seg[2];
+    int nseg = 1;
+    if (c.split)
+      nseg = split_segments(blk, nq, cut, seg);
+    else
+      seg[0] = Segment{query_tile(blk, nq, c.zig), 0, kWholeTile, -1};
+    Workgroup wg(c.W, name + " blk" + std::to_string(blk));
+    for (int sgi = 0; sgi < nseg; ++sgi) {
+      const Segment& sg = seg[sgi];
+      if (sgi > 0) wg.barrier_all(-1);  // the kernel's barrier between segments
+      const int q0 = sg.qt * BQ;
+      const int n_all = (std::min(q0 + BQ, S) - 1) / BK + 1;
+      // The kernel's segment(): n tiles (key tiles t0 .. t0 + n - 1), n_w per wave.
+      const int n = (sg.t1 == kWholeTile ? n_all : sg.t1) - sg.t0;
+      swept[{0, sg.qt}].push_back({sg.t0, sg.t0 + n});
+      if (sg.role >= 0) ++roles[{sg.qt, sg.role}];
+      const long base = 10000L * (sgi + 1);
       int n_w[8], q0w[8], kh[8];
       for (int w = 0; w < c.W; ++w) {
         kh[w] = c.ksplit == 1 ? 0 : w / (c.W / c.ksplit);
         q0w[w] = q0 + 32 * (c.ksplit > 1 ? w % (c.W / c.ksplit) : c.W == 8 ? 2 * (w & 3) + (w >> 2) : w);
-        n_w[w] = q0w[w] < S ? std::min(q0w[w] + 31, S - 1) / BK + 1 : 0;
+        const int nwf = q0w[w] < S ? std::min(q0w[w] + 31, S - 1) / BK + 1 : 0;
+        n_w[w] = std::min(std::max(nwf - sg.t0, 0), n);
       }
       for (int t = 0; t < c.slots - 1 && t < n; ++t)
-        for (int w = 0; w < c.W; ++w) wg.issue(w, {t % c.slots}, 1000 + t, 2 * kdma);
+        for (int w = 0; w < c.W; ++w) wg.issue(w, {t % c.slots}, base + 1000 + t, 2 * kdma);
       for (int t = 0; t < n; ++t) {
         wg.barrier_all(dq_in_flight(t, n, c.slots, 2 * kdma));
         for (int w = 0; w < c.W; ++w)
-          if (t < n_w[w]) wg.read(w, t % c.slots, 1000 + t);
+          if (t < n_w[w]) wg.read(w, t % c.slots, base + 1000 + t);
         if (dq_next(t, c.slots) < n)
           for (int w = 0; w < c.W; ++w)
-            wg.issue(w, {dq_next(t, c.slots) % c.slots}, 1000 + dq_next(t, c.slots), 2 * kdma);
+            wg.issue(w, {dq_next(t, c.slots) % c.slots}, base + 1000 + dq_next(t, c.slots), 2 * kdma);
       }
-      wg.check();
       for (int w = 0; w < c.W; ++w)
-        if (q0w[w] < S && kh[w] == 0)
+        if (q0w[w] < S && dq_writes(kh[w], sg.role))
           for (int hh = 0; hh < bh; ++hh) rows.add((long)hh * S + q0w[w], 32, (long)hh * S + S);
     }
+    wg.check();
   }
   rows.expect_once(name + " dQ rows");
+  check_sweeps(name, swept, roles, [&](int qt) { return (std::min(qt * BQ + BQ, S) - 1) / BK + 1; });
 }
 
 // ---------------------------------------------------------------------------
@@ -324,28 +359,46 @@ static void check_dq(const DqCfg& c, int bh, int S) {
 // and each wave's K/V row staging (20 + w), which overlaps slot 2 and the P
 // buffers.
 // ---------------------------------------------------------------------------
-static void check_dkv(int D, int bh, int S, bool zig) {
+static void check_dkv(int D, int bh, int S, bool zig, bool split = false) {
   const int BKV = 128, nk = (S + BKV - 1) / BKV;
   const bool rs = D == 128;
   const int W = rs ? 8 : 4, slots = rs ? kDkvRsSlots : kDkvSwSlots;
   const int kdma = (D == 64 ? 8 : 16) / W;     // Q (or dO) blocks per wave and tile
-  const std::string name = std::string(rs ? "dkv_rs" : "dkv_sw") + (zig ? " zig" : "") + " bh" + std::to_string(bh) +
-                           " S" + std::to_string(S);
+  const int cut = split ? split_cut(bh, S, kCus, kDkvSplit) : 0;
+  const std::string name = std::string(rs ? "dkv_rs" : "dkv_sw") + (split ? " split" : zig ? " zig" : "") + " bh" +
+                           std::to_string(bh) + " S" + std::to_string(S);
   Coverage krows((long)bh * S);
+  Swept swept;
+  Roles roles;
   for (int blk = 0; blk < nk; ++blk) {
-    const int kt = key_block(blk, nk, zig);
-    const int k0 = kt * BKV;
-    const int first = k0 / BK;
-    const int nt = std::max((S + BK - 1) / BK - first, 3);
-    const int nh = 2 * nt;
-    {
-      Workgroup wg(W, name + " blk" + std::to_string(blk));
+    Segment seg[2];
+    int nseg = 1;
+    if (split)
+      nseg = split_segments(blk, nk, cut, seg);
+    else
+      seg[0] = Segment{nk - 1 - key_block(blk, nk, zig), 0, kWholeTile, -1};
+    Workgroup wg(W, name + " blk" + std::to_string(blk));
+    for (int sgi = 0; sgi < nseg; ++sgi) {
+      const Segment& sg = seg[sgi];
+      if (sgi > 0) wg.barrier_all(-1);  // the kernel's barrier between segments
+      // The kernel's segment(): key block kt = nk - 1 - qt over query tiles
+      // first .. (the end of the queries, or the segment's end qlim).
+      const int kt = nk - 1 - sg.qt;
+      const int k0 = kt * BKV;
+      const int first = k0 / BK + sg.t0;
+      const int qlim = sg.t1 == kWholeTile ? S : (k0 / BK + sg.t1) * BK;
+      const int nt = std::max((qlim + BK - 1) / BK - first, 3);
+      const int nh = 2 * nt;
+      swept[{0, kt}].push_back({sg.t0, (qlim + BK - 1) / BK - k0 / BK});
+      if (sg.role >= 0) ++roles[{kt, sg.role}];
+      const long sbase = 10000L * (sgi + 1) - 1000;
+      {
       // Ops of one tile for wave w: Q and dO blocks, plus the statistics rows
       // (every wave in the one-role kernel; waves 0 and 4 in the role split).
       auto tile_ops = [&](int w) { return 2 * kdma + (rs ? ((w & 3) == 0 ? 1 : 0) : 2); };
       if (!rs) {
         for (int t = 0; t < 2; ++t)
-          for (int w = 0; w < W; ++w) wg.issue(w, {t % slots}, 1000 + t, tile_ops(w));
+          for (int w = 0; w < W; ++w) wg.issue(w, {t % slots}, sbase + 1000 + t, tile_ops(w));
         // Barriers before half-steps -1, 1, 3, ... (one tile's instructions may fly).
         for (int h = -1; h <= nh; ++h) {
           if (h & 1) {
@@ -354,14 +407,14 @@ static void check_dkv(int D, int bh, int S, bool zig) {
             wg.barrier(fl);
           }
           for (int w = 0; w < W; ++w) {
-            if (h <= nh - 2) wg.read(w, ((h + 1) >> 1) % slots, 1000 + ((h + 1) >> 1));  // S, dP of half h + 1
-            if (h >= 0 && h <= nh - 1) wg.read(w, (h >> 1) % slots, 1000 + (h >> 1));  // P, dS of half h
-            if (h >= 1) wg.read(w, ((h - 1) >> 1) % slots, 1000 + ((h - 1) >> 1));      // dV, dK of half h - 1
+            if (h <= nh - 2) wg.read(w, ((h + 1) >> 1) % slots, sbase + 1000 + ((h + 1) >> 1));  // S, dP of half h + 1
+            if (h >= 0 && h <= nh - 1) wg.read(w, (h >> 1) % slots, sbase + 1000 + (h >> 1));  // P, dS of half h
+            if (h >= 1) wg.read(w, ((h - 1) >> 1) % slots, sbase + 1000 + ((h - 1) >> 1));      // dV, dK of half h - 1
           }
           const int t = dkv_sw_loaded(h);
           for (int w = 0; w < W; ++w) {
             const int ops = tile_ops(w), firsthalf = ops / 2;
-            wg.issue(w, {t % slots}, 1000 + t, (h & 1) ? firsthalf : ops - firsthalf);
+            wg.issue(w, {t % slots}, sbase + 1000 + t, (h & 1) ? firsthalf : ops - firsthalf);
           }
         }
       } else {
@@ -372,35 +425,40 @@ static void check_dkv(int D, int bh, int S, bool zig) {
         const std::vector<int> staging[8] = {{2, 20}, {2, 21}, {2, 22}, {2, 23},
                                              {2, 11, 24}, {11, 25}, {11, 12, 26}, {12, 27}};
         for (int w = 0; w < W; ++w) {
-          wg.issue(w, {0}, 1000, tile_ops(w));
-          wg.issue(w, staging[w], 3000 + w, 8);  // 32 rows of 256 bytes, 1 KB per instruction
+          wg.issue(w, {0}, sbase + 1000, tile_ops(w));
+          wg.issue(w, staging[w], sbase + 3000 + w, 8);  // 32 rows of 256 bytes, 1 KB per instruction
         }
         for (int h = -1; h <= nh; ++h) {
           std::vector<int> fl(W, (h & 1) ? 0 : -1);
           wg.barrier(fl);
           if (h == -1)
-            for (int w = 0; w < W; ++w) wg.read(w, 20 + w, 3000 + w);  // the rows back, in stage -1
+            for (int w = 0; w < W; ++w) wg.read(w, 20 + w, sbase + 3000 + w);  // the rows back, in stage -1
           for (int w = 0; w < W; ++w) {
             for (int t = std::max((h - 1) >> 1, 0); t <= ((h + 1) >> 1) && t < nt; ++t)
-              if (dkv_rs_first_read(t) <= h && h <= dkv_rs_last_read(t) && h <= nh) wg.read(w, t % slots, 1000 + t);
+              if (dkv_rs_first_read(t) <= h && h <= dkv_rs_last_read(t) && h <= nh) wg.read(w, t % slots, sbase + 1000 + t);
             // P of half h - 1 from A (written in half-step h - 1), read by B in h.
-            if (w >= 4 && h >= 1) wg.read(w, 11 + ((h - 1) & 1), 5000 + h - 1);
+            if (w >= 4 && h >= 1) wg.read(w, 11 + ((h - 1) & 1), sbase + 5000 + h - 1);
           }
           const int t = rs_loaded(h);
           if (t >= 0)
-            for (int w = 0; w < W; ++w) wg.issue(w, {t % slots}, 1000 + t, tile_ops(w));
+            for (int w = 0; w < W; ++w) wg.issue(w, {t % slots}, sbase + 1000 + t, tile_ops(w));
           // A writes P of half h (ds_write, no VMEM count), modelled as an
           // instant fill of that buffer in this epoch.
           if (h >= 0 && h <= nh - 1)
-            for (int w = 0; w < 4; ++w) wg.issue(w, {11 + (h & 1)}, 5000 + h, 0);
+            for (int w = 0; w < 4; ++w) wg.issue(w, {11 + (h & 1)}, sbase + 5000 + h, 0);
         }
       }
-      wg.check();
-      for (int w = 0; w < (rs ? 4 : W); ++w)
-        for (int hh = 0; hh < bh; ++hh) krows.add((long)hh * S + k0 + 32 * w, 32, (long)hh * S + S);
+      }
+      // dK/dV rows: a whole sweep's, or a shared block's once (by the second
+      // of its two workgroups to arrive; counted with role 0's share).
+      if (sg.role <= 0 || g_mutation == 8)
+        for (int w = 0; w < (rs ? 4 : W); ++w)
+          for (int hh = 0; hh < bh; ++hh) krows.add((long)hh * S + k0 + 32 * w, 32, (long)hh * S + S);
     }
+    wg.check();
   }
   krows.expect_once(name + " dK/dV rows");
+  check_sweeps(name, swept, roles, [&](int kt) { return (S + BK - 1) / BK - kt * BKV / BK; });
 }
 
 // ---------------------------------------------------------------------------
@@ -445,11 +503,14 @@ int main() {
       check_fwd(FwdCfg{64, 8, 2, zig, false}, bh, S);
       if (fwd_split_applies(bh, S, kCus)) check_fwd(FwdCfg{64, 8, 2, true, true}, bh, S);
       // dQ (dq_pp_launch): D = 128 8 waves 3 slots; D = 64 resident: 8 waves, key split, zig; else 4 waves.
-      check_dq(DqCfg{128, 8, 3, 1, false}, bh, S);
+      check_dq(DqCfg{128, 8, 3, 1, false, false}, bh, S);
       if (resident((long long)((S + 127) / 128) * bh, 2, kCus))
-        check_dq(DqCfg{64, 8, 2, 2, true}, bh, S);
+        check_dq(DqCfg{64, 8, 2, 2, true, false}, bh, S);
       else
-        check_dq(DqCfg{64, 4, 2, 1, false}, bh, S);
+        check_dq(DqCfg{64, 4, 2, 1, false, false}, bh, S);
+      // The split dQ and dK/dV where they apply (with a workspace).
+      if (split_applies(bh, S, kCus, kDqSplit)) check_dq(DqCfg{64, 8, 2, 2, true, true}, bh, S), ++launches;
+      if (split_applies(bh, S, kCus, kDkvSplit)) check_dkv(64, bh, S, true, true), ++launches;
       // dK/dV (dkv_pp_launch): D = 64 zig on a resident grid; D = 128 the role split.
       check_dkv(64, bh, S, resident((long long)((S + 127) / 128) * bh, 2, kCus));
       check_dkv(128, bh, S, false);
@@ -459,7 +520,11 @@ int main() {
     for (int S : {1, 100, 128, 200, 1000})
       for (int D : {256, 384, 1024}) check_wide(bh, S, D);
   // The split at the shapes it was built for, and a cut in each place it can fall.
-  for (int bh : {5, 6, 8}) check_fwd(FwdCfg{64, 8, 2, true, true}, bh, 8192);
+  for (int bh : {5, 6, 8}) {
+    check_fwd(FwdCfg{64, 8, 2, true, true}, bh, 8192);
+    check_dq(DqCfg{64, 8, 2, 2, true, true}, bh, 8192);
+    check_dkv(64, bh, 8192, true, true);
+  }
   if (failures) {
     std::fprintf(stderr, "%d schedule check(s) failed\n", failures);
     return 1;
@@ -467,15 +532,19 @@ int main() {
   // Each planted mistake must be caught.
   const char* planted[] = {"", "K loaded a stage late", "V loaded into a slot in use", "waits too shallow",
                            "dQ tile loaded into a slot in use", "O rows written by both halves of a pair",
-                           "dK/dV tile loaded a half-step pair early"};
+                           "dK/dV tile loaded a half-step pair early", "split dQ rows written by both shares",
+                           "split dK/dV rows written by both shares"};
+  constexpr int kPlanted = 8;
   quiet = true;
-  for (int m = 1; m <= 6; ++m) {
+  for (int m = 1; m <= kPlanted; ++m) {
     g_mutation = m;
     const int before = failures;
     check_fwd(FwdCfg{128, 8, 1, false, false}, 2, 1024);
     check_fwd(FwdCfg{64, 8, 2, true, true}, 6, 8192);
-    check_dq(DqCfg{64, 4, 2, 1, false}, 3, 1024);
+    check_dq(DqCfg{64, 4, 2, 1, false, false}, 3, 1024);
+    check_dq(DqCfg{64, 8, 2, 2, true, true}, 6, 8192);
     check_dkv(128, 2, 1024, false);
+    check_dkv(64, 6, 8192, true, true);
     if (failures == before) {
       std::fprintf(stderr, "planted mistake %d (%s) not caught\n", m, planted[m]);
       return 1;
@@ -484,7 +553,7 @@ int main() {
   }
   g_mutation = 0;
   quiet = false;
-  std::printf("attention schedules: %d launch configurations replayed, all checks passed; 6 planted mistakes caught\n",
-              launches);
+  std::printf("attention schedules: %d launch configurations replayed, all checks passed; %d planted mistakes caught\n",
+              launches, kPlanted);
   return 0;
 }

@@ -25,7 +25,7 @@ def _declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     declared = _declared_symbols()
-    assert len(declared) == 31
+    assert len(declared) == 35
     out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH], capture_output=True, text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s(\w+)", out))
     missing = [s for s in declared if s not in exported]
@@ -207,4 +207,29 @@ def test_forward_workspace_query():
         assert lib.ferrite_hip_attn_fwd_workspace(*args) == 0, args
     assert lib.ferrite_hip_attn_fwd_workspace(0, 8, 8192, 8192, 64, bf, 1) == -1
     rc = lib.ferrite_hip_attn_fwd_ex(1, 1, 1, 1, 1, 1, 8, 8192, 8192, 64, bf, 1, 0.125, None, 1024, None)
+    assert rc == 1 and "workspace" in _hip.last_error()
+
+
+def test_backward_workspace_query():
+    """ferrite_hip_attn_bwd_workspace: the split dK/dV and dQ's shared workspace (one 4-byte count
+    per pair of 128-row tiles, rounded up to 256 bytes, then two 64 KiB dK+dV shares per pair) for
+    the same long-context shapes as the forward's, 0 elsewhere, -1 for invalid shapes; each _ex
+    entry point refuses a positive size with no workspace. (256 CUs: no device here.)"""
+    lib = _hip.lib()
+    bf, f32 = _hip.BF16, _hip.F32
+    assert lib.ferrite_hip_attn_bwd_workspace(1, 8, 8192, 8192, 64, bf, 1) == 1024 + 256 * 2 * 65536
+    assert lib.ferrite_hip_attn_bwd_workspace(1, 1, 2048, 2048, 48, bf, 1) == 256 + 8 * 2 * 65536
+    assert lib.ferrite_hip_attn_bwd_workspace(1, 4, 8192, 8192, 64, bf, 1) == 512 + 128 * 2 * 65536
+    for args in [(1, 8, 8192, 8192, 128, bf, 1), (1, 1, 1792, 1792, 64, bf, 1), (4, 8, 4096, 4096, 64, bf, 1),
+                 (1, 8, 8192, 8192, 64, bf, 0), (1, 8, 8192, 8192, 64, f32, 1), (1, 8, 8128, 8128, 64, bf, 1),
+                 (1, 1, 1152, 1152, 64, bf, 1), (8, 12, 1024, 1024, 64, bf, 1), (1, 8, 8192, 4096, 64, bf, 1),
+                 (2, 8, 8192, 8192, 64, bf, 1)]:  # 1024 tiles: not resident at once
+        assert lib.ferrite_hip_attn_bwd_workspace(*args) == 0, args
+    assert lib.ferrite_hip_attn_bwd_workspace(1, 0, 8192, 8192, 64, bf, 1) == -1
+    p = [1] * 8
+    rc = lib.ferrite_hip_attn_bwd_dkv_ex(*p, 1, 8, 8192, 8192, 64, bf, 1, 0.125, None, 1024, None)
+    assert rc == 1 and "workspace" in _hip.last_error()
+    rc = lib.ferrite_hip_attn_bwd_dq_ex(*p[:7], 1, 8, 8192, 8192, 64, bf, 1, 0.125, None, 1024, None)
+    assert rc == 1 and "workspace" in _hip.last_error()
+    rc = lib.ferrite_hip_attn_bwd_dq_delta_ex(*p, 1, 8, 8192, 8192, 64, bf, 1, 0.125, None, 1024, None)
     assert rc == 1 and "workspace" in _hip.last_error()

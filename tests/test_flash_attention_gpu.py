@@ -211,6 +211,71 @@ def test_split_long_context_forward(dev, b, h, s, d):
 
 
 @pytest.mark.parametrize("fused", [True, False], ids=["delta_in_dq", "delta_pass"])
+@pytest.mark.parametrize("b,h,s,d", [
+    (1, 2, 2048, 64),   # one workgroup per CU: equal halves
+    (2, 2, 4096, 48),   # d < 64 (dK/dV leave from registers, not through LDS), one workgroup per CU
+    (1, 6, 8192, 64),   # two workgroups on most CUs: the older block takes 70% of the pair's tiles
+])
+def test_split_long_context_backward(dev, b, h, s, d, fused):
+    """The split backward (ferrite_hip_attn_bwd_dq_ex / _dq_delta_ex and _dkv_ex sharing one
+    workspace: the causal sweeps of each pair of tiles cut between the pair's two workgroups, the
+    dQ or dK/dV of the tile the cut falls in summed from the two shares by the later one) on
+    resident grids, in both backward orders: every output written (NaN prefill); a second call on
+    the same workspace gives the same bits; the per-pair counts are even after each kernel; against
+    the unsplit kernels the gradients differ only by the f32 summation order; on the first head
+    they meet the BASELINE bar against the oracle and are no less accurate than the unsplit ones."""
+    lib = _hip.lib()
+    bf = _hip.BF16
+    nbytes = lib.ferrite_hip_attn_bwd_workspace(b, h, s, s, d, bf, 1)
+    pairs = b * h * (s // 128) // 2
+    assert nbytes == (pairs * 4 + 255) // 256 * 256 + pairs * 2 * 65536
+    q, k, v = _qkv(90 + d, (b, h, s, d), "bf16")
+    do = normal(93 + d, q.shape, "bf16")
+    qt, kt, vt, dot = (to_dev(a, "bf16", dev) for a in (q, k, v, do))
+    scale, st = d ** -0.5, _hip.stream_of(qt)
+    out, lse = _flash_forward(qt, kt, vt, causal=True, scale=scale)
+    delta_pass = _flash_delta(out, dot)
+    P = lambda t: t.data_ptr()  # noqa: E731
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+
+    def run(workspace):
+        wsa = (None, 0) if workspace is None else (P(workspace), nbytes)
+        dq, dk, dv = (torch.full_like(qt, float("nan")) for _ in range(3))
+        if fused:
+            delta = torch.full((b, h, s), float("nan"), device=dev)
+            _hip.check(lib.ferrite_hip_attn_bwd_dq_delta_ex(P(qt), P(kt), P(vt), P(out), P(dot), P(lse), P(delta), P(dq),
+                                                            b, h, s, s, d, bf, 1, scale, *wsa, st), "dq_delta_ex")
+        else:
+            delta = delta_pass
+        _hip.check(lib.ferrite_hip_attn_bwd_dkv_ex(P(qt), P(kt), P(vt), P(dot), P(lse), P(delta), P(dk), P(dv),
+                                                   b, h, s, s, d, bf, 1, scale, *wsa, st), "dkv_ex")
+        if not fused:
+            _hip.check(lib.ferrite_hip_attn_bwd_dq_ex(P(qt), P(kt), P(vt), P(dot), P(lse), P(delta), P(dq),
+                                                      b, h, s, s, d, bf, 1, scale, *wsa, st), "dq_ex")
+        torch.cuda.synchronize()
+        return [to_np(t) for t in (dq, dk, dv, delta)]
+
+    runs = []
+    for call in range(2):
+        runs.append(run(ws))
+        counts = ws[:4 * pairs].view(torch.int32).cpu().numpy()
+        assert np.all(counts == 4 * (call + 1)), counts[:8]  # two kernels, each adds 2 per pair
+    for a, c in zip(runs[0], runs[1]):
+        np.testing.assert_array_equal(a, c)
+    split = runs[0]
+    assert not any(np.isnan(a).any() for a in split)
+    whole = run(None)
+    np.testing.assert_array_equal(split[3], whole[3])  # delta: each row computed the same way
+    grads_ref = oatt.backward(q[:1, :1], k[:1, :1], v[:1, :1], do[:1, :1], causal=True, dtype=np.float32)
+    for name, a, w, r in zip(("dq", "dk", "dv"), split, whole, grads_ref):
+        # Summation order only: a split tile's sum is two f32 partial sums added, then rounded to
+        # bf16 like the whole sweep's; they differ by at most a few bf16 ulps of the largest entry.
+        assert max_abs(a, w) <= 2 ** -6 * max(np.abs(w).max(), 1.0), (name, max_abs(a, w))
+        assert max_abs(a[:1, :1], r) <= 2e-2, (name, max_abs(a[:1, :1], r))
+        assert rel_fro(a[:1, :1], r) <= 1.1 * rel_fro(w[:1, :1], r) + 1e-5, name
+
+
+@pytest.mark.parametrize("fused", [True, False], ids=["delta_in_dq", "delta_pass"])
 def test_gpt_attention_shape(dev, fused):
     """The GPT step's attention, B=8, H=12, T=1024, d=64: 768 dQ workgroups, more than fit at
     once, so dQ takes its heaviest-first order rather than the paired one. Not a BASELINE
