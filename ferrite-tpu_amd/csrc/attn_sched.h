@@ -27,7 +27,7 @@
 #define FERRITE_DQ_OLDER_SHARE 62
 #endif
 #ifndef FERRITE_BWD_SPLIT_MIN_TWO
-#define FERRITE_BWD_SPLIT_MIN_TWO 64
+#define FERRITE_BWD_SPLIT_MIN_TWO 32
 #endif
 
 namespace ferrite {
@@ -117,7 +117,9 @@ constexpr SplitRule kFwdSplit{16, 64, 70};
 // dK/dV (key blocks sweeping query tiles) and dQ (query tiles sweeping key
 // tiles) at head dims <= 64: A takes 62% (1x8x8192x64 on MI355X, shares 55 /
 // 62 / 70 / 78: dK/dV 133.3 / 131.4 / 136.1 / 140.2 us against 157.1 unsplit,
-// dQ with delta 105.9 / 105.2 / 105.8 / 107.6 against 116.1).
+// dQ with delta 105.9 / 105.2 / 105.8 / 107.6 against 116.1), and two
+// workgroups per CU split from 32 tiles on (1x16x4096x64: dK/dV 87.9 -> 79.4,
+// dQ 66.0 -> 63.5 us; 4x8x2048x64, 16 tiles: dQ 38.9 -> 41.3, dK/dV even).
 constexpr SplitRule kDkvSplit{16, FERRITE_BWD_SPLIT_MIN_TWO, FERRITE_DKV_OLDER_SHARE};
 constexpr SplitRule kDqSplit{16, FERRITE_BWD_SPLIT_MIN_TWO, FERRITE_DQ_OLDER_SHARE};
 FERRITE_SCHED bool split_applies(long long bh, long long S, int cus, SplitRule r) {

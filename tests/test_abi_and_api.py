@@ -213,15 +213,18 @@ def test_forward_workspace_query():
 def test_backward_workspace_query():
     """ferrite_hip_attn_bwd_workspace: the split dK/dV and dQ's shared workspace (one 4-byte count
     per pair of 128-row tiles, rounded up to 256 bytes, then two 64 KiB dK+dV shares per pair) for
-    the same long-context shapes as the forward's, 0 elsewhere, -1 for invalid shapes; each _ex
-    entry point refuses a positive size with no workspace. (256 CUs: no device here.)"""
+    the forward's long-context shapes and, with two workgroups per CU, from 32 tiles on (the
+    forward splits from 64), 0 elsewhere, -1 for invalid shapes; each _ex entry point refuses a
+    positive size with no workspace. (256 CUs: no device here.)"""
     lib = _hip.lib()
     bf, f32 = _hip.BF16, _hip.F32
     assert lib.ferrite_hip_attn_bwd_workspace(1, 8, 8192, 8192, 64, bf, 1) == 1024 + 256 * 2 * 65536
     assert lib.ferrite_hip_attn_bwd_workspace(1, 1, 2048, 2048, 48, bf, 1) == 256 + 8 * 2 * 65536
     assert lib.ferrite_hip_attn_bwd_workspace(1, 4, 8192, 8192, 64, bf, 1) == 512 + 128 * 2 * 65536
+    assert lib.ferrite_hip_attn_bwd_workspace(1, 16, 4096, 4096, 64, bf, 1) == 1024 + 256 * 2 * 65536  # 32 tiles, two per CU
     for args in [(1, 8, 8192, 8192, 128, bf, 1), (1, 1, 1792, 1792, 64, bf, 1), (4, 8, 4096, 4096, 64, bf, 1),
-                 (1, 8, 8192, 8192, 64, bf, 0), (1, 8, 8192, 8192, 64, f32, 1), (1, 8, 8128, 8128, 64, bf, 1),
+                 (4, 8, 2048, 2048, 64, bf, 1), (1, 8, 8192, 8192, 64, bf, 0), (1, 8, 8192, 8192, 64, f32, 1),
+                 (1, 8, 8128, 8128, 64, bf, 1),
                  (1, 1, 1152, 1152, 64, bf, 1), (8, 12, 1024, 1024, 64, bf, 1), (1, 8, 8192, 4096, 64, bf, 1),
                  (2, 8, 8192, 8192, 64, bf, 1)]:  # 1024 tiles: not resident at once
         assert lib.ferrite_hip_attn_bwd_workspace(*args) == 0, args

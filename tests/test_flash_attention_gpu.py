@@ -214,7 +214,8 @@ def test_split_long_context_forward(dev, b, h, s, d):
 @pytest.mark.parametrize("b,h,s,d", [
     (1, 2, 2048, 64),   # one workgroup per CU: equal halves
     (2, 2, 4096, 48),   # d < 64 (dK/dV leave from registers, not through LDS), one workgroup per CU
-    (1, 6, 8192, 64),   # two workgroups on most CUs: the older block takes 70% of the pair's tiles
+    (1, 6, 8192, 64),   # two workgroups on most CUs: the older block takes 62% of the pair's tiles
+    (1, 16, 4096, 64),  # two workgroups per CU on every CU, 32 tiles: the shortest split sweep
 ])
 def test_split_long_context_backward(dev, b, h, s, d, fused):
     """The split backward (ferrite_hip_attn_bwd_dq_ex / _dq_delta_ex and _dkv_ex sharing one
