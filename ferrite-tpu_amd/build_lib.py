@@ -48,8 +48,15 @@ HIPCC_FLAGS = [
 # attention kernel uses fewer VGPRs. Measured A/B on one MI355X (medians of 7 interleaved
 # rounds, outputs bitwise equal): forward 73.5 -> 73.2 us at 4x16x2048x128 and 91.0 -> 91.6 us
 # at 1x8x8192x64, dQ with delta 135.6 -> 133.0 us at 1x8x8192x64, the rest unchanged.
+#
+# attention.hip also raises the size up to which `#pragma unroll` unrolls a loop fully. The D = 256
+# forward's stage (48 fragment slots with their DMA and softmax shares) is past the default, and a
+# loop left partly rolled indexes the fragment and accumulator arrays at run time, which puts them
+# in scratch (2,304 bytes per lane); fully unrolled it keeps them in registers (no scratch). The
+# other kernels come out the same.
 SOURCE_FLAGS = {
-    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-structurizecfg-skip-uniform-regions=true"],
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-structurizecfg-skip-uniform-regions=true",
+                      "-mllvm", "-pragma-unroll-threshold=200000"],
 }
 
 

@@ -994,7 +994,8 @@ struct FwdW {
   static constexpr int KS = D / 16, DT = D / 32;
   typedef PpKTile<D> KT;
   typedef PpVTile<D> VT;
-  static constexpr int kSlots = 3;
+  // D = 256: a slot of 64-key K and V tiles takes 68 KB, so two slots.
+  static constexpr int kSlots = D > 128 ? 2 : 3;
   static constexpr int kLds = kSlots * (KT::kBytes + VT::kBytes);
   static constexpr int kDma = KT::kBlocks / kWaves;  // DMA instructions per tile and wave
   static constexpr int kAhead = 3;                   // fragments read ahead of their MFMAs
@@ -1011,7 +1012,7 @@ struct FwdW {
 // workspace `ws`; the second to get there (an atomic count per pair, kept even
 // between launches) merges the two in a fixed order and writes O and lse.
 template <int D, int RB, int W, bool ZIG, int KSPLIT = 1, bool SPLIT = false>
-__global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4 : W == 4 ? 2 : 1)) void attn_fwd_sw_kernel(
+__global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4 : W == 4 && D <= 128 ? 2 : 1)) void attn_fwd_sw_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, bf16* __restrict__ o,
     float* __restrict__ lse, int bh_count, int S, int d, float scale_log2, int neg_q, int n_qtiles, AttnViews vw,
     char* __restrict__ ws, int cut) {
@@ -1086,15 +1087,16 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   // every load instruction touches 32 rows (32 cache lines for 1 KB). Each
   // wave reads its own rows back after sync(-1).
   constexpr int kQRow = 2 * D;
-  static_assert(2 * KT::kBytes + F::kWaves * 32 * RB * kQRow <= F::kLds, "the Q rows fit the idle ring slots");
+  constexpr int kQStage = sched::fwd_prologue_k(F::kSlots) * KT::kBytes;  // past the prologue's K tiles
+  static_assert(kQStage + F::kWaves * 32 * RB * kQRow <= F::kLds, "the Q rows fit the idle ring slots");
   const bool q_lds = d == D;
-  char* const qst = smem + 2 * KT::kBytes + wave * (32 * RB * kQRow);
+  char* const qst = smem + kQStage + wave * (32 * RB * kQRow);
   kdma.issue(kb, 0, nkv, ldk, kring);
   if (q_lds) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) dma_rows32<D>(qb, q0w + 32 * rb, S, ldq, qst + rb * 32 * kQRow);
   }
-  kdma.issue(kb, F::BK, nkv, ldk, kring + KT::kBytes);
+  if constexpr (sched::fwd_prologue_k(F::kSlots) > 1) kdma.issue(kb, F::BK, nkv, ldk, kring + KT::kBytes);
 
   bf16x8 qf[RB][KS];
   if (!q_lds) {
@@ -1111,16 +1113,15 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   const int vbase = VT::off((lane >> 5) * 16 + ((lane & 15) >> 2), 2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
   // Diagonal tile: key kt*32 + g*16 + r of the tile is invisible to row
   // rb*32 + l32 of the wave when r > lim[rb][kt].
+  // With SPLIT, a wave whose last tile of the segment lies below its diagonal
+  // sees all of it: a uniform offset lifts every limit out of reach (nwf and
+  // tt1 are 0 without SPLIT).
+  const int lim_lift = SPLIT && nwf > tt1 ? 1 << 20 : 0;
   int lim[RB][2];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) lim[rb][kt] = q0w % F::BK + rb * 32 + l32 - kt * 32 - g * 16;
-  if (SPLIT && nwf > tt1) {  // (SPLIT only: nwf and tt1 are 0 otherwise)
-    // This wave's last tile of the segment lies below its diagonal: all of it is visible.
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) lim[rb][0] = lim[rb][1] = 1 << 20;
-  }
+    for (int kt = 0; kt < 2; ++kt) lim[rb][kt] = q0w % F::BK + rb * 32 + l32 - kt * 32 - g * 16 + lim_lift;
 
   f32x16 acc[RB][DT];  // O^T per row block: register r of tile u = dim u*32 + (r/4)*8 + g*4 + r%4
 #pragma unroll
@@ -1145,13 +1146,17 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   // share. Issued unconditionally: a tile past the end has an empty buffer
   // range, so its instructions read nothing and write zeros into a slot nobody
   // reads again.
-  static_assert(F::kSlots == sched::kFwdSlots, "the ring of the schedule");
   auto dma_part = [&](int j, int qd) {
-    const int tk = sched::fwd_k_loaded(j), tv = sched::fwd_v_loaded(j);
-    if (qd < F::kDma)
+    const int tk = sched::fwd_k_loaded(j, F::kSlots), tv = sched::fwd_v_loaded(j, F::kSlots);
+    if (qd < F::kDma) {
       kdma.issue_one(kb, tk * F::BK, nkv, ldk, kring + (tk % F::kSlots) * KT::kBytes, qd);
-    else
-      vdma.issue_one(vb, tv * F::BK, nkv, ldv, vring + (tv % F::kSlots) * VT::kBytes, qd - F::kDma);
+    } else {
+      // Two slots load no V at stage -1: tile 0 with an empty range, which
+      // reads nothing (a select, not a branch, in the fenced slots).
+      const bool vl = sched::fwd_v_loads(j, F::kSlots);
+      const int tvc = vl ? tv : 0;
+      vdma.issue_one(vb, tvc * F::BK, vl ? nkv : 0, ldv, vring + (tvc % F::kSlots) * VT::kBytes, qd - F::kDma);
+    }
   };
   auto dma = [&](int j) {
 #pragma unroll
@@ -1311,12 +1316,13 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   using P1 = std::integral_constant<int, 1>;
   // The workgroup passes stages j = -1 .. n; sync(j) opens stage j.
   auto sync = [&](int j) {
-    // This wave's parts of K_{j+1} and V_{j-1} have landed; the loads issued
-    // by stage j - 1 (or K_1 of the prologue) may still be in flight.
+    // This wave's parts of K_{j+1} and V_{j-1} have landed; with three slots
+    // the loads issued by stage j - 1 (or K_1 of the prologue) may still be in
+    // flight, with two none is.
     if (j >= 0)
-      wait_vmem<sched::fwd_in_flight(0, F::kDma)>();
+      wait_vmem<sched::fwd_in_flight(0, F::kDma, F::kSlots)>();
     else
-      wait_vmem<sched::fwd_in_flight(-1, F::kDma)>();
+      wait_vmem<sched::fwd_in_flight(-1, F::kDma, F::kSlots)>();
     // Every wave's parts have landed and every wave has left stage j - 1.
     lds_barrier();
   };
@@ -1325,7 +1331,7 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   sync(-1);
   if (q_lds) {
     // This wave's Q rows have landed (sync(-1) waited for them); the barrier
-    // keeps stage -1's DMA (K_2, V_0) off the staging until every wave has
+    // keeps stage -1's DMA (K_2 and V_0, or with two slots K_1) off the staging until every wave has
     // read its rows.
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -3624,6 +3630,12 @@ int fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse,
       }
     }
     return fwd_pp_launch<D>(q, k, v, o, lse, s, causal, c, neg_q, stream);
+  }
+  if constexpr (sizeof(T) == 2 && AL && D == 256) {
+    // 128-row workgroups of four waves, one per SIMD (an O accumulator of 256
+    // columns and the Q fragments of 32 rows take ~300 VGPRs), over a two-slot
+    // K/V ring (136 KB of LDS): one workgroup per CU.
+    if (causal && s.sq == s.sk && s.sq % 64 == 0) return fwd_sw_launch<256, 1, 4>(q, k, v, o, lse, s, c, neg_q, stream);
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)(nq * bh)), dim3(kThreads), F::kLds, stream, static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<const T*>(v), static_cast<T*>(o), lse, (int)bh, (int)s.sq,

@@ -137,17 +137,24 @@ FERRITE_SCHED int fwd_split_cut(long long bh, long long S, int cus) { return spl
 FERRITE_SCHED bool resident(long long grid, int per_cu, int cus) { return grid <= (long long)per_cu * cus; }
 
 // ---- rings -------------------------------------------------------------------
-// Forward (attn_fwd_sw_kernel), three slots, tile t in slot t % 3. The prologue
-// loads K_0 and K_1; stage j (-1 .. n) loads K_{j+3} and V_{j+1} after its
-// barrier and reads K_{j+1} (S products) and V_{j-1} (P V products). Before
-// the barrier of stage j >= 0 a wave lets its previous stage's loads (2 kDma
-// instructions) stay in flight, before stage -1 its K_1 (kDma).
+// Forward (attn_fwd_sw_kernel), SLOTS = 3 (D <= 128) or 2 (D = 256, whose
+// 64-key K and V tiles take 68 KB a slot), tile t in slot t % SLOTS. Stage j
+// (-1 .. n) reads K_{j+1} (S products) and V_{j-1} (P V products).
+// Three slots: the prologue loads K_0 and K_1; stage j loads K_{j+3} and
+// V_{j+1} after its barrier; before the barrier of stage j >= 0 a wave lets its
+// previous stage's loads (2 kDma instructions) stay in flight, before stage -1
+// its K_1 (kDma). Two slots: the prologue loads K_0; stage j loads K_{j+2} and
+// V_j (none at stage -1); a wave lets nothing stay in flight before a barrier.
 constexpr int kFwdSlots = 3;
-FERRITE_SCHED int fwd_k_loaded(int j) { return j + 3; }
-FERRITE_SCHED int fwd_v_loaded(int j) { return j + 1; }
+FERRITE_SCHED int fwd_k_loaded(int j, int slots = kFwdSlots) { return j + slots; }
+FERRITE_SCHED int fwd_v_loaded(int j, int slots = kFwdSlots) { return j + slots - 2; }
+FERRITE_SCHED bool fwd_v_loads(int j, int slots = kFwdSlots) { return fwd_v_loaded(j, slots) >= 0; }
 FERRITE_SCHED int fwd_k_read(int j) { return j + 1; }
 FERRITE_SCHED int fwd_v_read(int j) { return j - 1; }
-FERRITE_SCHED int fwd_in_flight(int j, int kdma) { return j >= 0 ? 2 * kdma : kdma; }
+FERRITE_SCHED int fwd_prologue_k(int slots = kFwdSlots) { return slots - 1; }  // K tiles the prologue loads
+FERRITE_SCHED int fwd_in_flight(int j, int kdma, int slots = kFwdSlots) {
+  return slots == 2 ? 0 : j >= 0 ? 2 * kdma : kdma;
+}
 
 // dQ (attn_dq_pp_kernel), SLOTS = 2 or 3, tile t in slot t % SLOTS. The
 // prologue loads tiles 0 .. SLOTS - 2; after the barrier of step t the wave

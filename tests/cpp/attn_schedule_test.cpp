@@ -151,18 +151,21 @@ constexpr int kCus = 256;
 // Planted mistakes, to show that the checks catch them (main runs each on a few
 // shapes and expects failures): 0 = the kernels' schedules.
 static int g_mutation = 0;
-static int k_loaded(int j) { return g_mutation == 1 ? j + 2 : fwd_k_loaded(j); }      // K one stage late
-static int v_loaded(int j) { return g_mutation == 2 ? j + 2 : fwd_v_loaded(j); }      // V into a slot in use
-static int fwd_wait(int j, int kdma) { return g_mutation == 3 ? 4 * kdma : fwd_in_flight(j, kdma); }
+static int k_loaded(int j, int slots) { return g_mutation == 1 ? j + slots - 1 : fwd_k_loaded(j, slots); }  // K a stage late
+static int v_loaded(int j, int slots) { return g_mutation == 2 ? j + slots - 1 : fwd_v_loaded(j, slots); }  // V into a slot in use
+static int fwd_wait(int j, int kdma, int slots) {
+  return g_mutation == 3 ? fwd_in_flight(j, kdma, slots) + kdma : fwd_in_flight(j, kdma, slots);  // waits too shallow
+}
 static int dq_next(int t, int slots) { return g_mutation == 4 ? t + slots : dq_loaded(t, slots); }
 static bool fwd_writes(int kh, int role) { return g_mutation == 5 ? role != 0 : kh == 0 && (role < 0 || role == 1); }
 static int rs_loaded(int h) { return g_mutation == 6 ? ((h & 1) ? (h + 5) >> 1 : -1) : dkv_rs_loaded(h); }
 constexpr int BK = 64;  // keys per tile of the forward and dQ rings, queries per tile of dK/dV's
 
 // ---------------------------------------------------------------------------
-// Forward: attn_fwd_sw_kernel. Regions 0-2: K slots, 3-5: V slots. Q rows
-// are staged in K slot 2 and the V slots (d == D) and read between sync(-1)
-// and a second barrier.
+// Forward: attn_fwd_sw_kernel. Regions 0 .. slots - 1: K slots, then the V
+// slots (three of each at D <= 128, two at D = 256). Q rows are staged in the
+// K slots past the prologue's tiles and in the V slots (d == D) and read
+// between sync(-1) and a second barrier.
 // ---------------------------------------------------------------------------
 struct FwdCfg {
   int D, W, ksplit;
@@ -212,7 +215,8 @@ static void check_sweeps(const std::string& name, const Swept& swept, const Role
 static void check_fwd(const FwdCfg& c, int bh, int S) {
   const int WR = c.W / c.ksplit, BQ = 32 * WR;
   const int nq = (S + BQ - 1) / BQ;
-  const int kdma = 16 / c.W;             // K (or V) blocks per wave and tile: 16 blocks of 1 KB
+  const int slots = c.D > 128 ? 2 : 3;   // FwdW::kSlots
+  const int kdma = c.D / 8 / c.W;        // K (or V) blocks per wave and tile: D / 8 blocks of 1 KB
   const int qdma = 32 * 2 * c.D / 1024;  // this wave's 32 Q rows, 1 KB per instruction
   const int cut = c.split ? fwd_split_cut(bh, S, kCus) : 0;
   const std::string name = "fwd D" + std::to_string(c.D) + (c.split ? " split" : c.zig ? " zig" : "") + " bh" +
@@ -246,30 +250,45 @@ static void check_fwd(const FwdCfg& c, int bh, int S) {
         }
         // Labels: K tile t -> 1000 + t, V tile t -> 2000 + t, Q -> 3000 (per segment).
         const long base = 10000L * (sgi + 1);
-        auto kslot = [](int t) { return t % kFwdSlots; };
-        auto vslot = [](int t) { return 3 + t % kFwdSlots; };
-        // Prologue: K_0, this wave's Q rows, K_1.
+        auto kslot = [&](int t) { return t % slots; };
+        auto vslot = [&](int t) { return slots + t % slots; };
+        // Prologue: K_0, this wave's Q rows, and with three slots K_1. The Q
+        // rows take K slot 2 and the V slots (three slots), or K slot 1 and the
+        // V slots (two: 16 KB a wave from K slot 1's start, wave 2 across
+        // into V slot 0).
+        const std::vector<int> qst = slots == 3 ? std::vector<int>{2, 3, 4, 5} : std::vector<int>{1, 2, 3};
         for (int w = 0; w < c.W; ++w) {
           wg.issue(w, {kslot(0)}, base + 1000, kdma);
-          wg.issue(w, {2, 3, 4, 5}, base + 3000, qdma);
-          wg.issue(w, {kslot(1)}, base + 1001, kdma);
+          wg.issue(w, qst, base + 3000, qdma);
+          if (fwd_prologue_k(slots) > 1) wg.issue(w, {kslot(1)}, base + 1001, kdma);
         }
         // sync(-1), the Q reads, a barrier.
-        std::vector<int> fl(c.W, fwd_wait(-1, kdma));
+        std::vector<int> fl(c.W, fwd_wait(-1, kdma, slots));
         wg.barrier(fl);
-        for (int w = 0; w < c.W; ++w) wg.read(w, 2 + (w % 4), base + 3000);
+        for (int w = 0; w < c.W; ++w) {
+          if (slots == 3) {
+            wg.read(w, 2 + (w % 4), base + 3000);
+          } else {
+            if (w <= 2) wg.read(w, 1, base + 3000);
+            if (w >= 2) wg.read(w, 2, base + 3000);
+          }
+        }
         wg.barrier_all(-1);
         // Stages -1 .. n: this wave's reads, then everyone's DMA.
         for (int j = -1; j <= n; ++j) {
-          if (j >= 0) wg.barrier_all(fwd_wait(j, kdma));
+          if (j >= 0) wg.barrier_all(fwd_wait(j, kdma, slots));
           for (int w = 0; w < c.W; ++w) {
             // K reads in stages -1 .. n_w - 2 (tile j + 1), V reads in 1 .. n_w (tile j - 1).
             if (n_w[w] > 0 && j <= n_w[w] - 2) wg.read(w, kslot(fwd_k_read(j)), base + 1000 + fwd_k_read(j));
             if (n_w[w] > 0 && j >= 1 && j <= n_w[w]) wg.read(w, vslot(fwd_v_read(j)), base + 2000 + fwd_v_read(j));
           }
           for (int w = 0; w < c.W; ++w) {
-            wg.issue(w, {kslot(k_loaded(j))}, base + 1000 + k_loaded(j), kdma);
-            wg.issue(w, {vslot(v_loaded(j))}, base + 2000 + v_loaded(j), kdma);
+            wg.issue(w, {kslot(k_loaded(j, slots))}, base + 1000 + k_loaded(j, slots), kdma);
+            // (Two slots: no V at stage -1; the kernel's instructions read nothing and still count.)
+            if (fwd_v_loads(j, slots))
+              wg.issue(w, {vslot(v_loaded(j, slots))}, base + 2000 + v_loaded(j, slots), kdma);
+            else
+              wg.vmem(w, kdma);
           }
         }
         // O rows: a whole tile's writers, or the merge of a shared one.
@@ -498,6 +517,7 @@ int main() {
       // The forward's launch choices (fwd_launch): D = 128 one 8-wave workgroup per CU; D <= 64 the
       // key-split kernel, zig on a resident grid, the split where it applies.
       check_fwd(FwdCfg{128, 8, 1, false, false}, bh, S);
+      check_fwd(FwdCfg{256, 4, 1, false, false}, bh, S);  // D = 256: four waves, two slots
       const int nq64 = (S + 127) / 128;
       const bool zig = resident((long long)nq64 * bh, 2, kCus);
       check_fwd(FwdCfg{64, 8, 2, zig, false}, bh, S);
@@ -514,7 +534,7 @@ int main() {
       // dK/dV (dkv_pp_launch): D = 64 zig on a resident grid; D = 128 the role split.
       check_dkv(64, bh, S, resident((long long)((S + 127) / 128) * bh, 2, kCus));
       check_dkv(128, bh, S, false);
-      launches += 7;
+      launches += 8;
     }
   for (int bh : {1, 3, 8})
     for (int S : {1, 100, 128, 200, 1000})
@@ -540,6 +560,7 @@ int main() {
     g_mutation = m;
     const int before = failures;
     check_fwd(FwdCfg{128, 8, 1, false, false}, 2, 1024);
+    check_fwd(FwdCfg{256, 4, 1, false, false}, 2, 1024);
     check_fwd(FwdCfg{64, 8, 2, true, true}, 6, 8192);
     check_dq(DqCfg{64, 4, 2, 1, false, false}, 3, 1024);
     check_dq(DqCfg{64, 8, 2, 2, true, true}, 6, 8192);

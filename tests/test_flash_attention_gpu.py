@@ -210,6 +210,36 @@ def test_split_long_context_forward(dev, b, h, s, d):
     assert rel_fro(o_split[:1, :1], o_ref) <= 1.1 * rel_fro(to_np(o1)[:1, :1], o_ref) + 1e-5
 
 
+@pytest.mark.parametrize("b,h,s,d", [
+    (1, 2, 64, 256),     # one key tile: the diagonal stage only
+    (2, 3, 192, 256),    # three tiles, odd head count
+    (1, 2, 1024, 256),
+    (2, 8, 2048, 256),   # 256 workgroups, one per CU
+    (3, 5, 704, 256),    # 11 key tiles, an odd tile count, 90 workgroups
+])
+def test_forward_d256_bf16(dev, b, h, s, d):
+    """The causal bf16 forward at head dim 256 (the largest the reference's contract admits below
+    the slab kernels: d <= 128 or a multiple of 128), run by the four-wave, one-wave-per-SIMD kernel
+    with a two-slot K/V ring for lengths that are multiples of 64: O at 2e-2 and lse at 1e-3 against
+    the oracle, every row written (NaN prefill), the same bits on a rerun."""
+    q, k, v = _qkv(110 + d + s, (b, h, s, d), "bf16")
+    qt, kt, vt = (to_dev(a, "bf16", dev) for a in (q, k, v))
+    lib, st, scale = _hip.lib(), _hip.stream_of(qt), d ** -0.5
+    runs = []
+    for _ in range(2):
+        o = torch.full_like(qt, float("nan"))
+        lse = torch.full((b, h, s), float("nan"), device=dev)
+        _hip.check(lib.ferrite_hip_attn_fwd(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                            b, h, s, s, d, _hip.BF16, 1, scale, st), "fwd")
+        torch.cuda.synchronize()
+        runs.append((to_np(o), to_np(lse)))
+    np.testing.assert_array_equal(runs[0][0], runs[1][0])
+    np.testing.assert_array_equal(runs[0][1], runs[1][1])
+    o_ref, lse_ref = oatt.forward(q, k, v, causal=True, dtype=np.float32)
+    assert max_abs(runs[0][0], o_ref) <= 2e-2
+    assert max_abs(runs[0][1], lse_ref) <= 1e-3
+
+
 @pytest.mark.parametrize("fused", [True, False], ids=["delta_in_dq", "delta_pass"])
 @pytest.mark.parametrize("b,h,s,d", [
     (1, 2, 2048, 64),   # one workgroup per CU: equal halves
