@@ -10,7 +10,8 @@ one forward pass over that batch; K steps are timed back to back with HIP
 events on the stream the kernels run on, with inputs resident in HBM. The same
 line carries every other kernel of the path under "kernels": attention
 backward (delta, dK/dV, dQ), the long-context variant (B=1, H=8, T=8192, d=64),
-fused add+RMSNorm ([4096,1024] bf16, timed over 24 rotating buffer sets so the
+head dim 256 (B=4, H=8, T=2048, d=256), fused add+RMSNorm ([4096,1024] bf16,
+timed over 24 rotating buffer sets so the
 working set exceeds the 256 MB Infinity Cache) and the blocked matmul (bf16
 4096^3, f32 1000^3). Each carries its roofline fraction against MI355X peaks.
 "gpt_train_step" times the caller of these kernels: one forward+backward+AdamW
@@ -608,6 +609,9 @@ def main(argv=None):
         kernels["attention"] = bench_attention(4, 16, 2048, 128, a.steps, a.warmup)
         kernels["attention_long_context"] = bench_attention(1, 8, 8192, 64, max(a.steps // 2, 3), 2, seed=27)
         kernels["attention_fwd_parts"] = bench_attention_fwd_parts(max(a.steps // 2, 5), 2)
+        # Head dim 256 (the reference's tests run it), at the headline's FLOPs: the forward on the
+        # pipelined four-wave kernel, the backward on the 128-column slab kernels.
+        kernels["attention_d256"] = bench_attention(4, 8, 2048, 256, max(a.steps // 5, 3), 2, seed=31)
     if a.only in ("rmsnorm", "all"):
         kernels["add_rmsnorm"] = bench_rmsnorm(4096, 1024, a.steps, a.warmup)
         ceil = bench_stream_ceilings()
