@@ -17,9 +17,15 @@
 #endif
 
 // Share (percent) of a pair's tiles that the older workgroup takes in the split
-// dK/dV and dQ kernels when two share a CU, and the fewest 128-row tiles for
-// which they split then; compile-time settings so that other values can be
-// built and timed.
+// forward, dK/dV and dQ kernels when two share a CU, and the fewest 128-row
+// tiles for which the backward splits then; compile-time settings so that
+// other values can be built and timed.
+#ifndef FERRITE_FWD_OLDER_SHARE
+#define FERRITE_FWD_OLDER_SHARE 70
+#endif
+#ifndef FERRITE_FWD_SPLIT_MIN_TWO
+#define FERRITE_FWD_SPLIT_MIN_TWO 64
+#endif
 #ifndef FERRITE_DKV_OLDER_SHARE
 #define FERRITE_DKV_OLDER_SHARE 62
 #endif
@@ -113,7 +119,7 @@ struct SplitRule {
 };
 constexpr int kSplitRows = 128;
 // The forward: A runs about 2.5 stages for each of B's.
-constexpr SplitRule kFwdSplit{16, 64, 70};
+constexpr SplitRule kFwdSplit{16, FERRITE_FWD_SPLIT_MIN_TWO, FERRITE_FWD_OLDER_SHARE};
 // dK/dV (key blocks sweeping query tiles) and dQ (query tiles sweeping key
 // tiles) at head dims <= 64: A takes 62% (1x8x8192x64 on MI355X, shares 55 /
 // 62 / 70 / 78: dK/dV 133.3 / 131.4 / 136.1 / 140.2 us against 157.1 unsplit,

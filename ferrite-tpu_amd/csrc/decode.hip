@@ -7,7 +7,7 @@
 // names a decode-attention kernel as its next step (README.md:283-285).
 //
 // HBM-bound: a step reads (pos + 1) keys and values per head once. Keys are
-// split into chunks of kChunk per workgroup (flash-decoding), so short batches
+// split into chunks of 256 or 1024 per workgroup (flash-decoding), so short batches
 // still spread over the CUs; each chunk keeps an online (max, sum, acc)
 // softmax and writes f32 partials, and a second kernel merges the chunks of a
 // head. A row of LPR = D / (16 / sizeof(T)) lanes holds one key: each lane
@@ -24,8 +24,13 @@ namespace ferrite {
 namespace {
 
 constexpr int kDecThreads = 256;  // 4 waves
-constexpr int kChunk = 256;       // keys per workgroup
-constexpr int kUnroll = 4;        // row steps whose loads are issued together
+constexpr int kUnroll = 2;        // row steps whose loads are issued together
+// Keys per workgroup: 1024 for grids of at least kLongGrid workgroups that way
+// (8x32x8192x128: 2048 of them; 211 -> 180 us on MI355X against 256-key
+// chunks), 256 otherwise, so that short caches and small batches still spread
+// over the CUs.
+constexpr int kChunkShort = 256, kChunkLong = 1024;
+constexpr int64_t kLongGrid = 512;
 
 template <typename T>
 struct Vec16 {
@@ -60,7 +65,7 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float* acc, floa
 }
 
 // grid (chunks, H, B). Partials: [B, H, chunks, D + 2] = (acc[D], m, l) in the log2 domain.
-template <typename T, int D, bool DIRECT>
+template <typename T, int D, bool DIRECT, int kChunk>
 __global__ __launch_bounds__(kDecThreads) void decode_attn_kernel(const T* __restrict__ q, const T* __restrict__ k_new,
                                                                   const T* __restrict__ v_new, T* __restrict__ k_cache,
                                                                   T* __restrict__ v_cache, const int32_t* __restrict__ pos,
@@ -71,6 +76,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_attn_kernel(const T* __res
   constexpr int RPW = 64 / LPR;       // rows per wave step
   constexpr int kWaveRows = kChunk / (kDecThreads / 64);
   static_assert(D % V == 0 && LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "head dim");
+  static_assert(kWaveRows % (RPW * kUnroll) == 0, "a wave's rows in whole unrolled steps");
   __shared__ float red[kDecThreads / 64][D + 2];
 
   const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -113,8 +119,15 @@ __global__ __launch_bounds__(kDecThreads) void decode_attn_kernel(const T* __res
       } else if (r == last) {
         load_vec(k_new + bh * D + sub * V, kv[u]);
         load_vec(v_new + bh * D + sub * V, vv[u]);
+      } else {
+        // Past the last key: zeros, weighted 0 below.
+#pragma unroll
+        for (int e = 0; e < V; ++e) kv[u][e] = vv[u][e] = 0.f;
       }
     }
+    // The kUnroll scores of a row group first, then one rescale to their max.
+    float sc[kUnroll];
+    float mb = -INFINITY;
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int r = r0 + rs + u * RPW + grp;
@@ -125,15 +138,23 @@ __global__ __launch_bounds__(kDecThreads) void decode_attn_kernel(const T* __res
       }
 #pragma unroll
       for (int off = 1; off < LPR; off <<= 1) s += __shfl_xor(s, off, 64);
-      if (r <= last) {
-        s *= c;
-        const float mn = fmaxf(m, s);
-        const float a = exp2f(m - mn), pr = exp2f(s - mn);
-        l = l * a + pr;
+      sc[u] = r <= last ? s * c : -INFINITY;
+      mb = fmaxf(mb, sc[u]);
+    }
+    if (mb > -INFINITY) {
+      const float mn = fmaxf(m, mb);
+      const float a = exp2f(m - mn);
+      l *= a;
 #pragma unroll
-        for (int e = 0; e < V; ++e) acc[e] = acc[e] * a + pr * vv[u][e];
-        m = mn;
+      for (int e = 0; e < V; ++e) acc[e] *= a;
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const float pr = exp2f(sc[u] - mn);
+        l += pr;
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc[e] = __builtin_fmaf(pr, vv[u][e], acc[e]);
       }
+      m = mn;
     }
   }
 
@@ -181,7 +202,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_attn_kernel(const T* __res
 // Loads go out eight chunks at a time, so a thread waits on a few batches of
 // independent loads rather than on one chain of dependent ones. An empty chunk
 // (m = -inf, l = acc = 0) gets weight exp2(-inf) = 0.
-template <typename T, int D>
+template <typename T, int D, int kChunk>
 __global__ __launch_bounds__(256) void decode_combine_kernel(const float* __restrict__ part, const int32_t* __restrict__ pos,
                                                              T* __restrict__ out, int nchunks, int max_len) {
   constexpr int G = 8;
@@ -229,12 +250,15 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const float* __rest
   }
 }
 
-int64_t chunks_for(int64_t max_len) { return cdiv(max_len, (int64_t)kChunk); }
+int chunk_for(int64_t b, int64_t h, int64_t max_len) {
+  return b * h * cdiv(max_len, (int64_t)kChunkLong) >= kLongGrid ? kChunkLong : kChunkShort;
+}
+int64_t chunks_for(int64_t b, int64_t h, int64_t max_len) { return cdiv(max_len, (int64_t)chunk_for(b, h, max_len)); }
 
-template <typename T, int D>
-int decode_launch(const void* q, const void* kn, const void* vn, void* kc, void* vc, const int32_t* pos, void* out,
-                  int64_t B, int64_t H, int64_t L, float scale, void* ws, int64_t ws_bytes, hipStream_t st) {
-  const int64_t nch = chunks_for(L);
+template <typename T, int D, int kChunk>
+int decode_launch_c(const void* q, const void* kn, const void* vn, void* kc, void* vc, const int32_t* pos, void* out,
+                    int64_t B, int64_t H, int64_t L, float scale, void* ws, int64_t ws_bytes, hipStream_t st) {
+  const int64_t nch = cdiv(L, (int64_t)kChunk);
   const float c = scale * kLog2e;
   const dim3 grid((unsigned)nch, (unsigned)H, (unsigned)B);
   auto tq = static_cast<const T*>(q);
@@ -244,17 +268,25 @@ int decode_launch(const void* q, const void* kn, const void* vn, void* kc, void*
   auto cv = static_cast<T*>(vc);
   auto to = static_cast<T*>(out);
   if (nch == 1) {
-    hipLaunchKernelGGL((decode_attn_kernel<T, D, true>), grid, dim3(kDecThreads), 0, st, tq, tk, tv, ck, cv, pos, to,
+    hipLaunchKernelGGL((decode_attn_kernel<T, D, true, kChunk>), grid, dim3(kDecThreads), 0, st, tq, tk, tv, ck, cv, pos, to,
                        nullptr, (int)L, c);
   } else {
     if (!ws || ws_bytes < B * H * nch * (D + 2) * (int64_t)sizeof(float))
       return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_decode_attention: workspace too small");
-    hipLaunchKernelGGL((decode_attn_kernel<T, D, false>), grid, dim3(kDecThreads), 0, st, tq, tk, tv, ck, cv, pos, to,
+    hipLaunchKernelGGL((decode_attn_kernel<T, D, false, kChunk>), grid, dim3(kDecThreads), 0, st, tq, tk, tv, ck, cv, pos, to,
                        static_cast<float*>(ws), (int)L, c);
-    hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3((unsigned)H, (unsigned)B), dim3(std::min(D, 256)), 0, st,
+    hipLaunchKernelGGL((decode_combine_kernel<T, D, kChunk>), dim3((unsigned)H, (unsigned)B), dim3(std::min(D, 256)), 0, st,
                        static_cast<const float*>(ws), pos, to, (int)nch, (int)L);
   }
   return check_launch("ferrite_decode_attention");
+}
+
+template <typename T, int D>
+int decode_launch(const void* q, const void* kn, const void* vn, void* kc, void* vc, const int32_t* pos, void* out,
+                  int64_t B, int64_t H, int64_t L, float scale, void* ws, int64_t ws_bytes, hipStream_t st) {
+  if (chunk_for(B, H, L) == kChunkLong)
+    return decode_launch_c<T, D, kChunkLong>(q, kn, vn, kc, vc, pos, out, B, H, L, scale, ws, ws_bytes, st);
+  return decode_launch_c<T, D, kChunkShort>(q, kn, vn, kc, vc, pos, out, B, H, L, scale, ws, ws_bytes, st);
 }
 
 }  // namespace
@@ -262,7 +294,7 @@ int decode_launch(const void* q, const void* kn, const void* vn, void* kc, void*
 
 extern "C" int64_t ferrite_hip_decode_attention_workspace(int64_t b, int64_t h, int64_t max_len, int64_t d) {
   if (b < 0 || h < 1 || max_len < 1 || d < 1) return -1;
-  const int64_t nch = ferrite::chunks_for(max_len);
+  const int64_t nch = ferrite::chunks_for(b, h, max_len);
   return nch > 1 ? b * h * nch * (d + 2) * (int64_t)sizeof(float) : 0;
 }
 
