@@ -2252,7 +2252,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_dkv_wide_kernel(const T* __r
 }
 
 // ===========================================================================
-// Backward, bf16 with D in {64, 128}: streamed tiles read as rows and transposed
+// Backward, bf16 with D in {64, 128, 256}: streamed tiles read as rows and transposed
 // ===========================================================================
 // The backward kernels read each streamed 64-row tile twice: as row
 // fragments (16-byte reads, A operand of S = Q K^T or S^T = K Q^T) and
@@ -2264,23 +2264,35 @@ __global__ __launch_bounds__(kThreads, 1) void attn_dkv_wide_kernel(const T* __r
 // different 64-byte bank groups (transposed reads), and every fragment
 // address is a per-lane base plus a constant. Rows are stored in the MFMA
 // output order of perm_row, as in the forward K tile.
+// D = 256 (512-byte rows): a 1 KB block holds two rows, so the tile is two
+// such 16-block halves, rows 0-31 and 32-63, one after the other. Every
+// offset inside a half differs from the D = 128 tile's only by multiples of
+// 256 bytes (a row position times 512 instead of 256), so the lanes of a
+// read meet the same banks as there. The DMA then moves 32 blocks of 1 KB
+// (two rows each, every lane carrying data).
 template <int D>
 struct BwdTile {
-  static_assert(D == 64 || D == 128, "128- or 256-byte rows");
+  static_assert(D == 64 || D == 128 || D == 256, "128-, 256- or 512-byte rows");
   static constexpr int kRowBytes = 2 * D;
   static constexpr int kChunks = kRowBytes / 16;
-  static constexpr int kBlocks = 16;
+  static constexpr int kHalves = D == 256 ? 2 : 1;
+  static constexpr int kBlocks = 16 * kHalves;  // 1 KB DMA blocks
   static constexpr int kStride = 1024 + 16;
-  static constexpr int kBytes = kBlocks * kStride;
+  static constexpr int kHalfBytes = 16 * kStride;
+  static constexpr int kBytes = kHalves * kHalfBytes;
   static __host__ __device__ constexpr int place(int b) { return 4 * (b & 3) + (b >> 2); }
-  static __host__ __device__ constexpr int block_off(int b) { return place(b) * kStride; }
+  static __host__ __device__ constexpr int block_off(int b) { return (b >> 4) * kHalfBytes + place(b & 15) * kStride; }
   static __host__ __device__ constexpr int off(int p, int byte) {
-    return block_off(p & 15) + (p >> 4) * kRowBytes + byte;
+    return D == 256 ? (p >> 5) * kHalfBytes + place(p & 15) * kStride + ((p >> 4) & 1) * kRowBytes + byte
+                    : place(p & 15) * kStride + (p >> 4) * kRowBytes + byte;
   }
   // With 128-byte rows a block holds its four rows in its first 512 bytes;
   // lanes 32-63 of its DMA instruction are switched off (they write zeros
-  // into the unused half).
-  static __host__ __device__ constexpr int dma_row(int b, int L) { return b + 16 * (L / kChunks); }
+  // into the unused half). With 512-byte rows block b holds rows
+  // 32 (b / 16) + b % 16 and that + 16.
+  static __host__ __device__ constexpr int dma_row(int b, int L) {
+    return D == 256 ? 32 * (b >> 4) + (b & 15) + 16 * (L / kChunks) : b + 16 * (L / kChunks);
+  }
   static __host__ __device__ constexpr int dma_chunk(int L) { return L % kChunks; }
   static __device__ __forceinline__ bool dma_lane(int L) { return L / kChunks < 4; }
   // Row fragment (physical rows 32 half + l32, bytes 32 kk + 16 g): lane base
@@ -2302,6 +2314,39 @@ struct BwdTile {
   static __device__ __forceinline__ int row(const Bases& b, int half, int kk) { return b.r + row_at(half, kk); }
   static __device__ __forceinline__ int tr(const Bases& b, int half, int h, int u) { return b.t + tr_at(half, h, u); }
 };
+
+// Compile-time check of a BwdTile's DMA: lane L of block instruction b writes
+// LDS bytes block_off(b) + 16 L, which must be where off() keeps the row and
+// chunk the lane loads, every (row, chunk) of the 64 rows exactly once; and,
+// for G waves sharing the instructions (PpDma), the source row of a wave's
+// instruction i is its row for instruction 0 plus a delta independent of the
+// wave and the lane.
+template <int D, int G>
+constexpr bool bwd_tile_dma_ok() {
+  typedef BwdTile<D> T;
+  bool seen[64 * T::kChunks] = {};
+  for (int b = 0; b < T::kBlocks; ++b)
+    for (int L = 0; L < 64; ++L) {
+      if (L / T::kChunks >= 4) continue;
+      const int p = T::dma_row(b, L), c = T::dma_chunk(L);
+      if (p < 0 || p >= 64 || seen[p * T::kChunks + c]) return false;
+      seen[p * T::kChunks + c] = true;
+      if (T::block_off(b) + 16 * L != T::off(p, 16 * c)) return false;
+    }
+  for (bool x : seen)
+    if (!x) return false;
+  for (int gw = 0; gw < G; ++gw)
+    for (int i = 0; i < T::kBlocks / G; ++i) {
+      const int d0 = perm_src(T::dma_row(G * i, 0)) - perm_src(T::dma_row(0, 0));
+      for (int L = 0; L < 64; ++L)
+        if (L / T::kChunks < 4 && perm_src(T::dma_row(gw + G * i, L)) != perm_src(T::dma_row(gw, L)) + d0)
+          return false;
+    }
+  return true;
+}
+static_assert(bwd_tile_dma_ok<64, 4>() && bwd_tile_dma_ok<64, 8>() && bwd_tile_dma_ok<128, 4>() &&
+                  bwd_tile_dma_ok<128, 8>() && bwd_tile_dma_ok<256, 4>() && bwd_tile_dma_ok<256, 8>(),
+              "BwdTile DMA blocks cover the tile once, where the reads expect them");
 
 // Compact tile for D = 64 (128-byte rows): 8 KB of rows in 8 blocks of 8
 // consecutive physical rows (row p in block p / 8 at position p % 8), the
@@ -3147,7 +3192,7 @@ struct DqPp {
 // fragments are loaded anyway) and written out for the dK/dV kernel, which
 // then runs after this one: the separate delta pass over O and dO goes away.
 template <int D, int W, int SLOTS, bool ZIG, bool FUSED = false, int KSPLIT = 1, bool SPLIT = false>
-__global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+__global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : D > 128 ? 1 : 2)) void attn_dq_pp_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                                 const bf16* __restrict__ v,
                                                                 const bf16* __restrict__ dout,
                                                                 const float* __restrict__ lse,
@@ -3433,7 +3478,7 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : 2)) void attn_dq_pp_ker
     }
   }
 
-  if (D == 128 && d == D) {
+  if (D >= 128 && d == D) {
     // Whole-row stores through LDS (store_acc_rows_lds); the barrier keeps the
     // other waves' last reads off this wave's region (every DMA has landed: the
     // last tile's wait was vmcnt(0)). At D = 64 (two workgroups per CU, 128-byte
@@ -3689,8 +3734,13 @@ int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, 
     const bool one_round = causal && sched::resident(cdiv(s.sq, F4::BQ) * s.b * s.h, 2, cus);
     return one_round ? dq_pp_launch_t<D, 8, 2, true, 2>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw)
                      : dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
-  } else {
+  } else if constexpr (D == 128) {
     return dq_pp_launch_t<D, 8, 3, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
+  } else {
+    // D = 256: the Q and dO fragments of 32 rows (128 VGPRs) and a dQ
+    // accumulator of 256 columns (128) take one SIMD's registers for one wave:
+    // four waves, one per SIMD, over a two-slot K/V ring (130 KB of LDS).
+    return dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
   }
 }
 
@@ -4035,6 +4085,8 @@ extern "C" int ferrite_hip_attn_bwd_dq_delta_ex(const void* q, const void* k, co
                               workspace_bytes);
     return dq_pp_launch<128>(q, k, v, dout, lse, delta, dq, s, causal, scale, st, o);
   }
+  if (dtype == FERRITE_BF16 && al && d == 256)
+    return dq_pp_launch<256>(q, k, v, dout, lse, delta, dq, s, causal, scale, st, o);
   // Other dtypes and head dims: the delta kernel, then dQ reading it.
   if (int rc = ferrite_hip_attn_bwd_delta(o, dout, delta, b, h, sq, d, dtype, stream)) return rc;
   return ferrite_hip_attn_bwd_dq_ex(q, k, v, dout, lse, delta, dq, b, h, sq, sk, d, dtype, causal, scale, workspace,
@@ -4062,6 +4114,8 @@ extern "C" int ferrite_hip_attn_bwd_dq_ex(const void* q, const void* k, const vo
   const bool al = d % (dtype == FERRITE_BF16 ? 8 : 4) == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
                   aligned16(dout) && aligned16(dq);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d == 256 && dtype == FERRITE_BF16 && al)
+    return dq_pp_launch<256>(q, k, v, dout, lse, const_cast<float*>(delta), dq, s, causal, scale, st);
   if (d > 128) FERRITE_WIDE(dq_wide_launch, dtype, al, q, k, v, dout, lse, delta, dq, s, causal, scale, st);
 #define FERRITE_DISPATCH_256(LAUNCH, T, aligned, ...) \
   return fail(FERRITE_ERR_INVALID_ARGUMENT, "unreachable head_dim")

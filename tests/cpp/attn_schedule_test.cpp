@@ -318,7 +318,7 @@ static bool dq_writes(int kh, int role) { return g_mutation == 7 ? (kh == 0) : (
 static void check_dq(const DqCfg& c, int bh, int S) {
   const int BQ = 32 * c.W / c.ksplit;
   const int nq = (S + BQ - 1) / BQ;
-  const int kdma = 16 / c.W;  // BwdTile: 16 blocks per tile, split over the waves
+  const int kdma = (c.D == 256 ? 32 : 16) / c.W;  // BwdTile: 16 (D = 256: 32) blocks per tile, split over the waves
   const int cut = c.split ? split_cut(bh, S, kCus, kDqSplit) : 0;
   const std::string name = "dq D" + std::to_string(c.D) + " W" + std::to_string(c.W) + (c.split ? " split" : "") +
                            " bh" + std::to_string(bh) + " S" + std::to_string(S);
@@ -524,6 +524,7 @@ int main() {
       if (fwd_split_applies(bh, S, kCus)) check_fwd(FwdCfg{64, 8, 2, true, true}, bh, S);
       // dQ (dq_pp_launch): D = 128 8 waves 3 slots; D = 64 resident: 8 waves, key split, zig; else 4 waves.
       check_dq(DqCfg{128, 8, 3, 1, false, false}, bh, S);
+      check_dq(DqCfg{256, 4, 2, 1, false, false}, bh, S);  // D = 256: four waves, two slots
       if (resident((long long)((S + 127) / 128) * bh, 2, kCus))
         check_dq(DqCfg{64, 8, 2, 2, true, false}, bh, S);
       else
@@ -534,7 +535,7 @@ int main() {
       // dK/dV (dkv_pp_launch): D = 64 zig on a resident grid; D = 128 the role split.
       check_dkv(64, bh, S, resident((long long)((S + 127) / 128) * bh, 2, kCus));
       check_dkv(128, bh, S, false);
-      launches += 8;
+      launches += 9;
     }
   for (int bh : {1, 3, 8})
     for (int S : {1, 100, 128, 200, 1000})
@@ -563,6 +564,7 @@ int main() {
     check_fwd(FwdCfg{256, 4, 1, false, false}, 2, 1024);
     check_fwd(FwdCfg{64, 8, 2, true, true}, 6, 8192);
     check_dq(DqCfg{64, 4, 2, 1, false, false}, 3, 1024);
+    check_dq(DqCfg{256, 4, 2, 1, false, false}, 3, 1024);
     check_dq(DqCfg{64, 8, 2, 2, true, true}, 6, 8192);
     check_dkv(128, 2, 1024, false);
     check_dkv(64, 6, 8192, true, true);

@@ -307,6 +307,65 @@ def test_split_long_context_backward(dev, b, h, s, d, fused):
 
 
 @pytest.mark.parametrize("fused", [True, False], ids=["delta_in_dq", "delta_pass"])
+@pytest.mark.parametrize("b,h,sq,sk,causal", [
+    (1, 2, 64, 64, True),       # one key tile: the diagonal only
+    (2, 3, 192, 192, True),     # three tiles, odd head count
+    (1, 2, 200, 200, True),     # ragged: partial query and key tiles
+    (1, 1, 100, 260, False),    # non-causal, sk != sq, both ragged
+    (3, 5, 704, 704, True),     # 11 tiles, 90 query workgroups
+])
+def test_backward_d256_bf16(dev, b, h, sq, sk, causal, fused):
+    """The bf16 backward at head dim 256 through the C ABI (the pipelined dQ kernel with four waves
+    and a two-slot K/V ring): dQ, dK, dV against the oracle at 2e-2 or twice the reference's own bf16
+    recipe's error, every output written (NaN prefill), in both backward orders."""
+    _abi_case(dev, b, h, sq, sk, 256, "bf16", causal, seed=71 + sq, scale=256 ** -0.5, fused=fused)
+
+
+@pytest.mark.parametrize("fused", [True, False], ids=["delta_in_dq", "delta_pass"])
+def test_backward_d256_bench_shape(dev, fused):
+    """The head-dim-256 bench shape, 4x8x2048x256 causal bf16 (512 dQ workgroups, two rounds of
+    one per CU): every output written, the same bits on a rerun, and the first head against the
+    oracle at 2e-2 or twice the reference's own bf16 recipe's error (the gradients reach ~5 here,
+    where one bf16 ulp is 2^-5), as _abi_case holds the small shapes."""
+    b, h, s, d = 4, 8, 2048, 256
+    q, k, v = _qkv(131, (b, h, s, d), "bf16")
+    do = normal(133, q.shape, "bf16")
+    qt, kt, vt, dot = (to_dev(a, "bf16", dev) for a in (q, k, v, do))
+    scale, st, lib, bf = d ** -0.5, _hip.stream_of(qt), _hip.lib(), _hip.BF16
+    out, lse = _flash_forward(qt, kt, vt, causal=True, scale=scale)
+    P = lambda t: t.data_ptr()  # noqa: E731
+
+    def run():
+        dq, dk, dv = (torch.full_like(qt, float("nan")) for _ in range(3))
+        if fused:
+            delta = torch.full((b, h, s), float("nan"), device=dev)
+            _hip.check(lib.ferrite_hip_attn_bwd_dq_delta(P(qt), P(kt), P(vt), P(out), P(dot), P(lse), P(delta), P(dq),
+                                                         b, h, s, s, d, bf, 1, scale, st), "dq_delta")
+        else:
+            delta = _flash_delta(out, dot)
+        _hip.check(lib.ferrite_hip_attn_bwd_dkv(P(qt), P(kt), P(vt), P(dot), P(lse), P(delta), P(dk), P(dv),
+                                                b, h, s, s, d, bf, 1, scale, st), "dkv")
+        if not fused:
+            _hip.check(lib.ferrite_hip_attn_bwd_dq(P(qt), P(kt), P(vt), P(dot), P(lse), P(delta), P(dq),
+                                                   b, h, s, s, d, bf, 1, scale, st), "dq")
+        torch.cuda.synchronize()
+        return [to_np(t) for t in (dq, dk, dv)]
+
+    first, second = run(), run()
+    for a, c in zip(first, second):
+        assert not np.isnan(a).any()
+        np.testing.assert_array_equal(a, c)
+    q1, k1, v1, do1 = q[:1, :1], k[:1, :1], v[:1, :1], do[:1, :1]
+    grads_ref = oatt.backward(q1, k1, v1, do1, causal=True, dtype=np.float32)
+    ob, lb = oatt.flash_forward(q1, k1, v1, causal=True, scale=scale, bq=s, bk=s, bf16=True)
+    recipe = oatt.flash_backward(q1, k1, v1, do1, ob, lb, causal=True, scale=scale, bq=s, bk=s, bf16=True)
+    for name, a, rb, r in zip(("dq", "dk", "dv"), first, recipe, grads_ref):
+        err, rerr = max_abs(a[:1, :1], r), max_abs(rb, r)
+        assert err <= max(2e-2, 2.0 * rerr), (name, err, rerr)
+        assert rel_fro(a[:1, :1], r) <= 1.25 * rel_fro(rb, r) + 1e-3, name
+
+
+@pytest.mark.parametrize("fused", [True, False], ids=["delta_in_dq", "delta_pass"])
 def test_gpt_attention_shape(dev, fused):
     """The GPT step's attention, B=8, H=12, T=1024, d=64: 768 dQ workgroups, more than fit at
     once, so dQ takes its heaviest-first order rather than the paired one. Not a BASELINE
