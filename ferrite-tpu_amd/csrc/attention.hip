@@ -3160,6 +3160,421 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
   }
 }
 
+// ---- dK/dV at D = 256 -------------------------------------------------------
+// A 32-row granule of a 256-column bf16 tile: the first half of BwdTile<256>
+// (rows 0-31, 16 DMA blocks of 1 KB holding two rows each), so that its row
+// and transposed fragment reads are BwdTile<256>'s at half 0.
+struct BwdHalf256 {
+  typedef BwdTile<256> Full;
+  static constexpr int kRowBytes = Full::kRowBytes, kChunks = Full::kChunks;
+  static constexpr int kBlocks = 16;
+  static constexpr int kBytes = Full::kHalfBytes;
+  static __host__ __device__ constexpr int off(int p, int byte) { return Full::off(p, byte); }
+  static __host__ __device__ constexpr int block_off(int b) { return Full::block_off(b); }
+  static __host__ __device__ constexpr int dma_row(int b, int L) { return Full::dma_row(b, L); }
+  static __host__ __device__ constexpr int dma_chunk(int L) { return Full::dma_chunk(L); }
+  static __device__ __forceinline__ bool dma_lane(int L) { return Full::dma_lane(L); }
+};
+
+// Compile-time check of the granule's DMA, as bwd_tile_dma_ok: lane L of block
+// instruction b (every lane carries data) writes LDS bytes block_off(b) + 16 L
+// inside the granule, where off() keeps the row and chunk it loads, each of
+// the 32 rows x 32 chunks once; for G waves sharing the instructions, a
+// wave's instruction i loads its rows of instruction 0 moved by a delta that
+// depends on i alone.
+template <int G>
+constexpr bool half256_dma_ok() {
+  typedef BwdHalf256 T;
+  bool seen[32 * T::kChunks] = {};
+  for (int b = 0; b < T::kBlocks; ++b)
+    for (int L = 0; L < 64; ++L) {
+      const int p = T::dma_row(b, L), c = T::dma_chunk(L);
+      if (p < 0 || p >= 32 || seen[p * T::kChunks + c]) return false;
+      seen[p * T::kChunks + c] = true;
+      if (T::block_off(b) + 16 * L != T::off(p, 16 * c) || T::block_off(b) + 16 * L + 16 > T::kBytes) return false;
+    }
+  for (bool x : seen)
+    if (!x) return false;
+  for (int gw = 0; gw < G; ++gw)
+    for (int i = 0; i < T::kBlocks / G; ++i) {
+      const int d0 = perm_src(T::dma_row(G * i, 0)) - perm_src(T::dma_row(0, 0));
+      for (int L = 0; L < 64; ++L)
+        if (perm_src(T::dma_row(gw + G * i, L)) != perm_src(T::dma_row(gw, L)) + d0) return false;
+    }
+  return true;
+}
+static_assert(half256_dma_ok<8>(), "the 256-column granule's DMA blocks cover it once, where the reads expect them");
+
+// dK, dV at D = 256: the role split of attn_dkv_rs_kernel, each workgroup on
+// one 128-column slab of dK and dV. A 32-key block's K and V rows (256 columns
+// each) and its dK and dV accumulators would take 512 registers, a SIMD's
+// whole file; so a workgroup keeps only its slab's dK and dV columns, and both
+// slabs' workgroups compute the full-width S and dP (six products where one
+// pass would run four, in exchange for two waves per SIMD). Role A (wave
+// w < 4): S = Q K^T over 256 columns, P, dV^T[slab] += dO^T[slab] P for keys
+// k0 + 32 w; role B (wave w + 4, same SIMD): dP = dO V^T, dS = P (dP - delta),
+// dK^T[slab] += Q^T[slab] dS. P crosses from A to B in f32 through LDS, as
+// there. The query side streams in 32-row granules (BwdHalf256, 16.6 KB): a
+// ring of four for Q (granule x is read in step x - 1 by A's S products and in
+// step x + 1 by B's dK products) and one of three for dO (steps x and x + 1),
+// each loaded one step ahead (sched::dkv256_*); with the two P buffers they
+// take 153 KB. One workgroup barrier per step (32 queries).
+struct Dkv256 {
+  static constexpr int D = 256, kWaves = 8, kThreads = 64 * kWaves;
+  static constexpr int BKV = 128, BG = 32;  // keys per workgroup, queries per granule
+  static constexpr int KS = D / 16;         // k-chunks of S and dP
+  static constexpr int SDT = 4;             // 32-column output tiles of a 128-column slab
+  typedef BwdHalf256 G;
+  typedef BwdTile<256> Tile;
+  static constexpr int kQSlots = sched::kDkv256QSlots, kDoSlots = sched::kDkv256DoSlots;
+  // lse (Q ring) or delta (dO ring): one stat_dma instruction, 64 rows in its
+  // first 256 bytes and zeros from the other 48 lanes in the rest of 1 KB.
+  static constexpr int kStatBytes = 1024;
+  static constexpr int kSlotBytes = G::kBytes + kStatBytes;
+  static constexpr int kDoRing = kQSlots * kSlotBytes;
+  static constexpr int kXRing = kDoRing + kDoSlots * kSlotBytes;
+  static constexpr int kXBytes = 4 * 4096;  // P of one granule for the four SIMD pairs (f32)
+  static constexpr int kLds = kXRing + 2 * kXBytes;
+  static constexpr int kDma = G::kBlocks / kWaves;  // per wave per granule, for Q and for dO
+  static constexpr int kStage = kSlotBytes;         // K / V row staging: from Q slot 1 on, 16 KB a wave
+  static_assert(kStatBytes >= 64 * 16, "a statistics DMA writes 16 bytes for each of its 64 lanes");
+  static_assert(kLds <= 160 * 1024, "one workgroup per CU");
+  static_assert(kStage + kWaves * 32 * 2 * D <= kLds, "the K / V rows fit the staging");
+};
+
+template <bool SAMEP>
+__global__ __launch_bounds__(512, 1) void attn_dkv_rs256_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                               const bf16* __restrict__ v,
+                                                               const bf16* __restrict__ dout,
+                                                               const float* __restrict__ lse,
+                                                               const float* __restrict__ delta, bf16* __restrict__ dk,
+                                                               bf16* __restrict__ dv, int bh_count, int Sq, int Sk,
+                                                               int causal, float scale, float scale_log2, AttnViews vw) {
+  typedef Dkv256 F;
+  typedef F::G G;
+  typedef F::Tile Tile;
+  constexpr int KS = F::KS, SDT = F::SDT;
+  constexpr int kAhead = 3;
+  // Per wave and step: Q blocks, dO blocks, and a statistics row (waves 0 and 4 only).
+  constexpr int kStepDma = 2 * F::kDma + 1;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  // Blocks: heads fastest, then the two slabs of a key block, then key blocks
+  // from the heaviest (first) causal sweep on.
+  const int bh = blockIdx.x % bh_count;
+  const int rest = (int)(blockIdx.x / bh_count);
+  const int kt = rest >> 1, slab = rest & 1;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pair = wave & 3, role = wave >> 2;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 5;
+  const int k0 = kt * F::BKV;
+  const int k0w = k0 + 32 * pair;
+  const int kvrow = k0w + (lane & 31);
+
+  const int ldq = (int)vw.q.r, lddo = (int)vw.dout.r;
+  const bf16* qb = q + vw.q.at(bh, vw.heads);
+  const bf16* dob = dout + vw.dout.at(bh, vw.heads);
+  const float* lseb = lse + (int64_t)bh * Sq;
+  const float* db = delta + (int64_t)bh * Sq;
+
+  // Granules first .. first + nh - 1 of the queries (granule x: rows
+  // 32 (first + x) ..). nh is even and at least 6: granules past the end of
+  // the queries arrive as zeros (Q, dO, lse and delta all 0) and add exact
+  // zeros, as the padded sweeps of attn_dkv_sw_kernel.
+  const int first = causal ? k0 / F::BG : 0;
+  int nh = max((Sq + F::BG - 1) / F::BG - first, 6);
+  nh += nh & 1;
+
+  const PpDma<G, true, F::kWaves> dma(wave, ldq);
+  const PpDma<G, true, F::kWaves> dma_do(wave, SAMEP ? ldq : lddo);
+  auto qslot = [&](int x) { return smem + (x & (F::kQSlots - 1)) * F::kSlotBytes; };
+  auto doslot = [&](int x) { return smem + F::kDoRing + ((x + F::kDoSlots) % F::kDoSlots) * F::kSlotBytes; };
+  char* const xring = smem + F::kXRing;
+  // P of granule h, pair p: chunk c (four queries) of lane L at xbuf(h) + p 4096 + c 1024 + 16 L.
+  auto xbuf = [&](int h) { return xring + (h & 1) * F::kXBytes + pair * 4096; };
+  // Step h's DMA instruction qd: Q and lse of granule h + 2, dO and delta of
+  // granule h + 1 (none past the sweep); rows past the end of the queries
+  // arrive as zeros (empty buffer range).
+  auto dma_part = [&](int h, int qd) {
+    const int xq = sched::dkv256_q_loaded(h), xd = sched::dkv256_do_loaded(h);
+    if (qd < F::kDma) {
+      if (xq < nh) dma.issue_one(qb, (first + xq) * F::BG, Sq, ldq, qslot(xq), qd);
+    } else if (qd < 2 * F::kDma) {
+      if (xd < nh)
+        (SAMEP ? dma : dma_do).issue_one(dob, (first + xd) * F::BG, Sq, SAMEP ? ldq : lddo, doslot(xd), qd - F::kDma);
+    } else if (pair == 0) {
+      if (role == 0) {
+        if (xq < nh) stat_dma(lseb, (first + xq) * F::BG, Sq, qslot(xq) + G::kBytes);
+      } else {
+        if (xd < nh) stat_dma(db, (first + xd) * F::BG, Sq, doslot(xd) + G::kBytes);
+      }
+    }
+  };
+  auto dma_at = [&](int h, int f) {
+    if (f < kStepDma) dma_part(h, f);
+  };
+
+  // Prologue: Q and lse of granule 0, and each wave's K (role A) or V (role
+  // B) rows by row-coalesced DMA into the staging, which the ring reaches
+  // only from step -1's loads on.
+  char* const rst = smem + F::kStage + wave * (32 * 2 * F::D);
+  {
+    const bf16* kvb = role == 0 ? k + vw.k.at(bh, vw.heads) : v + vw.v.at(bh, vw.heads);
+    dma_rows32<256>(kvb, k0w, Sk, role == 0 ? (int)vw.k.r : (int)vw.v.r, rst);
+#pragma unroll
+    for (int qd = 0; qd < F::kDma; ++qd) dma.issue_one(qb, first * F::BG, Sq, ldq, qslot(0), qd);
+    if (wave == 0) stat_dma(lseb, first * F::BG, Sq, qslot(0) + G::kBytes);
+  }
+
+  const Tile::Bases tb(lane);
+  const int trs = tb.t + 256 * slab;  // transposed reads of the slab's columns
+  auto tr_slab = [&](const char* sl, int hh, int uu) -> bf16x8 {
+    return tr_frag(sl + trs + Tile::tr_at(0, hh, uu), Tile::kTrHi);
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+
+  // Barrier opening step h: every load of step h - 1 is first read in step h.
+  auto sync = [&]() {
+    wait_vmem<0>();
+    lds_barrier();
+  };
+  bf16x8 kvf[KS];  // K rows (role A) or V rows (role B), all 256 columns
+  sync();
+  row_frags_lds<256>(kvf, rst);
+  // Every wave has its rows before step -1's loads overwrite the staging.
+  lds_barrier();
+
+  if (role == 0) {
+    // ---- role A: S, P, dV ----
+    f32x16 dva[SDT];
+#pragma unroll
+    for (int u = 0; u < SDT; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dva[u][r] = 0.f;
+    f32x16 sa[2];     // S of a granule (register r: query 16 g + r, key kvrow), by parity
+    bf16x8 pf[2][2];  // [parity][8-query chunk]: P fragments
+
+    auto stage = [&](auto P_, auto GRAD_, auto SG_, auto MASK_, auto SDP_, int h) __attribute__((always_inline)) {
+      constexpr int P = decltype(P_)::value;
+      constexpr bool GRAD = decltype(GRAD_)::value, SG = decltype(SG_)::value;
+      constexpr bool MASK = decltype(MASK_)::value, SDP = decltype(SDP_)::value;
+      const f32x16& sc = sa[P];
+      f32x16& sn = sa[1 - P];
+      bf16x8(&pc)[2] = pf[P];
+      const bf16x8(&pp)[2] = pf[1 - P];
+      const char* qn = qslot(h + 1);   // S of granule h + 1: Q rows
+      const char* dop = doslot(h - 1);  // dV of granule h - 1: dO^T, the slab's columns
+      constexpr int NS = SDP ? KS : 0;       // S: k-chunk i
+      constexpr int NG = GRAD ? 2 * SDT : 0;  // dV: output tile i / 2, query chunk i % 2
+      constexpr int NF = NS + NG;
+      auto read = [&](int f) -> bf16x8 {
+        if (f < NS) return *reinterpret_cast<const bf16x8*>(qn + Tile::row(tb, 0, f));
+        const int i = f - NS;
+        return tr_slab(dop, i & 1, i >> 1);
+      };
+      auto prod = [&](int f, const bf16x8& a) {
+        if (f < NS) {
+          if (f == 0)
+            sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kvf[0], f32x16{}, 0, 0, 0);
+          else
+            mma32(a, kvf[f], sn);
+        } else {
+          const int i = f - NS;
+          mma32(a, pp[i & 1], dva[i >> 1]);
+        }
+      };
+      // Softmax of granule h: element r (query 16 g + r of the granule).
+      const float* st = reinterpret_cast<const float*>(qslot(h) + G::kBytes) + 16 * g;
+      const int qh = (first + h) * F::BG + 16 * g;
+      char* const xw = xbuf(h) + 16 * lane;
+      f32x4 ls[2];
+      float pv[8];
+      f32x4 p4;
+      auto sg_elem = [&](int r) {
+        if ((r & 3) == 0 && (r >> 2) + 1 < 4) ls[((r >> 2) + 1) & 1] = *reinterpret_cast<const f32x4*>(st + 4 * ((r >> 2) + 1));
+        const f32x4& l4 = ls[(r >> 2) & 1];
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, -l4[r & 3] * kLog2e));
+        if constexpr (MASK) p = (causal && kvrow > qh + r) ? 0.f : p;
+        pv[r & 7] = p;
+        p4[r & 3] = p;
+        if ((r & 3) == 3) *reinterpret_cast<f32x4*>(xw + (r >> 2) * 1024) = p4;
+        if ((r & 7) == 7) {
+          to_frag(pv, pc[r >> 3]);
+          pin(pc[r >> 3]);
+        }
+      };
+      if constexpr (SG) ls[0] = *reinterpret_cast<const f32x4*>(st);
+      if constexpr (NF > 0) {
+        bf16x8 buf[NF];
+#pragma unroll
+        for (int f = 0; f < kAhead && f < NF; ++f) buf[f] = read(f);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          if (f + kAhead < NF) buf[f + kAhead] = read(f + kAhead);
+          // The step's loads go out first: they have one step to land.
+          dma_at(h, f);
+          prod(f, buf[f]);
+          if constexpr (SG && NG > 0) {
+            if (f >= NS) {
+#pragma unroll
+              for (int r = (f - NS) * (16 / NG); r < (f - NS + 1) * (16 / NG); ++r) sg_elem(r);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int f = 0; f < kStepDma; ++f) dma_at(h, f);
+      }
+      if constexpr (SG && NG == 0) {
+        // No dV products to hide it behind (step 0): the softmax last.
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sg_elem(r);
+      }
+    };
+    // Step h: GRAD (dV) for 1 <= h <= nh, SG for 0 <= h < nh, SDP (S) for
+    // h + 1 < nh; the mask covers granules 0 .. 3 (the diagonal block).
+    stage(P1(), F_(), F_(), F_(), T_(), -1);
+    sync();
+    stage(P0(), F_(), T_(), T_(), T_(), 0);
+    sync();
+    stage(P1(), T_(), T_(), T_(), T_(), 1);
+    sync();
+    stage(P0(), T_(), T_(), T_(), T_(), 2);
+    sync();
+    stage(P1(), T_(), T_(), T_(), T_(), 3);
+    sync();
+    stage(P0(), T_(), T_(), F_(), T_(), 4);
+    for (int h = 5; h + 1 <= nh - 2; h += 2) {
+      sync();
+      stage(P1(), T_(), T_(), F_(), T_(), h);
+      sync();
+      stage(P0(), T_(), T_(), F_(), T_(), h + 1);
+    }
+    sync();
+    stage(P1(), T_(), T_(), F_(), F_(), nh - 1);
+    sync();
+    stage(P0(), T_(), F_(), F_(), F_(), nh);
+    wait_vmem<0>();
+    lds_barrier();  // as role B's: whole-row stores through LDS
+    if (k0w >= Sk) return;
+    store_acc_rows_lds<128>(dva, smem + wave * (32 * 256), dv + vw.dv.at(bh, vw.heads) + 128 * slab, k0w, Sk, 1.0f,
+                            vw.dv.r);
+  } else {
+    // ---- role B: dP, dS, dK ----
+    f32x16 dka[SDT];
+#pragma unroll
+    for (int u = 0; u < SDT; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dka[u][r] = 0.f;
+    f32x16 dpa[2];  // dP of a granule, by parity
+    bf16x8 dsf[2];  // dS fragments of the granule the step's dK products use
+
+    auto stage = [&](auto P_, auto SDP_, auto SG_, auto GRAD_, int h) __attribute__((always_inline)) {
+      constexpr int P = decltype(P_)::value;
+      constexpr bool SDP = decltype(SDP_)::value, SG = decltype(SG_)::value, GRAD = decltype(GRAD_)::value;
+      f32x16& dpn = dpa[P];            // dP of granule h
+      const f32x16& dpc = dpa[1 - P];  // dP of granule h - 1
+      const char* doc = doslot(h);     // dP of granule h: dO rows
+      const char* qp = qslot(h - 1);   // dK of granule h - 1: Q^T, the slab's columns
+      constexpr int NS = SDP ? KS : 0;        // dP: k-chunk i
+      constexpr int NG = GRAD ? 2 * SDT : 0;  // dK: output tile i / 2, query chunk i % 2
+      constexpr int NF = NS + NG;
+      auto read = [&](int f) -> bf16x8 {
+        if (f < NS) return *reinterpret_cast<const bf16x8*>(doc + Tile::row(tb, 0, f));
+        const int i = f - NS;
+        return tr_slab(qp, i & 1, i >> 1);
+      };
+      auto prod = [&](int f, const bf16x8& a) {
+        if (f < NS) {
+          if (f == 0)
+            dpn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kvf[0], f32x16{}, 0, 0, 0);
+          else
+            mma32(a, kvf[f], dpn);
+        } else {
+          const int i = f - NS;
+          mma32(a, dsf[i & 1], dka[i >> 1]);
+        }
+      };
+      // dS of granule h - 1: element r (query 16 g + r), P from A's step h - 1.
+      const float* st = reinterpret_cast<const float*>(doslot(h - 1) + G::kBytes) + 16 * g;
+      const char* xr = xbuf(h - 1) + 16 * lane;
+      f32x4 dl[2], px[2];
+      float dsv[8];
+      auto sg_elem = [&](int r) {
+        if ((r & 3) == 0 && (r >> 2) + 1 < 4) {
+          const int c = (r >> 2) + 1;
+          dl[c & 1] = *reinterpret_cast<const f32x4*>(st + 4 * c);
+          px[c & 1] = *reinterpret_cast<const f32x4*>(xr + c * 1024);
+        }
+        const float p = px[(r >> 2) & 1][r & 3];
+        dsv[r & 7] = p * (dpc[r] - dl[(r >> 2) & 1][r & 3]);
+        if ((r & 7) == 7) {
+          to_frag(dsv, dsf[r >> 3]);
+          pin(dsf[r >> 3]);
+        }
+      };
+      if constexpr (SG) {
+        dl[0] = *reinterpret_cast<const f32x4*>(st);
+        px[0] = *reinterpret_cast<const f32x4*>(xr);
+      }
+      if constexpr (SG && NS == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sg_elem(r);
+      }
+      if constexpr (NF > 0) {
+        bf16x8 buf[NF];
+#pragma unroll
+        for (int f = 0; f < kAhead && f < NF; ++f) buf[f] = read(f);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          if (f + kAhead < NF) buf[f + kAhead] = read(f + kAhead);
+          dma_at(h, f);
+          prod(f, buf[f]);
+          if constexpr (SG && NS > 0) {
+            if (f < NS) {
+#pragma unroll
+              for (int r = f * (16 / NS); r < (f + 1) * (16 / NS); ++r) sg_elem(r);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int f = 0; f < kStepDma; ++f) dma_at(h, f);
+      }
+    };
+    // Step h: SDP (dP) for 0 <= h < nh, SG (dS) and GRAD (dK) for 1 <= h <= nh.
+    stage(P1(), F_(), F_(), F_(), -1);
+    sync();
+    stage(P0(), T_(), F_(), F_(), 0);
+    for (int h = 1; h + 1 <= nh - 1; h += 2) {
+      sync();
+      stage(P1(), T_(), T_(), T_(), h);
+      sync();
+      stage(P0(), T_(), T_(), T_(), h + 1);
+    }
+    sync();
+    stage(P1(), T_(), T_(), T_(), nh - 1);
+    sync();
+    stage(P0(), F_(), T_(), T_(), nh);
+    wait_vmem<0>();
+    // Whole-row stores through LDS, each wave in its own 8 KB; the barrier
+    // (role A passes one too) keeps the other waves' last reads off it.
+    static_assert(8 * 32 * 256 <= Dkv256::kLds, "every wave's rows fit the ring");
+    lds_barrier();
+    if (k0w >= Sk) return;
+    store_acc_rows_lds<128>(dka, smem + wave * (32 * 256), dk + vw.dk.at(bh, vw.heads) + 128 * slab, k0w, Sk, scale,
+                            vw.dk.r);
+  }
+}
+
 // W waves of 32 queries; SLOTS K/V tile slots in LDS (3: tiles t + 1 and t + 2
 // load while tile t is used; 2: only t + 1, which halves the LDS so that two
 // workgroups share a CU).
@@ -3802,6 +4217,24 @@ int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout,
   }
 }
 
+// bf16 dK/dV at head dim 256 (d == 256, 16-byte aligned rows): the role
+// split on 128-column slabs, two workgroups per key block of 128.
+int dkv256_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
+                  void* dk, void* dv, const Shape& s, int causal, float scale, hipStream_t stream) {
+  typedef Dkv256 F;
+  const int64_t nk = cdiv(s.sk, F::BKV);
+  const int64_t bh = s.b * s.h;
+  if (2 * nk * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dkv: grid too large");
+  const AttnViews vw = dense_views(s);
+  auto kern = attn_dkv_rs256_kernel<true>;
+  if (int rc = set_lds(kern, F::kLds, stream)) return rc;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(2 * nk * bh)), dim3(F::kThreads), F::kLds, stream,
+                     static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
+                     static_cast<const bf16*>(dout), lse, delta, static_cast<bf16*>(dk), static_cast<bf16*>(dv),
+                     (int)bh, (int)s.sq, (int)s.sk, causal, scale, scale * kLog2e, vw);
+  return check_launch("ferrite_flash_attention_bwd_dkv");
+}
+
 template <typename T, int D, bool AL>
 int dkv_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
                void* dk, void* dv, const Shape& s, int causal, float scale, hipStream_t stream, void* ws = nullptr,
@@ -3974,6 +4407,8 @@ extern "C" int ferrite_hip_attn_bwd_dkv_ex(const void* q, const void* k, const v
   const bool al = d % (dtype == FERRITE_BF16 ? 8 : 4) == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
                   aligned16(dout) && aligned16(dk) && aligned16(dv);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d == 256 && dtype == FERRITE_BF16 && al)
+    return dkv256_launch(q, k, v, dout, lse, delta, dk, dv, s, causal, scale, st);
   if (d > 128) FERRITE_WIDE(dkv_wide_launch, dtype, al, q, k, v, dout, lse, delta, dk, dv, s, causal, scale, st);
 #define FERRITE_DISPATCH_256(LAUNCH, T, aligned, ...) \
   return fail(FERRITE_ERR_INVALID_ARGUMENT, "unreachable head_dim")

@@ -83,7 +83,7 @@ def test_backward_matches_reference(dev, causal, s, d, bs):
 @pytest.mark.parametrize("d", [128, 256, 512])
 def test_backward_bf16_is_close(dev, d):
     """tests/test_flash_attention.py:50-58: loss = sum(f32(out)^2), relative Frobenius < 5e-2
-    (d = 128 as there; 256 and 512 run the slab-wise backward)."""
+    (d = 128 as there; 256 runs the pipelined bf16 kernels, 512 the slab-wise backward)."""
     q, k, v = _qkv(10, (1, 2, 256, d), "bf16")
     qt, kt, vt = (to_dev(a, "bf16", dev).requires_grad_() for a in (q, k, v))
     (flash_attention(qt, kt, vt, causal=True).float() ** 2).sum().backward()
@@ -316,8 +316,9 @@ def test_split_long_context_backward(dev, b, h, s, d, fused):
 ])
 def test_backward_d256_bf16(dev, b, h, sq, sk, causal, fused):
     """The bf16 backward at head dim 256 through the C ABI (the pipelined dQ kernel with four waves
-    and a two-slot K/V ring): dQ, dK, dV against the oracle at 2e-2 or twice the reference's own bf16
-    recipe's error, every output written (NaN prefill), in both backward orders."""
+    and a two-slot K/V ring; dK/dV as the role split on 128-column slabs over 32-query granules):
+    dQ, dK, dV against the oracle at 2e-2 or twice the reference's own bf16 recipe's error, every
+    output written (NaN prefill), in both backward orders."""
     _abi_case(dev, b, h, sq, sk, 256, "bf16", causal, seed=71 + sq, scale=256 ** -0.5, fused=fused)
 
 
