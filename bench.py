@@ -293,6 +293,33 @@ def bench_stream_ceilings(nbytes: int = 1 << 30, iters: int = 10):
             "copy_frac_of_peak": copy / PEAK_HBM_GBS}
 
 
+def bench_mfma_ceiling(iters_per_launch: int = 4096, launches: int = 10):
+    """What this part's matrix pipes sustain on bf16: ferrite_hip_mfma_ceiling (every wave streams
+    independent v_mfma_f32_32x32x16_bf16 on register operands, no memory traffic) at one and two
+    waves per SIMD and one and two workgroups per CU, each launch ~1 ms, after the bench's
+    clock settling; the best rate is the ceiling of an MFMA-bound kernel on this part, as the
+    stream kernels give the HBM one."""
+    import torch
+
+    from ferrite import _hip
+
+    lib, st = _hip.lib(), torch.cuda.current_stream().cuda_stream
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.empty(2 * cus * 8, dtype=torch.float32, device="cuda:0")
+    rates = {}
+    for waves in (4, 8):
+        for per_cu in (1, 2):
+            blocks = per_cu * cus
+            run = lambda: _hip.check(lib.ferrite_hip_mfma_ceiling(sink.data_ptr(), blocks, waves,  # noqa: E731
+                                                                   iters_per_launch, st), "mfma_ceiling")
+            _settle(run, 0.1)
+            t = _events_time(run, launches, 1)
+            rates[f"waves{waves}_x{per_cu}"] = blocks * waves * iters_per_launch * 8 * 32768 / t / 1e12
+    best = max(rates.values())
+    return {"bf16_tflops": best, "frac_of_spec_peak": best / PEAK_BF16_TFLOPS, "by_config": rates,
+            "flops_per_launch_per_wave": iters_per_launch * 8 * 32768}
+
+
 def bench_rmsnorm(rows, dim, steps, warmup, sets=24):
     """add+RMSNorm over `sets` rotating buffer sets (24 x 33.5 MB = 805 MB > the 256 MB MALL),
     launched through a captured HIP graph so host launch cost does not pace the ~7 us kernels.
@@ -611,9 +638,16 @@ def main(argv=None):
         kernels["attention"] = bench_attention(4, 16, 2048, 128, a.steps, a.warmup)
         kernels["attention_long_context"] = bench_attention(1, 8, 8192, 64, max(a.steps // 2, 3), 2, seed=27)
         kernels["attention_fwd_parts"] = bench_attention_fwd_parts(max(a.steps // 2, 5), 2)
-        # Head dim 256 (the reference's tests run it), at the headline's FLOPs: the forward on the
-        # pipelined four-wave kernel, the backward on the 128-column slab kernels.
+        # Head dim 256 (the reference's tests run it), at the headline's FLOPs: the forward and dQ on
+        # the pipelined four-wave kernels, dK/dV on the role split over 128-column output slabs.
         kernels["attention_d256"] = bench_attention(4, 8, 2048, 256, max(a.steps // 5, 3), 2, seed=31)
+        # The bf16 rate a pure MFMA stream sustains on this part, and each attention line against it.
+        ceil = bench_mfma_ceiling()
+        kernels["mfma_ceiling"] = ceil
+        for key in ("attention", "attention_long_context", "attention_d256"):
+            r = kernels[key]
+            r["fwd_frac_of_measured_mfma_ceiling"] = r["fwd_tflops"] / ceil["bf16_tflops"]
+            r["bwd_frac_of_measured_mfma_ceiling"] = r["bwd_tflops"] / ceil["bf16_tflops"]
     if a.only in ("rmsnorm", "all"):
         kernels["add_rmsnorm"] = bench_rmsnorm(4096, 1024, a.steps, a.warmup)
         ceil = bench_stream_ceilings()

@@ -694,6 +694,39 @@ __global__ __launch_bounds__(64 * W, W == 8 ? 2 : 1) void gemm_dma_kernel(const 
 
 // out = sum over the K slices of the f32 partial slabs, in slice order
 // (deterministic), cast to TO. MN % 4 == 0.
+// The part's bf16 MFMA ceiling: every wave streams v_mfma_f32_32x32x16_bf16
+// over eight independent accumulators (a product waits for its own
+// accumulator only every eighth instruction, past the instruction's latency)
+// with register operands, no memory traffic and no other work. Operands are
+// varied bf16 values (not zeros or constants), so the matrix pipes switch as
+// they do on real data; the clock that load sustains sets the rate. Each wave
+// writes one float of its accumulators to sink so nothing is dead code.
+__global__ __launch_bounds__(512, 1) void mfma_ceiling_kernel(float* __restrict__ sink, int iters) {
+  const int lane = threadIdx.x & 63;
+  bf16x8 a, b;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t hsh = (uint32_t)(lane * 8 + e + 1) * 2654435761u;
+    a[e] = (bf16)((float)((hsh >> 8) & 0xffff) * (1.0f / 65536.0f) - 0.5f);
+    b[e] = (bf16)((float)((hsh >> 16) & 0xff) * (1.0f / 256.0f) - 0.5f);
+  }
+  f32x16 acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+  }
+  float t = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) t += acc[j][r];
+  if (lane == 0) sink[blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)] = t;
+}
+
 template <typename TO, int EPI = kEpiNone>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, TO* __restrict__ out,
                                                                 int64_t mn, int slices, bf16* __restrict__ aux) {
@@ -1015,4 +1048,16 @@ extern "C" int ferrite_hip_matmul_gelu(const void* x, const void* y, void* out, 
 extern "C" int ferrite_hip_matmul(const void* x, const void* y, void* out, int64_t m, int64_t n, int64_t k,
                                   int in_dtype, int out_dtype, void* stream) {
   return ferrite_hip_matmul_ex(x, y, out, m, n, k, 0, 0, in_dtype, out_dtype, nullptr, 0, stream);
+}
+
+extern "C" int ferrite_hip_mfma_ceiling(float* sink, int blocks, int waves, int iters, void* stream) {
+  using namespace ferrite;
+  if (blocks < 1 || blocks > 65536 || (waves != 4 && waves != 8) || iters < 1 || iters > (1 << 24))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT,
+                "ferrite_hip_mfma_ceiling: need 1 <= blocks <= 65536, waves 4 or 8, 1 <= iters <= 2^24");
+  if (!sink || (reinterpret_cast<uintptr_t>(sink) & 3))
+    return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_mfma_ceiling: null or unaligned sink");
+  hipLaunchKernelGGL(mfma_ceiling_kernel, dim3((unsigned)blocks), dim3(64 * waves), 0, static_cast<hipStream_t>(stream),
+                     sink, iters);
+  return check_launch("ferrite_hip_mfma_ceiling");
 }

@@ -47,6 +47,7 @@ SIGNATURES: dict[str, tuple] = {
     "ferrite_hip_stream_copy2": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _vp]),
     "ferrite_hip_stream_read": (_c_int, [_vp, _c_i64, _vp, _c_int, _vp]),
     "ferrite_hip_stream_fill": (_c_int, [_vp, _c_i64, ctypes.c_uint32, _c_int, _vp]),
+    "ferrite_hip_mfma_ceiling": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp]),
     "ferrite_hip_matmul": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _vp]),
     "ferrite_hip_matmul_workspace": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_int]),
     "ferrite_hip_matmul_ex": (

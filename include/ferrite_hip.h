@@ -153,6 +153,16 @@ int ferrite_hip_stream_read(const void* a, int64_t bytes, void* sink, int blocks
 int ferrite_hip_stream_fill(void* out, int64_t bytes, uint32_t value, int blocks, void* stream);
 
 /*
+ * The matrix-pipe counterpart of those ceilings, with no counterpart in the
+ * reference: `blocks` workgroups of `waves` (4 or 8: one or two per SIMD) each
+ * issue `iters` x 8 v_mfma_f32_32x32x16_bf16 (32768 FLOPs each) over eight
+ * independent accumulators of register operands, with no memory traffic.
+ * bench.py times it as the bf16 MFMA rate this part sustains. Each wave writes
+ * one float to sink[blocks * waves]. 1 <= blocks <= 65536, 1 <= iters <= 2^24.
+ */
+int ferrite_hip_mfma_ceiling(float* sink, int blocks, int waves, int iters, void* stream);
+
+/*
  * out[M, N] = x[M, K] @ y[K, N] with f32 accumulation (matmul.py:27-38, :52-86).
  * in_dtype FERRITE_BF16 uses bf16 MFMA; FERRITE_F32 uses fp32 MFMA (true fp32
  * products, the reference's Precision.HIGHEST, _compat.py:17-25). Ragged shapes

@@ -25,7 +25,7 @@ def _declared_symbols():
 
 def test_library_exports_every_declared_symbol():
     declared = _declared_symbols()
-    assert len(declared) == 35
+    assert len(declared) == 36
     out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH], capture_output=True, text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s(\w+)", out))
     missing = [s for s in declared if s not in exported]
@@ -183,6 +183,11 @@ def test_stream_kernels_argument_checks():
     assert lib.ferrite_hip_stream_fill(None, 32, 1, 0, None) == 1
     assert "null" in _hip.last_error()
     assert lib.ferrite_hip_stream_fill(None, 0, 1, 0, None) == 0
+    assert lib.ferrite_hip_mfma_ceiling(None, 256, 8, 16, None) == 1
+    assert "sink" in _hip.last_error()
+    assert lib.ferrite_hip_mfma_ceiling(None, 256, 6, 16, None) == 1
+    assert "waves 4 or 8" in _hip.last_error()
+    assert lib.ferrite_hip_mfma_ceiling(None, 0, 8, 16, None) == 1
 
 
 def test_forward_workspace_query():

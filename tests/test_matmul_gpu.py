@@ -282,3 +282,37 @@ def test_four_wave_tiles_match_eight_wave_tiles(dev, x_t, y_t):
     absb = np.abs(a[rows]).astype(np.float64) @ np.abs(b).astype(np.float64)
     got = to_np(big)[rows].astype(np.float64)
     assert np.all(np.abs(got - exact) <= bf16_ulp(exact) + 2.0**-20 * absb + 1e-30)
+
+
+def _ceiling_operands():
+    """The bf16 operands every lane of ferrite_hip_mfma_ceiling builds, as A[32, 16] and B[16, 32]
+    of v_mfma_f32_32x32x16_bf16 (lane l holds A[l % 32, 8 (l // 32) + e] and B[8 (l // 32) + e, l % 32])."""
+    from oracle.bf16 import round_bf16
+
+    A = np.zeros((32, 16)); B = np.zeros((16, 32))
+    for lane in range(64):
+        for e in range(8):
+            h = ((lane * 8 + e + 1) * 2654435761) & 0xFFFFFFFF
+            av = round_bf16(np.float32(((h >> 8) & 0xFFFF) * (1.0 / 65536.0) - 0.5))
+            bv = round_bf16(np.float32(((h >> 16) & 0xFF) * (1.0 / 256.0) - 0.5))
+            A[lane % 32, 8 * (lane // 32) + e] = av
+            B[8 * (lane // 32) + e, lane % 32] = bv
+    return A, B
+
+
+@pytest.mark.parametrize("waves,blocks,iters", [(8, 256, 64), (4, 512, 16)])
+def test_mfma_ceiling_runs_its_products(dev, waves, blocks, iters):
+    """The MFMA ceiling bench.py times does the products it is credited with: lane 0 of every wave
+    leaves the sum of its accumulators, iters x 8 x (rows 8 (r // 4) + r % 4 of column 0 of A B),
+    in sink, the same in every wave."""
+    lib = _hip.lib()
+    sink = torch.full((blocks * waves,), float("nan"), device=dev)
+    _hip.check(lib.ferrite_hip_mfma_ceiling(sink.data_ptr(), blocks, waves, iters, _hip.stream_of(sink)), "ceiling")
+    torch.cuda.synchronize()
+    got = to_np(sink)
+    A, B = _ceiling_operands()
+    D = A @ B
+    rows = [8 * (r // 4) + (r % 4) for r in range(16)]
+    want = iters * 8 * D[rows, 0].sum()
+    assert np.all(got == got[0]), "every wave computes the same sum"
+    assert abs(got[0] - want) <= 1e-4 * iters * 8 * np.abs(D[rows, 0]).sum() + 1e-6, (got[0], want)
