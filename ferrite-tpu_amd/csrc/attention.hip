@@ -328,11 +328,13 @@ __device__ __forceinline__ void row_frags_lds(bf16x8 (&f)[D / 16], const char* s
 // whole rows, 2D / 16 lanes per row. The caller keeps other waves' reads and
 // DMA off the region; one wave's LDS writes and reads are processed in order.
 // Rows row0 + r at or past nrows are skipped.
-template <int D>
+// FRESH: the lane from lane_id() (see there), for kernels at their register
+// limit whose lane terms would otherwise cross their stage loop.
+template <int D, bool FRESH = false>
 __device__ __forceinline__ void store_acc_rows_lds(const f32x16 (&acc)[D / 32], char* lds, bf16* __restrict__ out,
                                                    int64_t row0, int64_t nrows, float mul, int64_t ld) {
   constexpr int kRowBytes = 2 * D, kCh = kRowBytes / 16, kRowsPerInst = 64 / kCh;
-  const int lane = threadIdx.x & 63, l32 = lane & 31, g = lane >> 5;
+  const int lane = FRESH ? lane_id() : (int)(threadIdx.x & 63), l32 = lane & 31, g = lane >> 5;
 #pragma unroll
   for (int u = 0; u < D / 32; ++u)
 #pragma unroll
@@ -965,8 +967,9 @@ __device__ __forceinline__ f32x2 xget2(const float* p) {
                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 // Offset (floats) of register pair r2 of accumulator tile `tile` (a wave's
-// f32x16 tiles numbered by the caller) in a share laid out as above.
-__device__ __forceinline__ int xat(int tile, int r2) { return (tile * 8 + r2) * 128 + 2 * (threadIdx.x & 63); }
+// f32x16 tiles numbered by the caller) in a share laid out as above, for the
+// wave's lane `lane`.
+__device__ __forceinline__ int xat(int tile, int r2, int lane) { return (tile * 8 + r2) * 128 + 2 * lane; }
 // Every wave's stores of its share have reached memory; then one count per
 // workgroup (the pair's count is even before a launch and each launch adds
 // two). True for the second of the pair to arrive, which merges; called by
@@ -1051,6 +1054,10 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   // One segment, inlined once per call below (a loop over the segments left
   // the register allocation of the key-split kernel with spills).
   auto segment = [&](const int qt, const int t0, const int t1, const int role) __attribute__((always_inline)) {
+  // With SPLIT (two segments, 128 VGPRs), the lane terms are formed per
+  // segment: nothing lane-derived from the first segment stays live (or
+  // spills) across the second one's stage loop.
+  const int lane = SPLIT ? lane_id() : (int)(threadIdx.x & 63), l32 = lane & 31, g = lane >> 5;
   const int q0 = qt * F::BQ;
   const int q0w = q0 + 32 * RB * wr;
   // Tiles of 64 keys: n for the workgroup, n_w for this wave, whose last
@@ -1112,16 +1119,26 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   const int kbase = KT::off(32 * kh + l32, g * 16);
   const int vbase = VT::off((lane >> 5) * 16 + ((lane & 15) >> 2), 2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
   // Diagonal tile: key kt*32 + g*16 + r of the tile is invisible to row
-  // rb*32 + l32 of the wave when r > lim[rb][kt].
+  // rb*32 + l32 of the wave when r > lim_at(lane, rb, kt).
   // With SPLIT, a wave whose last tile of the segment lies below its diagonal
   // sees all of it: a uniform offset lifts every limit out of reach (nwf and
   // tt1 are 0 without SPLIT).
+  // With SPLIT the limits are formed in the masked stage from lane_id()
+  // (formed here, they would stay live across the stage loop and spill).
   const int lim_lift = SPLIT && nwf > tt1 ? 1 << 20 : 0;
   int lim[RB][2];
+  if constexpr (!SPLIT) {
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) lim[rb][kt] = q0w % F::BK + rb * 32 + l32 - kt * 32 - g * 16 + lim_lift;
+      for (int kt = 0; kt < 2; ++kt) lim[rb][kt] = q0w % F::BK + rb * 32 + l32 - kt * 32 - g * 16;
+  }
+  auto lim_at = [&](int ln, int rb, int kt) {
+    if constexpr (SPLIT)
+      return q0w % F::BK + rb * 32 + (ln & 31) - kt * 32 - (ln >> 5) * 16 + lim_lift;
+    else
+      return lim[rb][kt];
+  };
 
   f32x16 acc[RB][DT];  // O^T per row block: register r of tile u = dim u*32 + (r/4)*8 + g*4 + r%4
 #pragma unroll
@@ -1208,6 +1225,7 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
         mma32(a, pp[rb][cl], acc[rb][u]);
       }
     };
+    const int ln_mask = SPLIT && MASK ? lane_id() : 0;  // the lane for the diagonal's limits
     float t[RB][2];  // [row block][partial] sums of this tile's p in the lane
     // Softmax element e of the lane: row block e / (16 NKT), key subtile
     // (e / 16) % NKT of the wave's (kt + kh of the tile), register e % 16.
@@ -1216,7 +1234,7 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
     auto softmax_elem = [&](int e, const float(&nm)[RB]) {
       const int rb = e / (16 * NKT), kt = (e >> 4) % NKT, r = e & 15;
       float x = sc[kt][rb][r];
-      if constexpr (MASK) x = r > lim[rb][kt + kh] ? -INFINITY : x;
+      if constexpr (MASK) x = r > lim_at(ln_mask, rb, kt + kh) ? -INFINITY : x;
       p[r & 7] = __builtin_amdgcn_exp2f(__builtin_fmaf(x, scale_log2, nm[rb]));
       t[rb][r & 1] += p[r & 7];
       if ((r & 7) == 7) {
@@ -1289,7 +1307,7 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               float x = sc[kt][rb][r];
-              if constexpr (MASK) x = r > lim[rb][kt + kh] ? -INFINITY : x;
+              if constexpr (MASK) x = r > lim_at(ln_mask, rb, kt + kh) ? -INFINITY : x;
               mx = fmaxf(mx, x);
             }
           const float m_new = fmaxf(m[rb], lane32_max(mx) * scale_log2);
@@ -1393,6 +1411,9 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   }
   wait_vmem<0>();
 
+  // With SPLIT, the epilogue's lane terms from lane_id() (nothing lane-derived
+  // stays live across the stage loop).
+  const int lane_e = SPLIT ? lane_id() : lane, l32_e = lane_e & 31, g_e = lane_e >> 5;
   if constexpr (KSPLIT > 1) {
     // The upper key half hands its accumulators, maxima and partial sums to
     // the lower half of its rows through the (now idle) rings; the lower half
@@ -1407,15 +1428,15 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
       for (int u = 0; u < DT; ++u)
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4)
-          *reinterpret_cast<f32x4*>(xs + ((u * 4 + r4) * 64 + lane) * 4) =
+          *reinterpret_cast<f32x4*>(xs + ((u * 4 + r4) * 64 + lane_e) * 4) =
               f32x4{acc[0][u][4 * r4], acc[0][u][4 * r4 + 1], acc[0][u][4 * r4 + 2], acc[0][u][4 * r4 + 3]};
-      xs[16 * DT * 64 + lane] = m[0];
-      xs[16 * DT * 64 + 64 + lane] = lsum[0];
+      xs[16 * DT * 64 + lane_e] = m[0];
+      xs[16 * DT * 64 + 64 + lane_e] = lsum[0];
     }
     lds_barrier();
     if (kh == 0) {
-      const float m1 = xs[16 * DT * 64 + lane];
-      const float l1 = xs[16 * DT * 64 + 64 + lane];
+      const float m1 = xs[16 * DT * 64 + lane_e];
+      const float l1 = xs[16 * DT * 64 + 64 + lane_e];
       const float mm = fmaxf(m[0], m1);
       float a0 = __builtin_amdgcn_exp2f(m[0] - mm), a1 = __builtin_amdgcn_exp2f(m1 - mm);
       if (SPLIT && mm == -INFINITY) a0 = a1 = 0.f;  // neither half saw a key of the segment
@@ -1423,7 +1444,7 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
       for (int u = 0; u < DT; ++u)
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
-          const f32x4 o1 = *reinterpret_cast<const f32x4*>(xs + ((u * 4 + r4) * 64 + lane) * 4);
+          const f32x4 o1 = *reinterpret_cast<const f32x4*>(xs + ((u * 4 + r4) * 64 + lane_e) * 4);
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[0][u][4 * r4 + e] = acc[0][u][4 * r4 + e] * a0 + o1[e] * a1;
         }
@@ -1451,15 +1472,15 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
 #pragma unroll
         for (int u = 0; u < DT; ++u)
 #pragma unroll
-          for (int r2 = 0; r2 < 8; ++r2) xput2(part + xat(wr * DT + u, r2), acc[0][u][2 * r2], acc[0][u][2 * r2 + 1]);
-        if (g == 0) xput2(part + kAccFloats + 2 * (32 * wr + l32), m[0], lrow[0]);
+          for (int r2 = 0; r2 < 8; ++r2) xput2(part + xat(wr * DT + u, r2, lane_e), acc[0][u][2 * r2], acc[0][u][2 * r2 + 1]);
+        if (g_e == 0) xput2(part + kAccFloats + 2 * (32 * wr + l32_e), m[0], lrow[0]);
       }
       // The first of A and B to arrive is done with the long tile.
       if (!pair_arrive_second(count)) return;
       if (writer) {
         // Merge in role order whichever block runs it: A (keys before the
         // split), then B.
-        const f32x2 st = xget2(other + kAccFloats + 2 * (32 * wr + l32));
+        const f32x2 st = xget2(other + kAccFloats + 2 * (32 * wr + l32_e));
         const float mo = st[0], lo = st[1];
         const float ma = role == 0 ? m[0] : mo, mb = role == 0 ? mo : m[0];
         const float la = role == 0 ? lrow[0] : lo, lb = role == 0 ? lo : lrow[0];
@@ -1469,7 +1490,7 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
         for (int u = 0; u < DT; ++u)
 #pragma unroll
           for (int r2 = 0; r2 < 8; ++r2) {
-            const f32x2 oo = xget2(other + xat(wr * DT + u, r2));
+            const f32x2 oo = xget2(other + xat(wr * DT + u, r2, lane_e));
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
               const float mine = acc[0][u][2 * r2 + e];
@@ -1490,10 +1511,10 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
     if (!writer) return;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      const int row = q0w + 32 * rb + l32;
+      const int row = q0w + 32 * rb + l32_e;
       const float l = lrow[rb];
       store_acc_rows<bf16, D, true>(acc[rb], o + vw.o.at(bh, vw.heads), row, S, d, 1.0f / l, vw.o.r);
-      if (g == 0 && row < S) lse[(int64_t)bh * S + row] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
+      if (g_e == 0 && row < S) lse[(int64_t)bh * S + row] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
     }
     return;
   }
@@ -1507,11 +1528,11 @@ __global__ __launch_bounds__((FwdW<D, RB, W, KSPLIT>::kThreads), (KSPLIT > 1 ? 4
   char* const ot = smem + wave * (32 * RB * 2 * D);
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    const int row = q0w + 32 * rb + l32;
+    const int row = q0w + 32 * rb + l32_e;
     const float l = lrow[rb];
-    if (g == 0 && row < S) lse[(int64_t)bh * S + row] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
-    store_acc_rows_lds<D>(acc[rb], ot + rb * 32 * 2 * D, o + vw.o.at(bh, vw.heads), q0w + 32 * rb, S, 1.0f / l,
-                          vw.o.r);
+    if (g_e == 0 && row < S) lse[(int64_t)bh * S + row] = (m[rb] + __builtin_amdgcn_logf(l)) * kLn2;
+    store_acc_rows_lds<D, SPLIT>(acc[rb], ot + rb * 32 * 2 * D, o + vw.o.at(bh, vw.heads), q0w + 32 * rb, S,
+                                 1.0f / l, vw.o.r);
   }
   };  // segment
 
@@ -2728,16 +2749,16 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
       for (int u = 0; u < DT; ++u)
 #pragma unroll
         for (int r2 = 0; r2 < 8; ++r2) {
-          xput2(part + xat((wave * 2 + 0) * DT + u, r2), dka[u][2 * r2], dka[u][2 * r2 + 1]);
-          xput2(part + xat((wave * 2 + 1) * DT + u, r2), dva[u][2 * r2], dva[u][2 * r2 + 1]);
+          xput2(part + xat((wave * 2 + 0) * DT + u, r2, lane), dka[u][2 * r2], dka[u][2 * r2 + 1]);
+          xput2(part + xat((wave * 2 + 1) * DT + u, r2, lane), dva[u][2 * r2], dva[u][2 * r2 + 1]);
         }
       if (!pair_arrive_second(reinterpret_cast<int*>(ws) + slot_id)) return;
 #pragma unroll
       for (int u = 0; u < DT; ++u)
 #pragma unroll
         for (int r2 = 0; r2 < 8; ++r2) {
-          const f32x2 ok = xget2(other + xat((wave * 2 + 0) * DT + u, r2));
-          const f32x2 ov = xget2(other + xat((wave * 2 + 1) * DT + u, r2));
+          const f32x2 ok = xget2(other + xat((wave * 2 + 0) * DT + u, r2, lane));
+          const f32x2 ov = xget2(other + xat((wave * 2 + 1) * DT + u, r2, lane));
 #pragma unroll
           for (int e = 0; e < 2; ++e) {
             dka[u][2 * r2 + e] += ok[e];
@@ -3847,7 +3868,7 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : D > 128 ? 1 : 2)) void 
 #pragma unroll
           for (int u = 0; u < F::DT; ++u)
 #pragma unroll
-            for (int r2 = 0; r2 < 8; ++r2) xput2(part + xat(wr * F::DT + u, r2), acc[u][2 * r2], acc[u][2 * r2 + 1]);
+            for (int r2 = 0; r2 < 8; ++r2) xput2(part + xat(wr * F::DT + u, r2, lane), acc[u][2 * r2], acc[u][2 * r2 + 1]);
         }
         if (!pair_arrive_second(reinterpret_cast<int*>(ws) + slot_id)) return;
         if (kh == 0) {
@@ -3855,7 +3876,7 @@ __global__ __launch_bounds__((64 * W), (KSPLIT > 1 ? 4 : D > 128 ? 1 : 2)) void 
           for (int u = 0; u < F::DT; ++u)
 #pragma unroll
             for (int r2 = 0; r2 < 8; ++r2) {
-              const f32x2 oo = xget2(other + xat(wr * F::DT + u, r2));
+              const f32x2 oo = xget2(other + xat(wr * F::DT + u, r2, lane));
               acc[u][2 * r2] += oo[0];
               acc[u][2 * r2 + 1] += oo[1];
             }

@@ -134,6 +134,17 @@ __device__ __forceinline__ void dma16(const u32x4& rsrc, char* lds, uint32_t vof
                : "memory", "m0");
 }
 
+// The lane (0-63), formed where it is called: two mbcnt instructions in a
+// volatile asm, which the compiler neither merges with another call nor hoists.
+// Code after a kernel's main loop (or in a later work segment) that takes its
+// lane terms from here keeps nothing lane-derived live (or spilled) across the
+// loop; the thread index would be one value for the whole kernel.
+__device__ __forceinline__ int lane_id() {
+  int lane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+  return lane;
+}
+
 // Swap with the lane 32 away (gfx950 v_permlane32_swap) and combine: returns
 // op(x[lane % 32], x[lane % 32 + 32]) in every lane.
 __device__ __forceinline__ float lane32_max(float x) {
