@@ -313,6 +313,10 @@ def test_split_long_context_backward(dev, b, h, s, d, fused):
     (1, 2, 200, 200, True),     # ragged: partial query and key tiles
     (1, 1, 100, 260, False),    # non-causal, sk != sq, both ragged
     (3, 5, 704, 704, True),     # 11 tiles, 90 query workgroups
+    (2, 1, 33, 33, True),       # one 32-query granule and one row of the next
+    (1, 3, 160, 160, True),     # five granules: dK/dV sweeps padded to an even count
+    (1, 1, 96, 300, False),     # non-causal, sq < sk, three key blocks
+    (1, 2, 1000, 1000, True),   # ragged length over many granules and key blocks
 ])
 def test_backward_d256_bf16(dev, b, h, sq, sk, causal, fused):
     """The bf16 backward at head dim 256 through the C ABI (the pipelined dQ kernel with four waves
