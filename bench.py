@@ -639,7 +639,7 @@ def main(argv=None):
         kernels["attention_long_context"] = bench_attention(1, 8, 8192, 64, max(a.steps // 2, 3), 2, seed=27)
         kernels["attention_fwd_parts"] = bench_attention_fwd_parts(max(a.steps // 2, 5), 2)
         # Head dim 256 (the reference's tests run it), at the headline's FLOPs: the forward and dQ on
-        # the pipelined four-wave kernels, dK/dV on the role split over 128-column output slabs.
+        # the pipelined four-wave kernels, dK/dV in one pass, four roles per 32-key block.
         kernels["attention_d256"] = bench_attention(4, 8, 2048, 256, max(a.steps // 5, 3), 2, seed=31)
         # The bf16 rate a pure MFMA stream sustains on this part, and each attention line against it.
         ceil = bench_mfma_ceiling()

@@ -3224,74 +3224,85 @@ constexpr bool half256_dma_ok() {
     }
   return true;
 }
-static_assert(half256_dma_ok<8>(), "the 256-column granule's DMA blocks cover it once, where the reads expect them");
+static_assert(half256_dma_ok<8>() && half256_dma_ok<4>(),
+              "the 256-column granule's DMA blocks cover it once, where the reads expect them");
 
-// dK, dV at D = 256: the role split of attn_dkv_rs_kernel, each workgroup on
-// one 128-column slab of dK and dV. A 32-key block's K and V rows (256 columns
-// each) and its dK and dV accumulators would take 512 registers, a SIMD's
-// whole file; so a workgroup keeps only its slab's dK and dV columns, and both
-// slabs' workgroups compute the full-width S and dP (six products where one
-// pass would run four, in exchange for two waves per SIMD). Role A (wave
-// w < 4): S = Q K^T over 256 columns, P, dV^T[slab] += dO^T[slab] P for keys
-// k0 + 32 w; role B (wave w + 4, same SIMD): dP = dO V^T, dS = P (dP - delta),
-// dK^T[slab] += Q^T[slab] dS. P crosses from A to B in f32 through LDS, as
-// there. The query side streams in 32-row granules (BwdHalf256, 16.6 KB): a
-// ring of four for Q (granule x is read in step x - 1 by A's S products and in
-// step x + 1 by B's dK products) and one of three for dO (steps x and x + 1),
-// each loaded one step ahead (sched::dkv256_*); with the two P buffers they
-// take 153 KB. One workgroup barrier per step (32 queries).
-struct Dkv256 {
+// DMA of 64 f32 row statistics (lse or delta) starting at row r0 into `lds`, 4
+// bytes a lane: 256 bytes of LDS (rows past nrows arrive as zeros).
+__device__ __forceinline__ void stat_dma4(const float* base, int r0, int nrows, char* lds) {
+  const int lane = threadIdx.x & 63;
+  const int rows_left = nrows - r0 > 0 ? nrows - r0 : 0;
+  const uint64_t addr = reinterpret_cast<uint64_t>(base + r0);
+  const u32x4 rsrc = {(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
+                      (uint32_t)__builtin_amdgcn_readfirstlane((int)((addr >> 32) & 0xffffu)),
+                      (uint32_t)__builtin_amdgcn_readfirstlane(rows_left * 4), 0x00020000u};
+  const uint32_t voff = (uint32_t)(lane * 4);
+  const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)reinterpret_cast<uintptr_t>(lds));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// dK, dV at D = 256 in one pass: four roles per 32-key block, two blocks (64
+// keys) per workgroup. A 32-key block's K and V rows and its dK and dV
+// accumulators (512 registers in all) do not fit one SIMD's two waves; spread
+// over four waves (two SIMDs), S and dP are still computed once:
+//   role A (waves 0, 2): S = Q K^T over 256 columns, P, dV^T[0:128] += dO^T P;
+//   role B (waves 1, 3): dP = dO V^T, dS = P (dP - delta), dK^T[0:128] += Q^T dS;
+//   role A' (waves 4, 6): dV^T[128:256] += dO^T P, P from role A;
+//   role B' (waves 5, 7): dK^T[128:256] += Q^T dS, dS from role B.
+// Waves w and w + 4 share a SIMD: each SIMD pairs a role A or B wave (24
+// products a step) with an A' or B' wave (8 products, and the workgroup's DMA).
+// P crosses from A to B and A' in f32 through LDS (A' rounds it to the same
+// fragments A uses), dS from B to B' as fragments. B' runs one step behind B,
+// so a Q granule is read in steps x - 1 (S), x + 1 (dK, B) and x + 2 (dK, B'):
+// a ring of five Q granules and three dO granules (sched::dkv256q_*), the P and
+// dS buffers: 156 KB.
+struct Dkv256Q {
   static constexpr int D = 256, kWaves = 8, kThreads = 64 * kWaves;
-  static constexpr int BKV = 128, BG = 32;  // keys per workgroup, queries per granule
-  static constexpr int KS = D / 16;         // k-chunks of S and dP
-  static constexpr int SDT = 4;             // 32-column output tiles of a 128-column slab
+  static constexpr int BKV = 64, BG = 32;  // keys per workgroup, queries per granule
+  static constexpr int KS = D / 16, SDT = 4;
   typedef BwdHalf256 G;
   typedef BwdTile<256> Tile;
-  static constexpr int kQSlots = sched::kDkv256QSlots, kDoSlots = sched::kDkv256DoSlots;
-  // lse (Q ring) or delta (dO ring): one stat_dma instruction, 64 rows in its
-  // first 256 bytes and zeros from the other 48 lanes in the rest of 1 KB.
-  static constexpr int kStatBytes = 1024;
+  static constexpr int kQSlots = sched::kDkv256qQSlots, kDoSlots = sched::kDkv256qDoSlots;
+  static constexpr int kStatBytes = 256;  // 64 rows of lse (Q ring) or delta (dO ring): stat_dma4
   static constexpr int kSlotBytes = G::kBytes + kStatBytes;
   static constexpr int kDoRing = kQSlots * kSlotBytes;
-  static constexpr int kXRing = kDoRing + kDoSlots * kSlotBytes;
-  static constexpr int kXBytes = 4 * 4096;  // P of one granule for the four SIMD pairs (f32)
-  static constexpr int kLds = kXRing + 2 * kXBytes;
-  static constexpr int kDma = G::kBlocks / kWaves;  // per wave per granule, for Q and for dO
-  static constexpr int kStage = kSlotBytes;         // K / V row staging: from Q slot 1 on, 16 KB a wave
-  static_assert(kStatBytes >= 64 * 16, "a statistics DMA writes 16 bytes for each of its 64 lanes");
+  static constexpr int kXP = kDoRing + kDoSlots * kSlotBytes;  // P (f32) by parity and block: 4 KB each
+  static constexpr int kXDS = kXP + 2 * 2 * 4096;              // dS fragments by parity and block: 2 KB each
+  static constexpr int kLds = kXDS + 2 * 2 * 2048;
+  static constexpr int kLight = 4;                   // waves 4 .. 7 issue the ring's DMA
+  static constexpr int kDma = G::kBlocks / kLight;   // per light wave per granule, for Q and for dO
+  static constexpr int kStage = kSlotBytes;          // roles A and B: K / V rows from Q slot 1 on, 16 KB a wave
   static_assert(kLds <= 160 * 1024, "one workgroup per CU");
-  static_assert(kStage + kWaves * 32 * 2 * D <= kLds, "the K / V rows fit the staging");
+  static_assert(kStage + 4 * 32 * 2 * D <= kDoRing, "the K / V rows stage inside Q slots 1 ..");
 };
 
 template <bool SAMEP>
-__global__ __launch_bounds__(512, 1) void attn_dkv_rs256_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
-                                                               const bf16* __restrict__ v,
-                                                               const bf16* __restrict__ dout,
-                                                               const float* __restrict__ lse,
-                                                               const float* __restrict__ delta, bf16* __restrict__ dk,
-                                                               bf16* __restrict__ dv, int bh_count, int Sq, int Sk,
-                                                               int causal, float scale, float scale_log2, AttnViews vw) {
-  typedef Dkv256 F;
+__global__ __launch_bounds__(512, 1) void attn_dkv_q256_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                              const bf16* __restrict__ v,
+                                                              const bf16* __restrict__ dout,
+                                                              const float* __restrict__ lse,
+                                                              const float* __restrict__ delta, bf16* __restrict__ dk,
+                                                              bf16* __restrict__ dv, int bh_count, int Sq, int Sk,
+                                                              int causal, float scale, float scale_log2, AttnViews vw) {
+  typedef Dkv256Q F;
   typedef F::G G;
   typedef F::Tile Tile;
   constexpr int KS = F::KS, SDT = F::SDT;
   constexpr int kAhead = 3;
-  // Per wave and step: Q blocks, dO blocks, and a statistics row (waves 0 and 4 only).
-  constexpr int kStepDma = 2 * F::kDma + 1;
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
-  // Blocks: heads fastest, then the two slabs of a key block, then key blocks
-  // from the heaviest (first) causal sweep on.
+  // Blocks: heads fastest, then 64-key blocks from the heaviest causal sweep on.
   const int bh = blockIdx.x % bh_count;
-  const int rest = (int)(blockIdx.x / bh_count);
-  const int kt = rest >> 1, slab = rest & 1;
+  const int kt = (int)(blockIdx.x / bh_count);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int pair = wave & 3, role = wave >> 2;
+  const bool light = wave >= 4;
+  const int blk = (wave >> 1) & 1, role = wave & 1;  // role 0: A / A', 1: B / B'
   const int lane = threadIdx.x & 63;
   const int g = lane >> 5;
   const int k0 = kt * F::BKV;
-  const int k0w = k0 + 32 * pair;
-  const int kvrow = k0w + (lane & 31);
+  const int kb0 = k0 + 32 * blk;  // the wave's 32 keys
+  const int kvrow = kb0 + (lane & 31);
 
   const int ldq = (int)vw.q.r, lddo = (int)vw.dout.r;
   const bf16* qb = q + vw.q.at(bh, vw.heads);
@@ -3299,83 +3310,118 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs256_kernel(const bf16* __re
   const float* lseb = lse + (int64_t)bh * Sq;
   const float* db = delta + (int64_t)bh * Sq;
 
-  // Granules first .. first + nh - 1 of the queries (granule x: rows
-  // 32 (first + x) ..). nh is even and at least 6: granules past the end of
-  // the queries arrive as zeros (Q, dO, lse and delta all 0) and add exact
-  // zeros, as the padded sweeps of attn_dkv_sw_kernel.
+  // Granules first .. first + nh - 1 of the queries; nh even and at least 4
+  // (granules past the end of the queries arrive as zeros and add exact zeros).
   const int first = causal ? k0 / F::BG : 0;
-  int nh = max((Sq + F::BG - 1) / F::BG - first, 6);
+  int nh = max((Sq + F::BG - 1) / F::BG - first, 4);
   nh += nh & 1;
 
-  const PpDma<G, true, F::kWaves> dma(wave, ldq);
-  const PpDma<G, true, F::kWaves> dma_do(wave, SAMEP ? ldq : lddo);
-  auto qslot = [&](int x) { return smem + (x & (F::kQSlots - 1)) * F::kSlotBytes; };
+  auto qslot = [&](int x) { return smem + ((x + F::kQSlots) % F::kQSlots) * F::kSlotBytes; };
   auto doslot = [&](int x) { return smem + F::kDoRing + ((x + F::kDoSlots) % F::kDoSlots) * F::kSlotBytes; };
-  char* const xring = smem + F::kXRing;
-  // P of granule h, pair p: chunk c (four queries) of lane L at xbuf(h) + p 4096 + c 1024 + 16 L.
-  auto xbuf = [&](int h) { return xring + (h & 1) * F::kXBytes + pair * 4096; };
-  // Step h's DMA instruction qd: Q and lse of granule h + 2, dO and delta of
-  // granule h + 1 (none past the sweep); rows past the end of the queries
-  // arrive as zeros (empty buffer range).
-  auto dma_part = [&](int h, int qd) {
-    const int xq = sched::dkv256_q_loaded(h), xd = sched::dkv256_do_loaded(h);
-    if (qd < F::kDma) {
-      if (xq < nh) dma.issue_one(qb, (first + xq) * F::BG, Sq, ldq, qslot(xq), qd);
-    } else if (qd < 2 * F::kDma) {
-      if (xd < nh)
-        (SAMEP ? dma : dma_do).issue_one(dob, (first + xd) * F::BG, Sq, SAMEP ? ldq : lddo, doslot(xd), qd - F::kDma);
-    } else if (pair == 0) {
-      if (role == 0) {
-        if (xq < nh) stat_dma(lseb, (first + xq) * F::BG, Sq, qslot(xq) + G::kBytes);
-      } else {
-        if (xd < nh) stat_dma(db, (first + xd) * F::BG, Sq, doslot(xd) + G::kBytes);
-      }
+  // P of granule x (f32, chunk c of four queries of lane L at + c 1024 + 16 L), dS fragments of granule x.
+  auto xp = [&](int x) { return smem + F::kXP + ((x & 1) * 2 + blk) * 4096 + 16 * lane; };
+  auto xds = [&](int x) { return smem + F::kXDS + ((x & 1) * 2 + blk) * 2048 + 16 * lane; };
+
+  // The light waves' DMA of step h: Q and lse of granule h + 2, dO and delta of
+  // granule h + 1 (none past the sweep; rows past the queries arrive as zeros).
+  const PpDma<G, true, F::kLight> dma(light ? wave - 4 : 0, ldq);
+  const PpDma<G, true, F::kLight> dma_do(light ? wave - 4 : 0, SAMEP ? ldq : lddo);
+  auto step_dma = [&](int h) {
+    const int xq = sched::dkv256q_q_loaded(h), xd = sched::dkv256q_do_loaded(h);
+    if (xq < nh) {
+#pragma unroll
+      for (int i = 0; i < F::kDma; ++i) dma.issue_one(qb, (first + xq) * F::BG, Sq, ldq, qslot(xq), i);
+      if (wave == 4) stat_dma4(lseb, (first + xq) * F::BG, Sq, qslot(xq) + G::kBytes);
+    }
+    if (xd < nh) {
+#pragma unroll
+      for (int i = 0; i < F::kDma; ++i)
+        (SAMEP ? dma : dma_do).issue_one(dob, (first + xd) * F::BG, Sq, SAMEP ? ldq : lddo, doslot(xd), i);
+      if (wave == 5) stat_dma4(db, (first + xd) * F::BG, Sq, doslot(xd) + G::kBytes);
     }
   };
-  auto dma_at = [&](int h, int f) {
-    if (f < kStepDma) dma_part(h, f);
-  };
 
-  // Prologue: Q and lse of granule 0, and each wave's K (role A) or V (role
-  // B) rows by row-coalesced DMA into the staging, which the ring reaches
-  // only from step -1's loads on.
-  char* const rst = smem + F::kStage + wave * (32 * 2 * F::D);
-  {
+  // Prologue: roles A and B stage their K or V rows; the light waves load Q and lse of granule 0.
+  char* const rst = smem + F::kStage + (wave & 3) * (32 * 2 * F::D);
+  if (!light) {
     const bf16* kvb = role == 0 ? k + vw.k.at(bh, vw.heads) : v + vw.v.at(bh, vw.heads);
-    dma_rows32<256>(kvb, k0w, Sk, role == 0 ? (int)vw.k.r : (int)vw.v.r, rst);
+    dma_rows32<256>(kvb, kb0, Sk, role == 0 ? (int)vw.k.r : (int)vw.v.r, rst);
+  } else {
 #pragma unroll
-    for (int qd = 0; qd < F::kDma; ++qd) dma.issue_one(qb, first * F::BG, Sq, ldq, qslot(0), qd);
-    if (wave == 0) stat_dma(lseb, first * F::BG, Sq, qslot(0) + G::kBytes);
+    for (int i = 0; i < F::kDma; ++i) dma.issue_one(qb, first * F::BG, Sq, ldq, qslot(0), i);
+    if (wave == 4) stat_dma4(lseb, first * F::BG, Sq, qslot(0) + G::kBytes);
   }
 
   const Tile::Bases tb(lane);
-  const int trs = tb.t + 256 * slab;  // transposed reads of the slab's columns
-  auto tr_slab = [&](const char* sl, int hh, int uu) -> bf16x8 {
+  const int trs0 = tb.t, trs1 = tb.t + 256;  // transposed reads of the two slabs
+  auto tr_slab = [&](const char* sl, int trs, int hh, int uu) -> bf16x8 {
     return tr_frag(sl + trs + Tile::tr_at(0, hh, uu), Tile::kTrHi);
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
-
-  // Barrier opening step h: every load of step h - 1 is first read in step h.
   auto sync = [&]() {
     wait_vmem<0>();
     lds_barrier();
   };
-  bf16x8 kvf[KS];  // K rows (role A) or V rows (role B), all 256 columns
+  bf16x8 kvf[KS];  // roles A and B: K or V rows, all 256 columns
   sync();
-  row_frags_lds<256>(kvf, rst);
-  // Every wave has its rows before step -1's loads overwrite the staging.
-  lds_barrier();
+  if (!light) row_frags_lds<256>(kvf, rst);
+  lds_barrier();  // every staging read is done before step -1's loads
+
+  f32x16 acc[SDT];
+#pragma unroll
+  for (int u = 0; u < SDT; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[u][r] = 0.f;
+
+  if (light) {
+    // ---- roles A' and B': the second slab's products from the partner role's P or dS ----
+    const int lag = role == 0 ? 1 : 2;  // A': dV for granule h - 1; B': dK for granule h - 2
+    for (int h = -1; h <= nh + 1; ++h) {
+      if (h >= 0) sync();
+      step_dma(h);
+      const int x = h - lag;
+      if (x < 0 || x >= nh) continue;
+      bf16x8 fr[2];
+      if (role == 0) {
+        // P of granule x in f32 from role A, rounded to the fragments A uses.
+        const char* src = xp(x);
+        float pv[16];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const f32x4 p4 = *reinterpret_cast<const f32x4*>(src + c * 1024);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pv[4 * c + e] = p4[e];
+        }
+        to_frag(pv, fr[0]);
+        to_frag(pv + 8, fr[1]);
+      } else {
+        fr[0] = *reinterpret_cast<const bf16x8*>(xds(x));
+        fr[1] = *reinterpret_cast<const bf16x8*>(xds(x) + 1024);
+      }
+      const char* sl = role == 0 ? doslot(x) : qslot(x);  // dO^T or Q^T of granule x
+      bf16x8 buf[2 * SDT];
+#pragma unroll
+      for (int i = 0; i < 2 * SDT; ++i) buf[i] = tr_slab(sl, trs1, i & 1, i >> 1);
+#pragma unroll
+      for (int i = 0; i < 2 * SDT; ++i) mma32(buf[i], fr[i & 1], acc[i >> 1]);
+    }
+    wait_vmem<0>();
+    lds_barrier();
+    if (kb0 >= Sk) return;
+    if (role == 0)
+      store_acc_rows_lds<128>(acc, smem + wave * (32 * 256), dv + vw.dv.at(bh, vw.heads) + 128, kb0, Sk, 1.0f,
+                              vw.dv.r);
+    else
+      store_acc_rows_lds<128>(acc, smem + wave * (32 * 256), dk + vw.dk.at(bh, vw.heads) + 128, kb0, Sk, scale,
+                              vw.dk.r);
+    return;
+  }
 
   if (role == 0) {
-    // ---- role A: S, P, dV ----
-    f32x16 dva[SDT];
-#pragma unroll
-    for (int u = 0; u < SDT; ++u)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dva[u][r] = 0.f;
+    // ---- role A: S, P, dV^T[0:128] ----
     f32x16 sa[2];     // S of a granule (register r: query 16 g + r, key kvrow), by parity
     bf16x8 pf[2][2];  // [parity][8-query chunk]: P fragments
 
@@ -3387,15 +3433,15 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs256_kernel(const bf16* __re
       f32x16& sn = sa[1 - P];
       bf16x8(&pc)[2] = pf[P];
       const bf16x8(&pp)[2] = pf[1 - P];
-      const char* qn = qslot(h + 1);   // S of granule h + 1: Q rows
-      const char* dop = doslot(h - 1);  // dV of granule h - 1: dO^T, the slab's columns
-      constexpr int NS = SDP ? KS : 0;       // S: k-chunk i
-      constexpr int NG = GRAD ? 2 * SDT : 0;  // dV: output tile i / 2, query chunk i % 2
+      const char* qn = qslot(h + 1);
+      const char* dop = doslot(h - 1);
+      constexpr int NS = SDP ? KS : 0;
+      constexpr int NG = GRAD ? 2 * SDT : 0;
       constexpr int NF = NS + NG;
       auto read = [&](int f) -> bf16x8 {
         if (f < NS) return *reinterpret_cast<const bf16x8*>(qn + Tile::row(tb, 0, f));
         const int i = f - NS;
-        return tr_slab(dop, i & 1, i >> 1);
+        return tr_slab(dop, trs0, i & 1, i >> 1);
       };
       auto prod = [&](int f, const bf16x8& a) {
         if (f < NS) {
@@ -3405,13 +3451,12 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs256_kernel(const bf16* __re
             mma32(a, kvf[f], sn);
         } else {
           const int i = f - NS;
-          mma32(a, pp[i & 1], dva[i >> 1]);
+          mma32(a, pp[i & 1], acc[i >> 1]);
         }
       };
-      // Softmax of granule h: element r (query 16 g + r of the granule).
       const float* st = reinterpret_cast<const float*>(qslot(h) + G::kBytes) + 16 * g;
       const int qh = (first + h) * F::BG + 16 * g;
-      char* const xw = xbuf(h) + 16 * lane;
+      char* const xw = xp(h);
       f32x4 ls[2];
       float pv[8];
       f32x4 p4;
@@ -3437,8 +3482,6 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs256_kernel(const bf16* __re
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
           if (f + kAhead < NF) buf[f + kAhead] = read(f + kAhead);
-          // The step's loads go out first: they have one step to land.
-          dma_at(h, f);
           prod(f, buf[f]);
           if constexpr (SG && NG > 0) {
             if (f >= NS) {
@@ -3448,68 +3491,56 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs256_kernel(const bf16* __re
           }
           __builtin_amdgcn_sched_barrier(0);
         }
-      } else {
-#pragma unroll
-        for (int f = 0; f < kStepDma; ++f) dma_at(h, f);
       }
       if constexpr (SG && NG == 0) {
-        // No dV products to hide it behind (step 0): the softmax last.
 #pragma unroll
         for (int r = 0; r < 16; ++r) sg_elem(r);
       }
     };
     // Step h: GRAD (dV) for 1 <= h <= nh, SG for 0 <= h < nh, SDP (S) for
-    // h + 1 < nh; the mask covers granules 0 .. 3 (the diagonal block).
+    // h + 1 < nh; the mask covers granules 0 and 1 (the diagonal block).
     stage(P1(), F_(), F_(), F_(), T_(), -1);
     sync();
     stage(P0(), F_(), T_(), T_(), T_(), 0);
     sync();
     stage(P1(), T_(), T_(), T_(), T_(), 1);
-    sync();
-    stage(P0(), T_(), T_(), T_(), T_(), 2);
-    sync();
-    stage(P1(), T_(), T_(), T_(), T_(), 3);
-    sync();
-    stage(P0(), T_(), T_(), F_(), T_(), 4);
-    for (int h = 5; h + 1 <= nh - 2; h += 2) {
+    int h = 2;
+    for (; h + 1 < nh - 2; h += 2) {
       sync();
-      stage(P1(), T_(), T_(), F_(), T_(), h);
+      stage(P0(), T_(), T_(), F_(), T_(), h);
       sync();
-      stage(P0(), T_(), T_(), F_(), T_(), h + 1);
+      stage(P1(), T_(), T_(), F_(), T_(), h + 1);
     }
+    sync();
+    stage(P0(), T_(), T_(), F_(), T_(), nh - 2);
     sync();
     stage(P1(), T_(), T_(), F_(), F_(), nh - 1);
     sync();
     stage(P0(), T_(), F_(), F_(), F_(), nh);
+    sync();  // step nh + 1: role B' only
     wait_vmem<0>();
-    lds_barrier();  // as role B's: whole-row stores through LDS
-    if (k0w >= Sk) return;
-    store_acc_rows_lds<128>(dva, smem + wave * (32 * 256), dv + vw.dv.at(bh, vw.heads) + 128 * slab, k0w, Sk, 1.0f,
-                            vw.dv.r);
+    lds_barrier();
+    if (kb0 >= Sk) return;
+    store_acc_rows_lds<128>(acc, smem + wave * (32 * 256), dv + vw.dv.at(bh, vw.heads), kb0, Sk, 1.0f, vw.dv.r);
   } else {
-    // ---- role B: dP, dS, dK ----
-    f32x16 dka[SDT];
-#pragma unroll
-    for (int u = 0; u < SDT; ++u)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dka[u][r] = 0.f;
+    // ---- role B: dP, dS, dK^T[0:128] ----
     f32x16 dpa[2];  // dP of a granule, by parity
     bf16x8 dsf[2];  // dS fragments of the granule the step's dK products use
 
     auto stage = [&](auto P_, auto SDP_, auto SG_, auto GRAD_, int h) __attribute__((always_inline)) {
       constexpr int P = decltype(P_)::value;
       constexpr bool SDP = decltype(SDP_)::value, SG = decltype(SG_)::value, GRAD = decltype(GRAD_)::value;
-      f32x16& dpn = dpa[P];            // dP of granule h
-      const f32x16& dpc = dpa[1 - P];  // dP of granule h - 1
-      const char* doc = doslot(h);     // dP of granule h: dO rows
-      const char* qp = qslot(h - 1);   // dK of granule h - 1: Q^T, the slab's columns
-      constexpr int NS = SDP ? KS : 0;        // dP: k-chunk i
-      constexpr int NG = GRAD ? 2 * SDT : 0;  // dK: output tile i / 2, query chunk i % 2
+      f32x16& dpn = dpa[P];
+      const f32x16& dpc = dpa[1 - P];
+      const char* doc = doslot(h);
+      const char* qp = qslot(h - 1);
+      constexpr int NS = SDP ? KS : 0;
+      constexpr int NG = GRAD ? 2 * SDT : 0;
       constexpr int NF = NS + NG;
       auto read = [&](int f) -> bf16x8 {
         if (f < NS) return *reinterpret_cast<const bf16x8*>(doc + Tile::row(tb, 0, f));
         const int i = f - NS;
-        return tr_slab(qp, i & 1, i >> 1);
+        return tr_slab(qp, trs0, i & 1, i >> 1);
       };
       auto prod = [&](int f, const bf16x8& a) {
         if (f < NS) {
@@ -3519,12 +3550,14 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs256_kernel(const bf16* __re
             mma32(a, kvf[f], dpn);
         } else {
           const int i = f - NS;
-          mma32(a, dsf[i & 1], dka[i >> 1]);
+          mma32(a, dsf[i & 1], acc[i >> 1]);
         }
       };
-      // dS of granule h - 1: element r (query 16 g + r), P from A's step h - 1.
+      // dS of granule h - 1: element r (query 16 g + r), P from A's step h - 1;
+      // its fragments also go to role B' for the second slab.
       const float* st = reinterpret_cast<const float*>(doslot(h - 1) + G::kBytes) + 16 * g;
-      const char* xr = xbuf(h - 1) + 16 * lane;
+      const char* xr = xp(h - 1);
+      char* const xw = xds(h - 1);
       f32x4 dl[2], px[2];
       float dsv[8];
       auto sg_elem = [&](int r) {
@@ -3538,6 +3571,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs256_kernel(const bf16* __re
         if ((r & 7) == 7) {
           to_frag(dsv, dsf[r >> 3]);
           pin(dsf[r >> 3]);
+          *reinterpret_cast<bf16x8*>(xw + (r >> 3) * 1024) = dsf[r >> 3];
         }
       };
       if constexpr (SG) {
@@ -3556,7 +3590,6 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs256_kernel(const bf16* __re
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
           if (f + kAhead < NF) buf[f + kAhead] = read(f + kAhead);
-          dma_at(h, f);
           prod(f, buf[f]);
           if constexpr (SG && NS > 0) {
             if (f < NS) {
@@ -3566,13 +3599,9 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs256_kernel(const bf16* __re
           }
           __builtin_amdgcn_sched_barrier(0);
         }
-      } else {
-#pragma unroll
-        for (int f = 0; f < kStepDma; ++f) dma_at(h, f);
       }
     };
     // Step h: SDP (dP) for 0 <= h < nh, SG (dS) and GRAD (dK) for 1 <= h <= nh.
-    stage(P1(), F_(), F_(), F_(), -1);
     sync();
     stage(P0(), T_(), F_(), F_(), 0);
     for (int h = 1; h + 1 <= nh - 1; h += 2) {
@@ -3585,14 +3614,11 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs256_kernel(const bf16* __re
     stage(P1(), T_(), T_(), T_(), nh - 1);
     sync();
     stage(P0(), F_(), T_(), T_(), nh);
+    sync();  // step nh + 1: role B' only
     wait_vmem<0>();
-    // Whole-row stores through LDS, each wave in its own 8 KB; the barrier
-    // (role A passes one too) keeps the other waves' last reads off it.
-    static_assert(8 * 32 * 256 <= Dkv256::kLds, "every wave's rows fit the ring");
     lds_barrier();
-    if (k0w >= Sk) return;
-    store_acc_rows_lds<128>(dka, smem + wave * (32 * 256), dk + vw.dk.at(bh, vw.heads) + 128 * slab, k0w, Sk, scale,
-                            vw.dk.r);
+    if (kb0 >= Sk) return;
+    store_acc_rows_lds<128>(acc, smem + wave * (32 * 256), dk + vw.dk.at(bh, vw.heads), kb0, Sk, scale, vw.dk.r);
   }
 }
 
@@ -4238,18 +4264,18 @@ int dkv_pp_launch(const void* q, const void* k, const void* v, const void* dout,
   }
 }
 
-// bf16 dK/dV at head dim 256 (d == 256, 16-byte aligned rows): the role
-// split on 128-column slabs, two workgroups per key block of 128.
-int dkv256_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
-                  void* dk, void* dv, const Shape& s, int causal, float scale, hipStream_t stream) {
-  typedef Dkv256 F;
+// bf16 dK/dV at head dim 256 (d == 256, 16-byte aligned rows) in one pass
+// (attn_dkv_q256_kernel): four roles per 32-key block, 64 keys per workgroup.
+int dkv256q_launch(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
+                   void* dk, void* dv, const Shape& s, int causal, float scale, hipStream_t stream) {
+  typedef Dkv256Q F;
   const int64_t nk = cdiv(s.sk, F::BKV);
   const int64_t bh = s.b * s.h;
-  if (2 * nk * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dkv: grid too large");
+  if (nk * bh > 0x7fffffff) return fail(FERRITE_ERR_INVALID_ARGUMENT, "ferrite_hip_attn_bwd_dkv: grid too large");
   const AttnViews vw = dense_views(s);
-  auto kern = attn_dkv_rs256_kernel<true>;
+  auto kern = attn_dkv_q256_kernel<true>;
   if (int rc = set_lds(kern, F::kLds, stream)) return rc;
-  hipLaunchKernelGGL(kern, dim3((unsigned)(2 * nk * bh)), dim3(F::kThreads), F::kLds, stream,
+  hipLaunchKernelGGL(kern, dim3((unsigned)(nk * bh)), dim3(F::kThreads), F::kLds, stream,
                      static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
                      static_cast<const bf16*>(dout), lse, delta, static_cast<bf16*>(dk), static_cast<bf16*>(dv),
                      (int)bh, (int)s.sq, (int)s.sk, causal, scale, scale * kLog2e, vw);
@@ -4429,7 +4455,7 @@ extern "C" int ferrite_hip_attn_bwd_dkv_ex(const void* q, const void* k, const v
                   aligned16(dout) && aligned16(dk) && aligned16(dv);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (d == 256 && dtype == FERRITE_BF16 && al)
-    return dkv256_launch(q, k, v, dout, lse, delta, dk, dv, s, causal, scale, st);
+    return dkv256q_launch(q, k, v, dout, lse, delta, dk, dv, s, causal, scale, st);
   if (d > 128) FERRITE_WIDE(dkv_wide_launch, dtype, al, q, k, v, dout, lse, delta, dk, dv, s, causal, scale, st);
 #define FERRITE_DISPATCH_256(LAUNCH, T, aligned, ...) \
   return fail(FERRITE_ERR_INVALID_ARGUMENT, "unreachable head_dim")

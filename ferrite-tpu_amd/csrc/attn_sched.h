@@ -192,16 +192,18 @@ FERRITE_SCHED int dkv_rs_loaded(int h) { return (h & 1) ? (h + 3) >> 1 : -1; }
 FERRITE_SCHED int dkv_rs_first_read(int t) { return 2 * t - 1; }
 FERRITE_SCHED int dkv_rs_last_read(int t) { return 2 * t + 2; }
 
-// dK/dV at D = 256 (attn_dkv_rs256_kernel), steps h = -1 .. nh over 32-query
-// granules x = 0 .. nh - 1. Q (and lse) of granule x in Q slot x % 4, dO (and
-// delta) in dO slot x % 3. The prologue loads Q 0; step h loads Q h + 2 and
-// dO h + 1 after its barrier, and a wave waits for all its loads before every
-// barrier. Q x is read in steps x - 1 (S, role A) and x + 1 (dK, role B), lse x
-// in step x (A); dO x in steps x (dP, B) and x + 1 (dV, A), delta x in step
-// x + 1 (B).
-constexpr int kDkv256QSlots = 4, kDkv256DoSlots = 3;
-FERRITE_SCHED int dkv256_q_loaded(int h) { return h + 2; }
-FERRITE_SCHED int dkv256_do_loaded(int h) { return h + 1; }
+// dK/dV at D = 256 in one pass (attn_dkv_q256_kernel), steps h = -1 .. nh + 1
+// over 32-query granules x = 0 .. nh - 1: Q (and lse) of granule x in Q slot
+// x % 5, dO (and delta) in dO slot x % 3; the prologue loads Q 0, step h loads
+// Q h + 2 and dO h + 1 (by the light waves) after its barrier, and a wave waits
+// for all its loads before every barrier. Q x is read in steps x - 1 (S, role
+// A), x + 1 (dK, role B) and x + 2 (dK, role B'), lse x in step x; dO x in
+// steps x (dP, role B) and x + 1 (dV, roles A and A'), delta x in step x + 1.
+// P of granule x (role A, step x) is read by B and A' in step x + 1; dS of x
+// (role B, step x + 1) by B' in step x + 2.
+constexpr int kDkv256qQSlots = 5, kDkv256qDoSlots = 3;
+FERRITE_SCHED int dkv256q_q_loaded(int h) { return h + 2; }
+FERRITE_SCHED int dkv256q_do_loaded(int h) { return h + 1; }
 
 }  // namespace sched
 }  // namespace ferrite

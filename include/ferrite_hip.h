@@ -282,9 +282,8 @@ int ferrite_hip_adamw(int64_t n_tensors, void* const* params, const void* const*
  * (those the reference's _validate accepts, flash_attention.py:341-343): any
  * D <= 128 (zero-padded inside the kernel to 64 or 128) and any multiple of 128
  * (D > 256, and f32 or unaligned operands at D = 256, run slab-wise: 128 output
- * columns per workgroup, the scores recomputed per slab; the bf16 dK/dV at
- * D = 256 also splits its output into two 128-column slabs). The same holds
- * for the backward entry points below on
+ * columns per workgroup, the scores recomputed per slab). The same holds for
+ * the backward entry points below on
  * [B, H, S, D] tensors; the packed-QKV entry points (ferrite_hip_attn_fwd_qkv,
  * ferrite_hip_attn_bwd_qkv) are the exception and take head_dim 64 or 128 only.
  * Sq, Sk >= 1; Sq and Sk need not be multiples of any tile size.

@@ -13,8 +13,8 @@
 //   attn_dkv_sw_kernel   dK/dV at D = 64 (4 waves, 4 slots, half-steps; the
 //                        split long-context grid)
 //   attn_dkv_rs_kernel   dK/dV at D = 128 (8 waves in two roles, 3 slots)
-//   attn_dkv_rs256_kernel dK/dV at D = 256 (the role split on 128-column slabs,
-//                        a Q ring of 4 and a dO ring of 3 32-query granules)
+//   attn_dkv_q256_kernel dK/dV at D = 256 in one pass (four roles, a Q ring of
+//                        5 and a dO ring of 3 granules, P and dS buffers)
 //   attn_*_wide_kernel   head dims above 128 / 256 (the grid only: their LDS
 //                        staging is synchronous, between two barriers)
 //
@@ -161,8 +161,8 @@ static int fwd_wait(int j, int kdma, int slots) {
 static int dq_next(int t, int slots) { return g_mutation == 4 ? t + slots : dq_loaded(t, slots); }
 static bool fwd_writes(int kh, int role) { return g_mutation == 5 ? role != 0 : kh == 0 && (role < 0 || role == 1); }
 static int rs_loaded(int h) { return g_mutation == 6 ? ((h & 1) ? (h + 5) >> 1 : -1) : dkv_rs_loaded(h); }
-static int q256_loaded(int h) { return g_mutation == 9 ? h + 3 : dkv256_q_loaded(h); }    // Q into a slot in use
-static int do256_loaded(int h) { return g_mutation == 10 ? h + 2 : dkv256_do_loaded(h); }  // dO into a slot in use
+static int q256q_loaded(int h) { return g_mutation == 9 ? h + 3 : dkv256q_q_loaded(h); }   // Q into a slot in use
+static int do256q_loaded(int h) { return g_mutation == 10 ? h + 2 : dkv256q_do_loaded(h); }  // dO into a slot in use
 constexpr int BK = 64;  // keys per tile of the forward and dQ rings, queries per tile of dK/dV's
 
 // ---------------------------------------------------------------------------
@@ -485,92 +485,96 @@ static void check_dkv(int D, int bh, int S, bool zig, bool split = false) {
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV at D = 256: attn_dkv_rs256_kernel. Grid = heads x (key block, slab);
-// each workgroup sweeps 32-query granules from its block's diagonal on (at
-// least 6, an even number; the extra granules read as zeros). Regions 0-3:
-// the Q slots (Q and lse; 17664 bytes each), 4-6: the dO slots (dO and
-// delta), 7-8: the P buffers (16384 bytes each), 20 + w: wave w's K / V row
-// staging (16 KB from Q slot 1 on: over Q slots 1-3, the dO slots and the P
-// buffers), read back between the first barrier and a second one. A
-// statistics load fills the last 1 KB of its slot (its 64 lanes' 16 bytes).
+// dK/dV at D = 256 in one pass: attn_dkv_q256_kernel. Grid = heads x 64-key
+// blocks; each workgroup sweeps 32-query granules from its block's diagonal on
+// (at least 4, an even number). Regions 0-4: the Q slots (Q and lse), 5-7: the
+// dO slots (dO and delta), 8-9: the P buffers, 10-11: the dS buffers (by
+// granule parity; the two key blocks' halves of a buffer are one region),
+// 20 + w: wave w's K / V row staging (waves 0-3, 16 KB each from Q slot 1 on).
+// Roles: A (waves 0, 2), B (1, 3), A' (4, 6), B' (5, 7); the light waves A'
+// and B' issue the rings' loads.
 // ---------------------------------------------------------------------------
-static void check_dkv256(int bh, int Sq, int Sk, bool causal) {
-  const int BKV = 128, BG = 32, W = 8, nk = (Sk + BKV - 1) / BKV;
-  const int qs = kDkv256QSlots, ds = kDkv256DoSlots;
-  const std::string name = std::string("dkv_rs256") + (causal ? " causal" : "") + " bh" + std::to_string(bh) + " Sq" +
+static void check_dkv256q(int bh, int Sq, int Sk, bool causal) {
+  const int BKV = 64, BG = 32, W = 8, nk = (Sk + BKV - 1) / BKV;
+  const int qs = kDkv256qQSlots, ds = kDkv256qDoSlots;
+  const std::string name = std::string("dkv_q256") + (causal ? " causal" : "") + " bh" + std::to_string(bh) + " Sq" +
                            std::to_string(Sq) + " Sk" + std::to_string(Sk);
   Coverage cells((long)bh * Sk * 2);
-  // Staging of wave w: bytes [17664 + 16384 w, + 16384) against the region map
-  // (Q slots of 17664 bytes from 0, the dO slots from 70656, the P buffers of
-  // 16384 from 123648).
-  constexpr long kSlot = 17664, kDo = kSlot * kDkv256QSlots, kX = kDo + kSlot * kDkv256DoSlots;
+  for (int block = 0; block < bh * nk; ++block) {
+    const int head = block % bh, kt = block / bh;
+    for (int w = 0; w < W; ++w) {
+      const int blk = (w >> 1) & 1, slab = w >= 4 ? 1 : 0;
+      for (int r = kt * BKV + 32 * blk; r < std::min(kt * BKV + 32 * blk + 32, Sk); ++r)
+        if ((w & 1) == 0) cells.add(((long)head * Sk + r) * 2 + slab, 1, (long)bh * Sk * 2);  // dV (A, A')
+    }
+  }
+  cells.expect_once(name + " dV (row, slab)");
+  // Staging of wave w (0-3): bytes [16896 + 16384 w, + 16384), inside Q slots 1-4 (16896 bytes each).
+  constexpr long kSlot = 16896;
   auto staging = [&](int w) {
     std::vector<int> r;
     const long lo = kSlot + 16384L * w, hi = lo + 16384;
-    auto over = [&](long a, long b, int region) {
-      if (a < hi && lo < b) r.push_back(region);
-    };
-    for (int i = 0; i < qs; ++i) over(kSlot * i, kSlot * (i + 1), i);
-    for (int i = 0; i < ds; ++i) over(kDo + kSlot * i, kDo + kSlot * (i + 1), 4 + i);
-    for (int i = 0; i < 2; ++i) over(kX + 16384L * i, kX + 16384L * (i + 1), 7 + i);
+    for (int i = 0; i < qs; ++i)
+      if (kSlot * i < hi && lo < kSlot * (i + 1)) r.push_back(i);
+    if (lo + 16384 > kSlot * qs) r.push_back(99);  // past the Q ring: must not happen
     r.push_back(20 + w);
     return r;
   };
-  // The grid: block -> (head, key block, slab), every (key row, slab) once.
-  for (int block = 0; block < bh * nk * 2; ++block) {
-    const int rest = block / bh, kt = rest >> 1, slab = rest & 1, head = block % bh;
-    for (int w = 0; w < 4; ++w)
-      for (int r = kt * BKV + 32 * w; r < std::min(kt * BKV + 32 * w + 32, Sk); ++r)
-        cells.add(((long)head * Sk + r) * 2 + slab, 1, (long)bh * Sk * 2);
-  }
-  cells.expect_once(name + " dK/dV (row, slab)");
-  // The ring schedule depends on the key block alone: one replay per block.
   for (int kt = 0; kt < nk; ++kt) {
     const int k0 = kt * BKV;
     const int first = causal ? k0 / BG : 0;
-    int nh = std::max((Sq + BG - 1) / BG - first, 6);
+    int nh = std::max((Sq + BG - 1) / BG - first, 4);
     nh += nh & 1;
-    // Every query that sees a key of the block lies in granules first .. first + nh - 1.
     if (first * BG > (causal ? k0 : 0) || (first + nh) * BG < Sq) fail(name + ": a sweep misses queries");
     Workgroup wg(W, name + " kt" + std::to_string(kt));
-    // Ops per wave and step: two Q and two dO blocks, plus a statistics row for waves 0 (lse) and 4 (delta).
-    auto issue_q = [&](int w, int x) {
-      if (x < nh) wg.issue(w, {x % qs}, 1000 + x, 2 + (w == 0 ? 1 : 0));
+    // Light waves w = 4 .. 7 issue four Q and four dO blocks a granule, plus lse (wave 4) and delta (wave 5).
+    auto issue = [&](int x) {
+      if (x < nh)
+        for (int w = 4; w < W; ++w) wg.issue(w, {x % qs}, 1000 + x, 4 + (w == 4 ? 1 : 0));
     };
-    auto issue_do = [&](int w, int x) {
-      if (x < nh) wg.issue(w, {4 + x % ds}, 2000 + x, 2 + (w == 4 ? 1 : 0));
+    auto issue_do = [&](int x) {
+      if (x < nh)
+        for (int w = 4; w < W; ++w) wg.issue(w, {5 + x % ds}, 2000 + x, 4 + (w == 5 ? 1 : 0));
     };
-    for (int w = 0; w < W; ++w) {
-      wg.issue(w, staging(w), 3000 + w, 16);  // 32 rows of 512 bytes, 1 KB per instruction
-      issue_q(w, 0);
-    }
+    for (int w = 0; w < 4; ++w) wg.issue(w, staging(w), 3000 + w, 16);
+    issue(0);
     wg.barrier_all(0);
-    for (int w = 0; w < W; ++w) wg.read(w, 20 + w, 3000 + w);
+    for (int w = 0; w < 4; ++w) wg.read(w, 20 + w, 3000 + w);
     wg.barrier_all(-1);
-    for (int h = -1; h <= nh; ++h) {
+    for (int h = -1; h <= nh + 1; ++h) {
       if (h >= 0) wg.barrier_all(0);
       for (int w = 0; w < W; ++w) {
-        const bool a = w < 4;
-        if (a) {
-          if (h + 1 < nh) wg.read(w, (h + 1) % qs, 1000 + h + 1);          // S of granule h + 1: Q rows
-          if (h >= 0 && h < nh) wg.read(w, h % qs, 1000 + h);             // softmax of h: lse
-          if (h >= 1) wg.read(w, 4 + (h - 1) % ds, 2000 + h - 1);         // dV of h - 1: dO^T
+        const int role = (w & 1) + (w >= 4 ? 2 : 0);  // 0 A, 1 B, 2 A', 3 B'
+        if (role == 0) {
+          if (h + 1 < nh) wg.read(w, (h + 1) % qs, 1000 + h + 1);      // S of h + 1: Q rows
+          if (h >= 0 && h < nh) wg.read(w, h % qs, 1000 + h);         // softmax of h: lse
+          if (h >= 1 && h <= nh) wg.read(w, 5 + (h - 1) % ds, 2000 + h - 1);  // dV of h - 1: dO^T
+        } else if (role == 1) {
+          if (h >= 0 && h < nh) wg.read(w, 5 + h % ds, 2000 + h);     // dP of h: dO rows
+          if (h >= 1 && h <= nh) {
+            wg.read(w, 5 + (h - 1) % ds, 2000 + h - 1);               // dS of h - 1: delta
+            wg.read(w, 8 + ((h - 1) & 1), 5000 + h - 1);              // P of h - 1 from A
+            wg.read(w, (h - 1) % qs, 1000 + h - 1);                   // dK of h - 1: Q^T
+          }
+        } else if (role == 2) {
+          if (h >= 1 && h <= nh) {
+            wg.read(w, 8 + ((h - 1) & 1), 5000 + h - 1);              // P of h - 1 from A
+            wg.read(w, 5 + (h - 1) % ds, 2000 + h - 1);               // dV of h - 1: dO^T
+          }
         } else {
-          if (h >= 0 && h < nh) wg.read(w, 4 + h % ds, 2000 + h);         // dP of h: dO rows
-          if (h >= 1) {
-            wg.read(w, 4 + (h - 1) % ds, 2000 + h - 1);                   // dS of h - 1: delta
-            wg.read(w, 7 + ((h - 1) & 1), 5000 + h - 1);                  // P of h - 1 from A
-            wg.read(w, (h - 1) % qs, 1000 + h - 1);                       // dK of h - 1: Q^T
+          if (h >= 2 && h <= nh + 1) {
+            wg.read(w, 10 + ((h - 2) & 1), 6000 + h - 2);             // dS of h - 2 from B
+            wg.read(w, (h - 2) % qs, 1000 + h - 2);                   // dK of h - 2: Q^T
           }
         }
       }
-      for (int w = 0; w < W; ++w) {
-        issue_q(w, q256_loaded(h));
-        issue_do(w, do256_loaded(h));
-      }
-      // A writes P of granule h (ds_write, no VMEM count): an instant fill in this epoch.
+      issue(q256q_loaded(h));
+      issue_do(do256q_loaded(h));
+      // A writes P of h, B writes dS of h - 1 (ds_write, no VMEM count): instant fills in this epoch.
       if (h >= 0 && h < nh)
-        for (int w = 0; w < 4; ++w) wg.issue(w, {7 + (h & 1)}, 5000 + h, 0);
+        for (int w = 0; w < 4; w += 2) wg.issue(w, {8 + (h & 1)}, 5000 + h, 0);
+      if (h >= 1 && h <= nh)
+        for (int w = 1; w < 4; w += 2) wg.issue(w, {10 + ((h - 1) & 1)}, 6000 + h - 1, 0);
     }
     wg.check();
   }
@@ -631,7 +635,7 @@ int main() {
       // dK/dV (dkv_pp_launch): D = 64 zig on a resident grid; D = 128 the role split.
       check_dkv(64, bh, S, resident((long long)((S + 127) / 128) * bh, 2, kCus));
       check_dkv(128, bh, S, false);
-      check_dkv256(bh, S, S, true);  // D = 256: the role split on slabs
+      check_dkv256q(bh, S, S, true);  // D = 256: one pass, four roles
       launches += 10;
     }
   for (int bh : {1, 3, 8})
@@ -639,7 +643,7 @@ int main() {
       for (int D : {256, 384, 1024}) check_wide(bh, S, D);
   for (int bh : {1, 3})
     for (int sq : {1, 100, 200, 260})
-      for (int sk : {1, 100, 260}) check_dkv256(bh, sq, sk, false), ++launches;
+      for (int sk : {1, 100, 260}) check_dkv256q(bh, sq, sk, false), ++launches;
   // The split at the shapes it was built for, and a cut in each place it can fall.
   for (int bh : {5, 6, 8}) {
     check_fwd(FwdCfg{64, 8, 2, true, true}, bh, 8192);
@@ -669,7 +673,7 @@ int main() {
     check_dq(DqCfg{64, 8, 2, 2, true, true}, 6, 8192);
     check_dkv(128, 2, 1024, false);
     check_dkv(64, 6, 8192, true, true);
-    check_dkv256(2, 1024, 1024, true);
+    check_dkv256q(2, 1024, 1024, true);
     if (failures == before) {
       std::fprintf(stderr, "planted mistake %d (%s) not caught\n", m, planted[m]);
       return 1;

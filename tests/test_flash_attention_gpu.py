@@ -320,7 +320,7 @@ def test_split_long_context_backward(dev, b, h, s, d, fused):
 ])
 def test_backward_d256_bf16(dev, b, h, sq, sk, causal, fused):
     """The bf16 backward at head dim 256 through the C ABI (the pipelined dQ kernel with four waves
-    and a two-slot K/V ring; dK/dV as the role split on 128-column slabs over 32-query granules):
+    and a two-slot K/V ring; dK/dV in one pass, four roles per 32-key block over 32-query granules):
     dQ, dK, dV against the oracle at 2e-2 or twice the reference's own bf16 recipe's error, every
     output written (NaN prefill), in both backward orders."""
     _abi_case(dev, b, h, sq, sk, 256, "bf16", causal, seed=71 + sq, scale=256 ** -0.5, fused=fused)
