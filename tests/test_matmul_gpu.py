@@ -293,8 +293,8 @@ def _ceiling_operands():
     for lane in range(64):
         for e in range(8):
             h = ((lane * 8 + e + 1) * 2654435761) & 0xFFFFFFFF
-            av = round_bf16(np.float32(((h >> 8) & 0xFFFF) * (1.0 / 65536.0) - 0.5))
-            bv = round_bf16(np.float32(((h >> 16) & 0xFF) * (1.0 / 256.0) - 0.5))
+            av = float(np.asarray(round_bf16(np.float32(((h >> 8) & 0xFFFF) * (1.0 / 65536.0) - 0.5))).reshape(-1)[0])
+            bv = float(np.asarray(round_bf16(np.float32(((h >> 16) & 0xFF) * (1.0 / 256.0) - 0.5))).reshape(-1)[0])
             A[lane % 32, 8 * (lane // 32) + e] = av
             B[8 * (lane // 32) + e, lane % 32] = bv
     return A, B
