@@ -268,7 +268,7 @@ __global__ __launch_bounds__((WM * WN * 64), 1) void gemm_kernel(const T* __rest
 // blockIdx.y selects one of several groups of S slices, whose sums go to the f32
 // partial slab blockIdx.y of `out` for gemm_splitk_reduce_kernel.
 //
-// With 16-byte rows (ALIGNED) the k-steps are software-pipelined: two register
+// The k-steps are software-pipelined: two register
 // stages, the loads of step kt + 2 and the LDS writes of step kt + 1 (loaded a
 // whole step earlier) issued one at a time between step kt's products, so that
 // neither waits in a burst at the step's edge (loads issued together after the
@@ -276,10 +276,11 @@ __global__ __launch_bounds__((WM * WN * 64), 1) void gemm_kernel(const T* __rest
 // are bounds-checked buffer loads with per-lane offsets fixed for the kernel and
 // the descriptor's base moved per step on the scalar unit; the y descriptor's
 // range ends at the slice's last k row, and x columns past it read as zeros
-// through the offset of a partial step. Measured on one MI355X against the
-// loop with one register stage (both bitwise equal): 1000^3 26.7 -> 23.8 us with
-// the two stages, -> 21.4 us (at K = 1024) with the loads spread and their
-// offsets fixed; 1000 x 1000 x 8192 147 -> 130 us.
+// through the offset of a partial step. 16-byte rows (ALIGNED) load 4-float
+// vectors, other rows single floats. Measured on one MI355X against the loop
+// with one register stage (both bitwise equal): 1000^3 26.7 -> 23.8 us with the
+// two stages, -> 21.4 us (at K = 1024) with the loads spread and their offsets
+// fixed; 1000 x 1000 x 8192 147 -> 130 us; 1000 x 1003 x 999 40.0 -> 30.9 us.
 template <typename TO, int S, bool ALIGNED>
 __global__ __launch_bounds__(128 * S, 1) void gemm_f32_slices_kernel(const float* __restrict__ x,
                                                                     const float* __restrict__ y,
@@ -316,105 +317,109 @@ __global__ __launch_bounds__(128 * S, 1) void gemm_f32_slices_kernel(const float
   const int64_t kbeg = kslice * ((int64_t)blockIdx.y * S + slice), kend = std::min(K, kbeg + kslice);
   out += (int64_t)blockIdx.y * M * N;
   const int nk = (int)(kslice / 32);
-  if constexpr (ALIGNED) {
-    // Offsets in bytes from the slice's first x column of row m0 and first y row at column
-    // n0 (the launcher keeps them under 2^31); rows past M and columns past N get an offset
-    // past every range and read zeros.
-    const int lane = threadIdx.x & 63;
-    const int l32 = lane & 31, g = lane >> 5;
-    uint32_t xv[4], yv[4];
+  // Offsets in bytes from the slice's first x column of row m0 and first y row at column n0
+  // (the launcher keeps them under 2^31); rows past M and columns past N get an offset past
+  // every range and read zeros. With 16-byte rows (ALIGNED) a load moves a 4-float vector,
+  // otherwise one float (8 or 32 loads per thread and stage).
+  constexpr int kPer = ALIGNED ? 1 : 4, kLoads = 8 * kPer;
+  const int lane = threadIdx.x & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+  uint32_t xv[4], yv[4];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {  // x vector p: row (t + 128 p) / 8, columns 4 (t % 8) ..
-      const int row = (t + 128 * p) >> 3;
-      xv[p] = m0 + row < M ? (uint32_t)((row * K + (t & 7) * 4) * 4) : 0x80000000u;
+  for (int p = 0; p < 4; ++p) {  // x vector p: row (t + 128 p) / 8, columns 4 (t % 8) ..
+    const int row = (t + 128 * p) >> 3;
+    xv[p] = m0 + row < M ? (uint32_t)((row * K + (t & 7) * 4) * 4) : 0x80000000u;
+  }
+  const int ycol = (t & 15) * 4, yrow = (t >> 4) * 4;  // y job: k rows yrow .. + 3, columns ycol ..
+#pragma unroll
+  for (int r = 0; r < 4; ++r) yv[r] = n0 + ycol < N ? (uint32_t)(((yrow + r) * N + ycol) * 4) : 0x80000000u;
+  const int ycols = (int)std::min<int64_t>(N - n0 - ycol, 4);  // columns of the job inside N
+  // The slice is wave-uniform; readfirstlane says so, and the per-step bases stay scalar.
+  auto uni = [](const float* ptr) {
+    const uint64_t a = reinterpret_cast<uint64_t>(ptr);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+    return reinterpret_cast<const float*>(((uint64_t)hi << 32) | lo);
+  };
+  const float* const xs = uni(x + m0 * K + kbeg);
+  const float* const ys = uni(y + kbeg * N + n0);
+  const int klen = __builtin_amdgcn_readfirstlane((int)(kend - kbeg));  // k rows of the slice (<= 0 past K)
+  // Load i of stage kt: x vector i / kPer (below 4) or y row yrow + i / kPer - 4; element
+  // i % kPer of it without ALIGNED. The y descriptor's range ends at the slice's last k row.
+  auto load_one = [&](typename G::Stage& st, int kt, int i) {
+    const int rem = klen - kt * 32;
+    const int vi = i / kPer, e = i % kPer;
+    if (vi < 4) {
+      const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)(xs + kt * 32), 0, 0x7ffffff0, 0x00020000);
+      const uint32_t off = rem >= 32 || (t & 7) * 4 + e < rem ? xv[vi] + 4 * e : 0x80000000u;
+      if constexpr (ALIGNED)
+        st.a[vi] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+      else
+        st.a[vi][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+    } else {
+      // readfirstlane: the clamp would otherwise become a VALU med3, and the descriptor a VGPR.
+      const int rows = __builtin_amdgcn_readfirstlane(rem < 0 ? 0 : rem < 32 ? rem : 32);
+      const __amdgpu_buffer_rsrc_t r =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(ys + (int64_t)kt * 32 * N), 0, rows * (int)N * 4, 0x00020000);
+      if constexpr (ALIGNED)
+        st.b[0][vi - 4] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)yv[vi - 4], 0, 0));
+      else
+        st.b[0][vi - 4][e] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(r, e < ycols ? (int)(yv[vi - 4] + 4 * e) : (int)0x80000000, 0, 0));
     }
-    const int ycol = (t & 15) * 4, yrow = (t >> 4) * 4;  // y job: k rows yrow .. + 3, columns ycol ..
+  };
+  typename G::Stage st0, st1;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) yv[r] = n0 + ycol < N ? (uint32_t)(((yrow + r) * N + ycol) * 4) : 0x80000000u;
-    // The slice is wave-uniform; readfirstlane says so, and the per-step bases stay scalar.
-    auto uni = [](const float* ptr) {
-      const uint64_t a = reinterpret_cast<uint64_t>(ptr);
-      const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-      const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
-      return reinterpret_cast<const float*>(((uint64_t)hi << 32) | lo);
+  for (int i = 0; i < kLoads; ++i) load_one(st0, 0, i);
+  G::store(st0, lds, t);
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) load_one(st1, 1, i);
+  __syncthreads();
+  // Step kt: products from LDS stage kt & 1 in four groups of 4 k pairs (k = 16 (q / 2) +
+  // 8 g + 4 (q % 2) + e for lane group g, the order G::compute uses), the next group's
+  // fragments read ahead; between the 16 product pairs, the loads of stage kt + 2 into
+  // `refill` (one per pair, or two) and the 8 LDS writes of stage kt + 1 from `next`.
+  auto step = [&](int kt, typename G::Stage& refill, const typename G::Stage& next) {
+    const char* cur = lds + (kt & 1) * G::kStageBytes;
+    char* nxt = lds + ((kt + 1) & 1) * G::kStageBytes;
+    f32x4 fa0[2], fa1[2], fb[2];
+    auto rd = [&](int q) {
+      const int k0 = (q >> 1) * 16 + g * 8 + (q & 1) * 4;
+      fa0[q & 1] = *reinterpret_cast<const f32x4*>(cur + lds_off<float>(l32, k0));
+      fa1[q & 1] = *reinterpret_cast<const f32x4*>(cur + lds_off<float>(32 + l32, k0));
+      fb[q & 1] = *reinterpret_cast<const f32x4*>(cur + 64 * 128 + lds_off<float>(wn0 + l32, k0));
     };
-    const float* const xs = uni(x + m0 * K + kbeg);
-    const float* const ys = uni(y + kbeg * N + n0);
-    const int klen = __builtin_amdgcn_readfirstlane((int)(kend - kbeg));  // k rows of the slice (<= 0 past K)
-    // Load i of stage kt: x vector i (i < 4) or y row yrow + i - 4.
-    auto load_one = [&](typename G::Stage& st, int kt, int i) {
-      const int rem = klen - kt * 32;
-      if (i < 4) {
-        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)(xs + kt * 32), 0, 0x7ffffff0, 0x00020000);
-        const uint32_t off = rem >= 32 || (t & 7) * 4 < rem ? xv[i] : 0x80000000u;
-        st.a[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-      } else {
-        // readfirstlane: the clamp would otherwise become a VALU med3, and the descriptor a VGPR.
-        const int rows = __builtin_amdgcn_readfirstlane(rem < 0 ? 0 : rem < 32 ? rem : 32);
-        const __amdgpu_buffer_rsrc_t r =
-            __builtin_amdgcn_make_buffer_rsrc((void*)(ys + (int64_t)kt * 32 * N), 0, rows * (int)N * 4, 0x00020000);
-        st.b[0][i - 4] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)yv[i - 4], 0, 0));
-      }
-    };
-    typename G::Stage st0, st1;
+    rd(0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) load_one(st0, 0, i);
-    G::store(st0, lds, t);
+    for (int q = 0; q < 4; ++q) {
+      if (q + 1 < 4) rd(q + 1);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) load_one(st1, 1, i);
-    __syncthreads();
-    // Step kt: products from LDS stage kt & 1 in four groups of 4 k pairs (k = 16 (q / 2) +
-    // 8 g + 4 (q % 2) + e for lane group g, the order G::compute uses), the next group's
-    // fragments read ahead; between the product pairs, alternately one load of stage kt + 2
-    // into `refill` and one LDS write of stage kt + 1 from `next`.
-    auto step = [&](int kt, typename G::Stage& refill, const typename G::Stage& next) {
-      const char* cur = lds + (kt & 1) * G::kStageBytes;
-      char* nxt = lds + ((kt + 1) & 1) * G::kStageBytes;
-      f32x4 fa0[2], fa1[2], fb[2];
-      auto rd = [&](int q) {
-        const int k0 = (q >> 1) * 16 + g * 8 + (q & 1) * 4;
-        fa0[q & 1] = *reinterpret_cast<const f32x4*>(cur + lds_off<float>(l32, k0));
-        fa1[q & 1] = *reinterpret_cast<const f32x4*>(cur + lds_off<float>(32 + l32, k0));
-        fb[q & 1] = *reinterpret_cast<const f32x4*>(cur + 64 * 128 + lds_off<float>(wn0 + l32, k0));
-      };
-      rd(0);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (q + 1 < 4) rd(q + 1);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[q & 1][e], fa0[q & 1][e], acc[0][0], 0, 0, 0);
-          acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[q & 1][e], fa1[q & 1][e], acc[0][1], 0, 0, 0);
-          const int pi = q * 4 + e;
+      for (int e = 0; e < 4; ++e) {
+        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[q & 1][e], fa0[q & 1][e], acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[q & 1][e], fa1[q & 1][e], acc[0][1], 0, 0, 0);
+        const int pi = q * 4 + e;
+        if constexpr (ALIGNED) {
           if ((pi & 1) == 0)
             load_one(refill, kt + 2, pi >> 1);
           else
             G::store_part(next, nxt, t, pi >> 1);
-          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          load_one(refill, kt + 2, 2 * pi);
+          load_one(refill, kt + 2, 2 * pi + 1);
+          if (pi & 1) G::store_part(next, nxt, t, pi >> 1);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __syncthreads();
-    };
-    // kslice is a multiple of 64, so nk is even and every pass runs both steps (a step
-    // behind a branch would leave the wait counts at the loop head unsettled). Stages past
-    // the slice read zeros and are never multiplied.
-    for (int kt = 0; kt < nk; kt += 2) {
-      step(kt, st0, st1);
-      step(kt + 1, st1, st0);
     }
-  } else {
-    typename G::Stage st;
-    G::load(st, x, y, m0, n0, kbeg, M, N, K, kend, t);
-    G::store(st, lds, t);
     __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      char* cur = lds + (kt & 1) * G::kStageBytes;
-      if (kt + 1 < nk) G::load(st, x, y, m0, n0, kbeg + (int64_t)(kt + 1) * 32, M, N, K, kend, t);
-      G::compute(cur, acc, 0, wn0);
-      if (kt + 1 < nk) G::store(st, lds + ((kt + 1) & 1) * G::kStageBytes, t);
-      __syncthreads();
-    }
+  };
+  // kslice is a multiple of 64, so nk is even and every pass runs both steps (a step behind a
+  // branch would leave the wait counts at the loop head unsettled). Stages past the slice
+  // read zeros and are never multiplied.
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(kt, st0, st1);
+    step(kt + 1, st1, st0);
   }
 
   // Slice s > 0 writes register r of accumulator i of its lane to dword
@@ -436,8 +441,6 @@ __global__ __launch_bounds__(128 * S, 1) void gemm_f32_slices_kernel(const float
       for (int r = 0; r < 16; ++r) acc[0][i][r] += xch[((s2 - 1) * 32 + i * 16 + r) * 128 + t];
 
   // Register r of accumulator i of lane (l32, g): C[m0 + i*32 + l32][n0 + wn0 + (r/4)*8 + g*4 + r%4].
-  const int lane = threadIdx.x & 63;
-  const int l32 = lane & 31, g = lane >> 5;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int64_t m = m0 + i * 32 + l32;
@@ -922,9 +925,7 @@ void launch_gemm_f32_slices(const float* x, const float* y, TO* out, int64_t M, 
   static_assert((S - 1) * 32 * 128 * 4 <= S * 2 * G::kStageBytes, "the slices' accumulators fit the stages");
   const int64_t kslice = cdiv(cdiv(K, (int64_t)S * groups), (int64_t)64) * 64;
   auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  // The pipelined loop's lane offsets (64 x rows of K, 32 y rows of N) stay under 2^31 bytes.
-  const bool aligned = K % 4 == 0 && N % 4 == 0 && a16(x) && a16(y) && a16(out) && 64 * K * 4 < 0x7ffffff0 &&
-                       32 * N * 4 < 0x7ffffff0;
+  const bool aligned = K % 4 == 0 && N % 4 == 0 && a16(x) && a16(y) && a16(out);
   auto go = [&](auto kern) {
     (void)allow_lds((const void*)kern, (int)lds, stream, "ferrite_matmul");  // a failure resurfaces as the launch's error
     hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)groups), dim3(128 * S), lds, stream, x, y, out, M, N, K,
@@ -959,8 +960,10 @@ int launch_gemm_f32_small(const void* x, const void* y, void* out, int64_t M, in
   F32Split sp = f32_split(M, N, K, cus);
   if (sp.g > 1 && (ws == nullptr || ws_bytes < f32_workspace(M, N, K, cus) || (reinterpret_cast<uintptr_t>(ws) & 15)))
     sp.g = 1;
-  if (sp.s == 4) return launch_gemm_f32_split<TO, 4>(x, y, out, M, N, K, sp.g, ws, stream);
-  if (sp.s == 2) return launch_gemm_f32_split<TO, 2>(x, y, out, M, N, K, sp.g, ws, stream);
+  // The sliced kernel's lane offsets (64 x rows of K, 32 y rows of N bytes) stay under 2^31.
+  const bool offsets_fit = 64 * K * 4 < 0x7ffffff0 && 32 * N * 4 < 0x7ffffff0;
+  if (offsets_fit && sp.s == 4) return launch_gemm_f32_split<TO, 4>(x, y, out, M, N, K, sp.g, ws, stream);
+  if (offsets_fit && sp.s == 2) return launch_gemm_f32_split<TO, 2>(x, y, out, M, N, K, sp.g, ws, stream);
   return launch_gemm<float, TO, 64, 64, 32, 1, 2>(x, y, out, M, N, K, stream);
 }
 
