@@ -2586,11 +2586,11 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
     const bf16x8(&dsp)[2] = dsf[1 - P];
     // Tiles and halves: SDP reads half h + 1, SG half h, GRAD half h - 1.
     const char* sl_n = slot((h + 1) >> 1);
-    const int half_n = (h + 1) & 1;
+    const int half_n = 1 - P;  // h & 1 == P
     const char* sl_c = slot(h >> 1);
-    const int half_c = h & 1;
+    const int half_c = P;
     const char* sl_p = slot((h - 1) >> 1);
-    const int half_p = (h - 1) & 1;
+    const int half_p = 1 - P;
     constexpr int NS = SDP ? 2 * KS : 0;  // S (even) and dP (odd) products over the k-chunks
     constexpr int NG = GRAD ? 4 * DT : 0;  // per output tile: two key chunks, dV (even) and dK (odd)
     constexpr int NF = NS + NG;
@@ -2945,20 +2945,24 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
       bf16x8(&pc)[2] = pf[P];
       const bf16x8(&pp)[2] = pf[1 - P];
       const char* sl_n = slot((h + 1) >> 1);  // S of half h + 1: Q rows
-      const int half_n = (h + 1) & 1;
+      const int half_n = 1 - P;  // h & 1 == P
       const char* sl_p = slot((h - 1) >> 1);  // dV of half h - 1: dO^T
-      const int half_p = (h - 1) & 1;
-      const int half_c = h & 1;
+      const int half_p = 1 - P;
+      const int half_c = P;
       // The S products come first and the dV products, with the softmax between
       // them, second: B's VALU work sits in the first half of its half-step, so
       // the two waves of a SIMD alternate between products and VALU work.
       constexpr int NS = SDP ? KS : 0;       // S: k-chunk i
       constexpr int NG = GRAD ? 2 * DT : 0;  // dV: output tile u = i / 2, query chunk i % 2
       constexpr int NF = NS + NG;
+      // One lane address per read kind and half-step, opaque to the compiler: otherwise it
+      // hoists a lane address per fragment out of the loop and adds the slot to each.
+      int ro = (int)(sl_n - smem) + tb.r, to = (int)(sl_p - smem) + Tile::kBytes + tb.t;
+      asm volatile("" : "+v"(ro), "+v"(to));
       auto read = [&](int f) -> bf16x8 {
-        if (f < NS) return *reinterpret_cast<const bf16x8*>(sl_n + Tile::row(tb, half_n, f));
+        if (f < NS) return *reinterpret_cast<const bf16x8*>(smem + ro + Tile::row_at(half_n, f));
         const int i = f - NS;
-        return tr_frag(sl_p + Tile::kBytes + Tile::tr(tb, half_p, i & 1, i >> 1), Tile::kTrHi);
+        return tr_frag(smem + to + Tile::tr_at(half_p, i & 1, i >> 1), Tile::kTrHi);
       };
       auto prod = [&](int f, const bf16x8& a) {
         if (f < NS) {
@@ -3076,16 +3080,19 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
       f32x16& dpn = dpa[P];             // dP of half h
       const f32x16& dpc = dpa[1 - P];   // dP of half h - 1
       const char* sl_c = slot(h >> 1);  // dP of half h: dO rows
-      const int half_c = h & 1;
+      const int half_c = P;
       const char* sl_p = slot((h - 1) >> 1);  // dS and dK of half h - 1: Q^T, delta
-      const int half_p = (h - 1) & 1;
+      const int half_p = 1 - P;
       constexpr int NS = SDP ? KS : 0;       // dP: k-chunk i
       constexpr int NG = GRAD ? 2 * DT : 0;  // dK: output tile u = i / 2, query chunk i % 2
       constexpr int NF = NS + NG;
+      // One lane address per read kind and half-step (as role A's).
+      int ro = (int)(sl_c - smem) + Tile::kBytes + tb.r, to = (int)(sl_p - smem) + tb.t;
+      asm volatile("" : "+v"(ro), "+v"(to));
       auto read = [&](int f) -> bf16x8 {
-        if (f < NS) return *reinterpret_cast<const bf16x8*>(sl_c + Tile::kBytes + Tile::row(tb, half_c, f));
+        if (f < NS) return *reinterpret_cast<const bf16x8*>(smem + ro + Tile::row_at(half_c, f));
         const int i = f - NS;
-        return tr_frag(sl_p + Tile::tr(tb, half_p, i & 1, i >> 1), Tile::kTrHi);
+        return tr_frag(smem + to + Tile::tr_at(half_p, i & 1, i >> 1), Tile::kTrHi);
       };
       auto prod = [&](int f, const bf16x8& a) {
         if (f < NS) {
