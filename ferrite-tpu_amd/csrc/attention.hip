@@ -2448,6 +2448,20 @@ __device__ __forceinline__ void stat_dma(const float* base, int r0, int nrows, c
                : "memory", "m0");
 }
 
+// One statistics row (64 floats from row r0 of base, zeros past nrows) into
+// registers: lane L gets row r0 + L. A bounds-checked buffer load, counted in
+// vmcnt like the DMA it replaces.
+__device__ __forceinline__ float stat_load(const float* base, int r0, int nrows) {
+  const int lane = threadIdx.x & 63;
+  const int rows_left = nrows - r0 > 0 ? nrows - r0 : 0;
+  const uint64_t addr = reinterpret_cast<uint64_t>(base + r0);
+  const uint64_t ua = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(addr >> 32)) << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<void*>(ua), 0, __builtin_amdgcn_readfirstlane(rows_left * 4), 0x00020000);
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, 0, 0));
+}
+
 // dK, dV, software-pipelined (the forward's scheme); D = 64 (D = 128 runs
 // attn_dkv_rs_kernel below, which splits a key block over two waves). Half-step h of a wave
 // (32 queries) first issues dV^T += dO^T P and dK^T += Q^T dS for half h - 1
@@ -2878,6 +2892,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
   char* const xring = smem + F::kSlots * F::kSlotBytes;
   // P of half h, pair p: chunk c (four queries) of lane L at xbuf(h) + p 4096 + c 1024 + 16 L.
   auto xbuf = [&](int h) { return xring + (h & 1) * F::kXBytes + pair * 4096; };
+  // The lse row of a tile comes into wave 0's registers with the tile's DMA and goes to
+  // the tile's slot scaled by -log2(e) at the next odd half-step (the first after the
+  // barrier that waited for it), so that the softmax spends no multiply on it per element.
+  float lse_next = 0.f;
   // DMA instruction qd of tile t; rows past the end of the queries arrive as
   // zeros (empty buffer range), which the padded sweeps rely on.
   auto dma_part = [&](int t, int qd) {
@@ -2887,8 +2905,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
       dma.issue_one(qb, r0, Sq, ldq, sl, qd);
     else if (qd < 2 * F::kDma)
       (SAMEP ? dma : dma_do).issue_one(dob, r0, Sq, SAMEP ? ldq : lddo, sl + Tile::kBytes, qd - F::kDma);
+    else if (pair == 0 && role)
+      stat_dma(db, r0, Sq, sl + 2 * Tile::kBytes + 1024);
     else if (pair == 0)
-      stat_dma(role ? db : lseb, r0, Sq, sl + 2 * Tile::kBytes + role * 1024);
+      lse_next = stat_load(lseb, r0, Sq);
   };
 #pragma unroll
   for (int qd = 0; qd < kTileDma; ++qd) dma_part(0, qd);
@@ -2944,6 +2964,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
       f32x16& sn = sa[1 - P];
       bf16x8(&pc)[2] = pf[P];
       const bf16x8(&pp)[2] = pf[1 - P];
+      // Odd half-steps: wave 0 writes the lse row of tile (h + 1) / 2, loaded at h - 2 and
+      // waited for at this half-step's barrier; read from half-step h + 1 on.
+      if constexpr (P == 1)
+        if (pair == 0) reinterpret_cast<float*>(slot((h + 1) >> 1) + 2 * Tile::kBytes)[lane] = -lse_next * kLog2e;
       const char* sl_n = slot((h + 1) >> 1);  // S of half h + 1: Q rows
       const int half_n = 1 - P;  // h & 1 == P
       const char* sl_p = slot((h - 1) >> 1);  // dV of half h - 1: dO^T
@@ -2985,7 +3009,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkv_rs_kernel(const bf16* __restr
       auto sg_elem = [&](int r) {
         if ((r & 3) == 0 && (r >> 2) + 1 < 4) ls[((r >> 2) + 1) & 1] = *reinterpret_cast<const f32x4*>(st + 4 * ((r >> 2) + 1));
         const f32x4& l4 = ls[(r >> 2) & 1];
-        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, -l4[r & 3] * kLog2e));
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, l4[r & 3]));  // l4: -lse log2(e)
         if constexpr (MASK) p = (causal && kvrow > qh + r) ? 0.f : p;
         pv[r & 7] = p;
         p4[r & 3] = p;

@@ -163,6 +163,8 @@ static bool fwd_writes(int kh, int role) { return g_mutation == 5 ? role != 0 : 
 static int rs_loaded(int h) { return g_mutation == 6 ? ((h & 1) ? (h + 5) >> 1 : -1) : dkv_rs_loaded(h); }
 static int q256q_loaded(int h) { return g_mutation == 9 ? h + 3 : dkv256q_q_loaded(h); }   // Q into a slot in use
 static int do256q_loaded(int h) { return g_mutation == 10 ? h + 2 : dkv256q_do_loaded(h); }  // dO into a slot in use
+// The half-step in which wave 0 of attn_dkv_rs_kernel writes tile t's scaled lse row (2t - 1).
+static int rs_lse_write(int t) { return g_mutation == 11 ? 2 * t : 2 * t - 1; }  // a half-step late
 constexpr int BK = 64;  // keys per tile of the forward and dQ rings, queries per tile of dK/dV's
 
 // ---------------------------------------------------------------------------
@@ -447,8 +449,17 @@ static void check_dkv(int D, int bh, int S, bool zig, bool split = false) {
         // buffers. Region 20 + w is wave w's own piece.
         const std::vector<int> staging[8] = {{2, 20}, {2, 21}, {2, 22}, {2, 23},
                                              {2, 11, 24}, {11, 25}, {11, 12, 26}, {12, 27}};
+        // Wave 0's statistics instruction loads the tile's lse row into registers (no LDS
+        // region); it writes the row, scaled, into region 30 + t % slots at odd half-step
+        // 2t - 1 (tile 0: -1), a ds_write modelled as an instant fill, and role A reads it
+        // in the tile's two softmax half-steps.
+        auto issue_tile = [&](int w, int t) {
+          const int lse_reg = w == 0 ? 1 : 0;
+          wg.issue(w, {t % slots}, sbase + 1000 + t, tile_ops(w) - lse_reg);
+          wg.vmem(w, lse_reg);
+        };
         for (int w = 0; w < W; ++w) {
-          wg.issue(w, {0}, sbase + 1000, tile_ops(w));
+          issue_tile(w, 0);
           wg.issue(w, staging[w], sbase + 3000 + w, 8);  // 32 rows of 256 bytes, 1 KB per instruction
         }
         for (int h = -1; h <= nh; ++h) {
@@ -456,15 +467,19 @@ static void check_dkv(int D, int bh, int S, bool zig, bool split = false) {
           wg.barrier(fl);
           if (h == -1)
             for (int w = 0; w < W; ++w) wg.read(w, 20 + w, sbase + 3000 + w);  // the rows back, in stage -1
+          for (int t = std::max(h >> 1, 0); t <= ((h + 2) >> 1); ++t)
+            if (rs_lse_write(t) == h) wg.issue(0, {30 + t % slots}, sbase + 7000 + t, 0);
           for (int w = 0; w < W; ++w) {
             for (int t = std::max((h - 1) >> 1, 0); t <= ((h + 1) >> 1) && t < nt; ++t)
               if (dkv_rs_first_read(t) <= h && h <= dkv_rs_last_read(t) && h <= nh) wg.read(w, t % slots, sbase + 1000 + t);
             // P of half h - 1 from A (written in half-step h - 1), read by B in h.
             if (w >= 4 && h >= 1) wg.read(w, 11 + ((h - 1) & 1), sbase + 5000 + h - 1);
+            // The lse row of the half's tile, in role A's softmax.
+            if (w < 4 && h >= 0 && h <= nh - 1) wg.read(w, 30 + (h >> 1) % slots, sbase + 7000 + (h >> 1));
           }
           const int t = rs_loaded(h);
           if (t >= 0)
-            for (int w = 0; w < W; ++w) wg.issue(w, {t % slots}, sbase + 1000 + t, tile_ops(w));
+            for (int w = 0; w < W; ++w) issue_tile(w, t);
           // A writes P of half h (ds_write, no VMEM count), modelled as an
           // instant fill of that buffer in this epoch.
           if (h >= 0 && h <= nh - 1)
@@ -659,8 +674,9 @@ int main() {
                            "dQ tile loaded into a slot in use", "O rows written by both halves of a pair",
                            "dK/dV tile loaded a half-step pair early", "split dQ rows written by both shares",
                            "split dK/dV rows written by both shares", "D = 256 Q granule loaded into a slot in use",
-                           "D = 256 dO granule loaded into a slot in use"};
-  constexpr int kPlanted = 10;
+                           "D = 256 dO granule loaded into a slot in use",
+                           "D = 128 lse row written a half-step late"};
+  constexpr int kPlanted = 11;
   quiet = true;
   for (int m = 1; m <= kPlanted; ++m) {
     g_mutation = m;
