@@ -2647,11 +2647,19 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
     };
     // Softmax gradient of half h: element r (query 16 g + r of the half).
     const float* st = reinterpret_cast<const float*>(sl_c + 2 * Tile::kBytes) + 32 * half_c + 16 * g;
+    // The lse row scaled by -log2(e), 512 bytes into the lse row's 1 KB of DMA space (which
+    // holds zeros past the row): each wave writes the whole row at the tile's first softmax
+    // half-step (P == 0) from the landed row and reads its part after its own write, so
+    // every wave sees it without a barrier (the waves write the same values), and the
+    // softmax spends no multiply on it per element.
+    float* const lsc = reinterpret_cast<float*>(slot(h >> 1) + 2 * Tile::kBytes + 512);
+    if constexpr (SG && P == 0) lsc[lane] = -reinterpret_cast<const float*>(sl_c + 2 * Tile::kBytes)[lane] * kLog2e;
+    const float* const stl = lsc + 32 * half_c + 16 * g;
     const int qh = (first + (h >> 1)) * F::BQ + 32 * half_c + 16 * g;
-    // lse and delta of queries 4 c .. 4 c + 3, read one group ahead of use.
+    // -lse log2(e) and delta of queries 4 c .. 4 c + 3, read one group ahead of use.
     f32x4 ls[2], dl[2];
     auto read_stats = [&](int c) {
-      ls[c & 1] = *reinterpret_cast<const f32x4*>(st + 4 * c);
+      ls[c & 1] = *reinterpret_cast<const f32x4*>(stl + 4 * c);
       dl[c & 1] = *reinterpret_cast<const f32x4*>(st + 256 + 4 * c);
     };
     float pv[8], dsv[8];
@@ -2659,7 +2667,7 @@ __global__ __launch_bounds__(256, DkvPp<D>::kMinBlocks) void attn_dkv_sw_kernel(
       if ((r & 3) == 0 && (r >> 2) + 1 < 4) read_stats((r >> 2) + 1);
       const f32x4& l4 = ls[(r >> 2) & 1];
       const f32x4& d4 = dl[(r >> 2) & 1];
-      float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, -l4[r & 3] * kLog2e));
+      float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, l4[r & 3]));
       if constexpr (MASK) p = (causal && kvrow > qh + r) ? 0.f : p;
       pv[r & 7] = p;
       dsv[r & 7] = p * (dpc[r] - d4[r & 3]);
