@@ -281,13 +281,19 @@ __global__ __launch_bounds__((WM * WN * 64), 1) void gemm_kernel(const T* __rest
 // with one register stage (both bitwise equal): 1000^3 26.7 -> 23.8 us with the
 // two stages, -> 21.4 us (at K = 1024) with the loads spread and their offsets
 // fixed; 1000 x 1000 x 8192 147 -> 130 us; 1000 x 1003 x 999 40.0 -> 30.9 us.
-template <typename TO, int S, bool ALIGNED>
-__global__ __launch_bounds__(128 * S, 1) void gemm_f32_slices_kernel(const float* __restrict__ x,
-                                                                    const float* __restrict__ y,
-                                                                    TO* __restrict__ out, int64_t M, int64_t N,
-                                                                    int64_t K, int tiles_n, int64_t kslice) {
-  typedef Gemm<float, TO, 64, 64, 32, 1, 2, ALIGNED> G;
-  static_assert(G::kThreads == 128 && G::kTN == 1 && G::kTM == 2, "two waves of 64 x 32 per slice");
+//
+// BMN = 128 runs the same loop on 128 x 128 tiles of four waves (64 x 64 each), one slice:
+// the f32 products with enough tiles for every CU.
+template <typename TO, int S, bool ALIGNED, int BMN = 64>
+__global__ __launch_bounds__((BMN == 64 ? 128 : 256) * S, 1) void gemm_f32_slices_kernel(
+    const float* __restrict__ x, const float* __restrict__ y, TO* __restrict__ out, int64_t M, int64_t N, int64_t K,
+    int tiles_n, int64_t kslice) {
+  constexpr int WM = BMN / 64;
+  typedef Gemm<float, TO, BMN, BMN, 32, WM, 2, ALIGNED> G;
+  constexpr int kT = G::kThreads, kTM = G::kTM, kTN = G::kTN;
+  static_assert(G::kAVecs == 4 && G::kBJobs == 1, "four x vectors and one y job per thread and stage");
+  static_assert((BMN == 64 && kT == 128 && kTM == 2 && kTN == 1) || (BMN == 128 && S == 1 && kT == 256 && kTM == 2 && kTN == 2),
+                "two waves of 64 x 32 per slice, or four of 64 x 64 and one slice");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   // Blocks are dealt to the 8 XCDs round robin: the tiles of one XCD are made
   // consecutive and walked in groups of 4 tile rows, so that an XCD's L2 holds
@@ -300,17 +306,20 @@ __global__ __launch_bounds__(128 * S, 1) void gemm_f32_slices_kernel(const float
   const int tiles_m = ntiles / tiles_n;
   const int first_m = v / (kGroup * tiles_n) * kGroup;
   const int gsize = min(tiles_m - first_m, kGroup);
-  const int64_t m0 = (int64_t)(first_m + (v % (kGroup * tiles_n)) % gsize) * 64;
-  const int64_t n0 = (int64_t)((v % (kGroup * tiles_n)) / gsize) * 64;
-  const int slice = threadIdx.x >> 7, t = threadIdx.x & 127;
-  const int wn0 = ((threadIdx.x >> 6) & 1) * 32;
+  const int64_t m0 = (int64_t)(first_m + (v % (kGroup * tiles_n)) % gsize) * BMN;
+  const int64_t n0 = (int64_t)((v % (kGroup * tiles_n)) / gsize) * BMN;
+  const int slice = threadIdx.x / kT, t = threadIdx.x % kT;
+  const int ws = t >> 6;  // the wave within its slice
+  const int wm0 = (ws / 2) * G::kWTM, wn0 = (ws % 2) * G::kWTN;
   char* const lds = smem + slice * 2 * G::kStageBytes;
 
-  f32x16 acc[1][2];
+  f32x16 acc[kTN][kTM];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int j = 0; j < kTN; ++j)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[0][i][r] = 0.f;
+    for (int i = 0; i < kTM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
 
   // Every slice runs the same number of k-steps (the workgroup's barriers are
   // shared); a short last slice reads zeros past K.
@@ -326,11 +335,11 @@ __global__ __launch_bounds__(128 * S, 1) void gemm_f32_slices_kernel(const float
   const int l32 = lane & 31, g = lane >> 5;
   uint32_t xv[4], yv[4];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {  // x vector p: row (t + 128 p) / 8, columns 4 (t % 8) ..
-    const int row = (t + 128 * p) >> 3;
+  for (int p = 0; p < 4; ++p) {  // x vector p: row (t + kT p) / 8, columns 4 (t % 8) ..
+    const int row = (t + kT * p) >> 3;
     xv[p] = m0 + row < M ? (uint32_t)((row * K + (t & 7) * 4) * 4) : 0x80000000u;
   }
-  const int ycol = (t & 15) * 4, yrow = (t >> 4) * 4;  // y job: k rows yrow .. + 3, columns ycol ..
+  const int ycol = (t % (BMN / 4)) * 4, yrow = (t / (BMN / 4)) * 4;  // y job: k rows yrow .. + 3, columns ycol ..
 #pragma unroll
   for (int r = 0; r < 4; ++r) yv[r] = n0 + ycol < N ? (uint32_t)(((yrow + r) * N + ycol) * 4) : 0x80000000u;
   const int ycols = (int)std::min<int64_t>(N - n0 - ycol, 4);  // columns of the job inside N
@@ -382,12 +391,14 @@ __global__ __launch_bounds__(128 * S, 1) void gemm_f32_slices_kernel(const float
   auto step = [&](int kt, typename G::Stage& refill, const typename G::Stage& next) {
     const char* cur = lds + (kt & 1) * G::kStageBytes;
     char* nxt = lds + ((kt + 1) & 1) * G::kStageBytes;
-    f32x4 fa0[2], fa1[2], fb[2];
+    f32x4 fa[2][kTM], fb[2][kTN];
     auto rd = [&](int q) {
       const int k0 = (q >> 1) * 16 + g * 8 + (q & 1) * 4;
-      fa0[q & 1] = *reinterpret_cast<const f32x4*>(cur + lds_off<float>(l32, k0));
-      fa1[q & 1] = *reinterpret_cast<const f32x4*>(cur + lds_off<float>(32 + l32, k0));
-      fb[q & 1] = *reinterpret_cast<const f32x4*>(cur + 64 * 128 + lds_off<float>(wn0 + l32, k0));
+#pragma unroll
+      for (int i = 0; i < kTM; ++i) fa[q & 1][i] = *reinterpret_cast<const f32x4*>(cur + lds_off<float>(wm0 + 32 * i + l32, k0));
+#pragma unroll
+      for (int j = 0; j < kTN; ++j)
+        fb[q & 1][j] = *reinterpret_cast<const f32x4*>(cur + BMN * 128 + lds_off<float>(wn0 + 32 * j + l32, k0));
     };
     rd(0);
     __builtin_amdgcn_sched_barrier(0);
@@ -396,8 +407,11 @@ __global__ __launch_bounds__(128 * S, 1) void gemm_f32_slices_kernel(const float
       if (q + 1 < 4) rd(q + 1);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[q & 1][e], fa0[q & 1][e], acc[0][0], 0, 0, 0);
-        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[q & 1][e], fa1[q & 1][e], acc[0][1], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < kTN; ++j)
+#pragma unroll
+          for (int i = 0; i < kTM; ++i)
+            acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[q & 1][j][e], fa[q & 1][i][e], acc[j][i], 0, 0, 0);
         const int pi = q * 4 + e;
         if constexpr (ALIGNED) {
           if ((pi & 1) == 0)
@@ -423,7 +437,8 @@ __global__ __launch_bounds__(128 * S, 1) void gemm_f32_slices_kernel(const float
   }
 
   // Slice s > 0 writes register r of accumulator i of its lane to dword
-  // (i * 16 + r) * 128 + t of its exchange area; slice 0 reads the same places.
+  // (i * 16 + r) * 128 + t of its exchange area; slice 0 reads the same places
+  // (S > 1 runs 64 x 64 tiles only: kTN = 1, 128 threads per slice).
   float* const xch = reinterpret_cast<float*>(smem);
   if (slice > 0) {
 #pragma unroll
@@ -440,31 +455,34 @@ __global__ __launch_bounds__(128 * S, 1) void gemm_f32_slices_kernel(const float
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[0][i][r] += xch[((s2 - 1) * 32 + i * 16 + r) * 128 + t];
 
-  // Register r of accumulator i of lane (l32, g): C[m0 + i*32 + l32][n0 + wn0 + (r/4)*8 + g*4 + r%4].
+  // Register r of accumulator (j, i) of lane (l32, g):
+  // C[m0 + wm0 + i*32 + l32][n0 + wn0 + j*32 + (r/4)*8 + g*4 + r%4].
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int64_t m = m0 + i * 32 + l32;
-    if (m >= M) continue;
+  for (int j = 0; j < kTN; ++j)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t n = n0 + wn0 + q * 8 + g * 4;
-      TO* dst = out + m * N + n;
-      if (ALIGNED && n + 3 < N) {
-        if constexpr (sizeof(TO) == 2) {
-          bf16x4 v = {(bf16)acc[0][i][q * 4 + 0], (bf16)acc[0][i][q * 4 + 1], (bf16)acc[0][i][q * 4 + 2],
-                      (bf16)acc[0][i][q * 4 + 3]};
-          *reinterpret_cast<bf16x4*>(dst) = v;
+    for (int i = 0; i < kTM; ++i) {
+      const int64_t m = m0 + wm0 + i * 32 + l32;
+      if (m >= M) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t n = n0 + wn0 + j * 32 + q * 8 + g * 4;
+        TO* dst = out + m * N + n;
+        if (ALIGNED && n + 3 < N) {
+          if constexpr (sizeof(TO) == 2) {
+            bf16x4 v = {(bf16)acc[j][i][q * 4 + 0], (bf16)acc[j][i][q * 4 + 1], (bf16)acc[j][i][q * 4 + 2],
+                        (bf16)acc[j][i][q * 4 + 3]};
+            *reinterpret_cast<bf16x4*>(dst) = v;
+          } else {
+            *reinterpret_cast<f32x4*>(dst) =
+                f32x4{acc[j][i][q * 4 + 0], acc[j][i][q * 4 + 1], acc[j][i][q * 4 + 2], acc[j][i][q * 4 + 3]};
+          }
         } else {
-          *reinterpret_cast<f32x4*>(dst) =
-              f32x4{acc[0][i][q * 4 + 0], acc[0][i][q * 4 + 1], acc[0][i][q * 4 + 2], acc[0][i][q * 4 + 3]};
-        }
-      } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (n + e < N) dst[e] = Elem<TO>::from_f32(acc[0][i][q * 4 + e]);
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) dst[e] = Elem<TO>::from_f32(acc[j][i][q * 4 + e]);
+        }
       }
     }
-  }
 }
 
 // ===========================================================================
@@ -916,11 +934,11 @@ int64_t f32_workspace(int64_t M, int64_t N, int64_t K, int64_t cus) {
   return sp.g > 1 ? (int64_t)sp.g * M * N * (int64_t)sizeof(float) : 0;
 }
 
-template <typename TO, int S>
+template <typename TO, int S, int BMN = 64>
 void launch_gemm_f32_slices(const float* x, const float* y, TO* out, int64_t M, int64_t N, int64_t K, int groups,
                             hipStream_t stream) {
-  typedef Gemm<float, TO, 64, 64, 32, 1, 2, true> G;
-  const int64_t tiles_n = cdiv(N, (int64_t)64), tiles = cdiv(M, (int64_t)64) * tiles_n;
+  typedef Gemm<float, TO, BMN, BMN, 32, BMN / 64, 2, true> G;
+  const int64_t tiles_n = cdiv(N, (int64_t)BMN), tiles = cdiv(M, (int64_t)BMN) * tiles_n;
   const size_t lds = (size_t)S * 2 * G::kStageBytes;
   static_assert((S - 1) * 32 * 128 * 4 <= S * 2 * G::kStageBytes, "the slices' accumulators fit the stages");
   const int64_t kslice = cdiv(cdiv(K, (int64_t)S * groups), (int64_t)64) * 64;
@@ -928,13 +946,26 @@ void launch_gemm_f32_slices(const float* x, const float* y, TO* out, int64_t M, 
   const bool aligned = K % 4 == 0 && N % 4 == 0 && a16(x) && a16(y) && a16(out);
   auto go = [&](auto kern) {
     (void)allow_lds((const void*)kern, (int)lds, stream, "ferrite_matmul");  // a failure resurfaces as the launch's error
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)groups), dim3(128 * S), lds, stream, x, y, out, M, N, K,
-                       (int)tiles_n, kslice);
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)groups), dim3(G::kThreads * S), lds, stream, x, y, out, M,
+                       N, K, (int)tiles_n, kslice);
   };
   if (aligned)
-    go(gemm_f32_slices_kernel<TO, S, true>);
+    go(gemm_f32_slices_kernel<TO, S, true, BMN>);
   else
-    go(gemm_f32_slices_kernel<TO, S, false>);
+    go(gemm_f32_slices_kernel<TO, S, false, BMN>);
+}
+
+// f32 products with at least a CU's worth of 128 x 128 tiles: the pipelined loop on those
+// tiles (four waves, no K split), while its lane offsets (128 x rows of K floats, 32 y rows
+// of N) stay under 2^31 bytes; else the register-staged 128 x 128 kernel.
+template <typename TO>
+int launch_gemm_f32_big(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  if (128 * K * 4 < 0x7ffffff0 && 32 * N * 4 < 0x7ffffff0) {
+    launch_gemm_f32_slices<TO, 1, 128>(static_cast<const float*>(x), static_cast<const float*>(y), static_cast<TO*>(out),
+                                       M, N, K, 1, stream);
+    return check_launch("ferrite_matmul");
+  }
+  return launch_gemm<float, TO, 128, 128, 32, 2, 2>(x, y, out, M, N, K, stream);
 }
 
 template <typename TO, int S>
@@ -1129,8 +1160,8 @@ extern "C" int ferrite_hip_matmul_ex(const void* x, const void* y, void* out, in
     if (out_dtype == FERRITE_BF16) return launch_gemm_f32_small<bf16>(x, y, out, m, n, k, workspace, workspace_bytes, s);
     return launch_gemm_f32_small<float>(x, y, out, m, n, k, workspace, workspace_bytes, s);
   }
-  if (out_dtype == FERRITE_BF16) return launch_gemm<float, bf16, 128, 128, 32, 2, 2>(x, y, out, m, n, k, s);
-  return launch_gemm<float, float, 128, 128, 32, 2, 2>(x, y, out, m, n, k, s);
+  if (out_dtype == FERRITE_BF16) return launch_gemm_f32_big<bf16>(x, y, out, m, n, k, s);
+  return launch_gemm_f32_big<float>(x, y, out, m, n, k, s);
 }
 
 extern "C" int ferrite_hip_matmul_gelu(const void* x, const void* y, void* out, void* aux, int64_t m, int64_t n,

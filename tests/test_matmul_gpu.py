@@ -152,6 +152,37 @@ def test_f32_small_products_split_k(dev, m, k, n):
             assert np.all(np.abs(got - exact) <= bf16_ulp(exact) + 1e-5 * np.max(np.abs(exact)))
 
 
+@pytest.mark.parametrize("m,k,n", [
+    (2048, 1000, 2048),  # 256 tiles of 128 x 128: the pipelined loop on the large tiles, 16-byte rows
+    (2100, 1003, 2050),  # the same with 4-byte loads (K and N not multiples of 4), ragged tiles
+    (2048, 64, 2176),    # one pass of the loop (two k-steps)
+])
+def test_f32_large_products_pipelined(dev, m, k, n):
+    """f32 products with a CU's worth of 128 x 128 tiles run the pipelined loop on those tiles:
+    every element written (NaN-prefilled), within 1e-5 of the f64 product relative to its largest
+    magnitude (bf16 output: one bf16 ulp more), and two runs bitwise equal."""
+    x, y = uniform(41, (m, k), "f32"), uniform(42, (k, n), "f32")
+    xt, yt = to_dev(x, "f32", dev), to_dev(y, "f32", dev)
+    exact = x.astype(np.float64) @ y.astype(np.float64)
+    lib = _hip.lib()
+    assert lib.ferrite_hip_matmul_workspace(m, n, k, _hip.F32) == 0
+    for out_code, tdt in ((_hip.F32, torch.float32), (_hip.BF16, torch.bfloat16)):
+        outs = []
+        for _ in range(2):
+            o = torch.full((m, n), float("nan"), dtype=tdt, device=dev)
+            _hip.check(lib.ferrite_hip_matmul_ex(xt.data_ptr(), yt.data_ptr(), o.data_ptr(), m, n, k, 0, 0, _hip.F32,
+                                                 out_code, None, 0, _hip.stream_of(xt)), "matmul")
+            torch.cuda.synchronize()
+            outs.append(o.clone())
+        got = to_np(outs[0]).astype(np.float64)
+        assert not np.isnan(got).any()
+        assert torch.equal(outs[0], outs[1])
+        if tdt == torch.float32:
+            assert np.max(np.abs(got - exact)) <= 1e-5 * np.max(np.abs(exact))
+        else:
+            assert np.all(np.abs(got - exact) <= bf16_ulp(exact) + 1e-5 * np.max(np.abs(exact)))
+
+
 @pytest.mark.parametrize("m,k,n", [(300, 128, 264), (257, 192, 520), (1000, 512, 776), (64, 64, 8)])
 def test_bf16_dma_path_tails(dev, m, k, n):
     """bf16 inputs with K a multiple of 64 and N a multiple of 8 take the DMA-fed kernel, whose
