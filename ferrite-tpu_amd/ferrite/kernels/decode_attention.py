@@ -4,7 +4,8 @@ Reference: src/ferrite/serving/engine.py:89-104 (_cache_attention, _write_cache)
 which the reference leaves to XLA; a decode-attention kernel is its own named
 next step. One call (csrc/decode.hip: ferrite_hip_decode_attention) writes the
 new key/value rows into the cache at each sequence's position and attends the
-query over keys 0..pos, split over 256- or 1024-key chunks merged in f32.
+query over keys 0..pos, split over key chunks (a power of two from 256 keys up,
+as few as keep the grid within 512 workgroups) merged in f32.
 """
 
 from __future__ import annotations

@@ -214,10 +214,11 @@ int ferrite_hip_matmul_gelu(const void* x, const void* y, void* out, void* aux, 
  * `dtype`; pos: device int32 [B]. Writes k_new/v_new into the caches at row
  * pos[b], then out[b, h] = softmax_j(scale * q . k_j) . v_j over j = 0..pos[b]
  * (f32 statistics). A pos outside [0, max_len) writes nothing and gives NaN.
- * D in {64, 128, 256}; all pointers 16-byte aligned. With max_len > 256 the
- * keys are split over workgroups and `workspace` (device memory of
- * ferrite_hip_decode_attention_workspace(b, h, max_len, d) bytes) holds the
- * f32 partials.
+ * D in {64, 128, 256}; all pointers 16-byte aligned. Where the keys are split
+ * over workgroups (chunks of a power of two from 256 keys up, as few as keep
+ * the grid within 512 workgroups), `workspace` (device memory of
+ * ferrite_hip_decode_attention_workspace(b, h, max_len, d) bytes; 0 when a
+ * head's keys fit one chunk) holds the f32 partials.
  */
 int64_t ferrite_hip_decode_attention_workspace(int64_t b, int64_t h, int64_t max_len, int64_t d);
 int ferrite_hip_decode_attention(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,

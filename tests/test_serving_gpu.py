@@ -37,9 +37,15 @@ def _case(dev, b, h, L, d, dtype, seed):
     (1, 2, 256, 128, torch.float32, [100]),       # one chunk: direct output
     (2, 1, 300, 256, torch.bfloat16, [257, 299]),
     (4, 12, 2048, 64, torch.float32, [2047, 1024, 3, 1500]),
-    # grids of >= 512 workgroups at 1024 keys a chunk take the 1024-key chunks
+    # 128 heads: 1024-key chunks (the grid within 512 workgroups)
     (4, 32, 4096, 128, torch.bfloat16, [4095, 1023, 1024, 2500]),
     (2, 64, 4096, 64, torch.float32, [0, 4095]),
+    # 128 heads over 16384 keys: four 4096-key chunks; positions at chunk and
+    # row-step edges (a step of loads covers 32 rows at D = 64)
+    (2, 64, 16384, 64, torch.bfloat16, [16383, 4096]),
+    (2, 64, 16384, 64, torch.bfloat16, [4095, 8223]),
+    # 640 heads: one 1024-key chunk holds all 1000 keys (direct output)
+    (4, 160, 1000, 64, torch.float32, [999, 0, 500, 31]),
 ])
 def test_decode_attention_matches_reference(dev, b, h, L, d, dtype, pos):
     q, kn, vn, kc, vc = _case(dev, b, h, L, d, dtype, sum(pos) + L)
