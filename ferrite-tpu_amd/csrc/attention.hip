@@ -4236,7 +4236,14 @@ int dq_pp_launch(const void* q, const void* k, const void* v, const void* dout, 
     return one_round ? dq_pp_launch_t<D, 8, 2, true, 2>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw)
                      : dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
   } else if constexpr (D == 128) {
-    return dq_pp_launch_t<D, 8, 3, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
+    // 4-wave 128-query workgroups over a two-slot K/V ring (64 KB of LDS):
+    // two share a CU, so one's prologue (Q, dO and O loads, the first tiles)
+    // and its dQ store overlap the other's sweep. Against 8-wave 256-query
+    // workgroups over three slots, one per CU (MI355X, one process, outputs
+    // bitwise equal): 4x16x2048x128 113 -> 106 us, 2x8x4096x128 143 -> 117,
+    // 16x16x512x128 58 -> 52, 8x12x1024x128 56.8 -> 54.6; 1x16x8192x128
+    // 362 -> 368.
+    return dq_pp_launch_t<D, 4, 2, false>(q, k, v, dout, lse, delta, dq, s, causal, scale, stream, o, vw);
   } else {
     // D = 256: the Q and dO fragments of 32 rows (128 VGPRs) and a dQ
     // accumulator of 256 columns (128) take one SIMD's registers for one wave:

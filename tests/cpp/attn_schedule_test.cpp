@@ -7,7 +7,7 @@
 //   attn_fwd_sw_kernel   the forward (D = 128: 8 waves of 32 rows; D <= 64: 8
 //                        waves, pairs splitting every key tile; the split
 //                        long-context grid)
-//   attn_dq_pp_kernel    dQ (D = 128: 8 waves, 3 slots; D = 64: 4 waves and 2
+//   attn_dq_pp_kernel    dQ (D = 128: 4 waves, 2 slots; D = 64: 4 waves and 2
 //                        slots, or 8 waves splitting every key tile on a
 //                        resident grid; the split long-context grid)
 //   attn_dkv_sw_kernel   dK/dV at D = 64 (4 waves, 4 slots, half-steps; the
@@ -637,8 +637,9 @@ int main() {
       const bool zig = resident((long long)nq64 * bh, 2, kCus);
       check_fwd(FwdCfg{64, 8, 2, zig, false}, bh, S);
       if (fwd_split_applies(bh, S, kCus)) check_fwd(FwdCfg{64, 8, 2, true, true}, bh, S);
-      // dQ (dq_pp_launch): D = 128 8 waves 3 slots; D = 64 resident: 8 waves, key split, zig; else 4 waves.
-      check_dq(DqCfg{128, 8, 3, 1, false, false}, bh, S);
+      // dQ (dq_pp_launch): D = 128 4 waves 2 slots; D = 64 resident: 8 waves, key split, zig; else 4 waves.
+      check_dq(DqCfg{128, 4, 2, 1, false, false}, bh, S);
+      check_dq(DqCfg{128, 8, 3, 1, false, false}, bh, S);  // the three-slot ring the kernel still supports
       check_dq(DqCfg{256, 4, 2, 1, false, false}, bh, S);  // D = 256: four waves, two slots
       if (resident((long long)((S + 127) / 128) * bh, 2, kCus))
         check_dq(DqCfg{64, 8, 2, 2, true, false}, bh, S);
