@@ -30,9 +30,10 @@ constexpr int kUnroll = 4;        // row steps whose loads are issued together
 // that each wave streams one long contiguous stretch of the cache with kUnroll
 // row steps of non-temporal loads in flight. Measured on MI355X against the
 // previous fixed choice (1024-key chunks for grids of >= 512 such workgroups,
-// else 256; two row steps per batch of loads): 8x32x8192x128 bf16 186.7 ->
-// 162.4 us (4096-key chunks, 6.6 TB/s), 32x32x2048x128 bf16 190.9 -> 160.2
-// us, 8x16x8192x128 f32 168.8 -> 155.3 us, 1x32x8192x128 bf16 28.6 -> 20 us.
+// else 256; two row steps per batch of loads), one of the B sequences at a
+// third of the cache: 8x32x8192x128 bf16 186.7 -> 162.4 us (4096-key chunks),
+// 32x32x2048x128 bf16 190.9 -> 160.2 us, 8x16x8192x128 f32 168.8 -> 155.3 us,
+// 1x32x8192x128 bf16 28.6 -> 20 us.
 constexpr int kChunkMin = 256;
 constexpr int64_t kGridTarget = 512;
 
